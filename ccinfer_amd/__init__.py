@@ -1,0 +1,23 @@
+"""MI355X (gfx950) paged-attention hot path of ccInfer: HIP kernels behind a C ABI.
+
+The product is libccinfer_attn.so (built in-tree by ccinfer_amd.build). This package is the
+Python host side: a ctypes binding of the C ABI (`_lib`), torch-facing operators that mirror
+the reference's backend ops (`ops`), and seeded synthetic workloads (`workloads`).
+"""
+from .ops import (  # noqa: F401
+    CcinferError,
+    decode_attention,
+    decode_workspace_size,
+    prefill_attention,
+    prefill_workspace_size,
+    write_kv_cache,
+)
+
+__all__ = [
+    "CcinferError",
+    "decode_attention",
+    "decode_workspace_size",
+    "prefill_attention",
+    "prefill_workspace_size",
+    "write_kv_cache",
+]

@@ -1,0 +1,78 @@
+// Device-side helpers shared by the paged-attention kernels (gfx950 / CDNA4 only).
+//
+// KV cache layout (kept identical to the reference so callers need no change):
+//   k_cache, v_cache : [num_slots][num_kv_heads][head_dim] bf16, one buffer per layer,
+//   slot = physical_block * cache_block_size + offset_in_block
+//   (reference: src/cache/kv_cache_storage.cpp:75-136, src/kernel/attention/attn_common.cuh:7-27).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace ccinfer::hipk {
+
+using bf16x8 = __bf16 __attribute__((ext_vector_type(8)));
+using f32x4 = float __attribute__((ext_vector_type(4)));
+using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
+using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInf = -__builtin_inff();
+
+// Token-to-cache-row mapping of the reference (attn_common.cuh:7-27): returns the
+// element offset of (ctx_pos, kv_head) or -1 when the logical block is outside the
+// table row or the table entry is negative.
+__device__ __forceinline__ int64_t kv_row_offset(int ctx_pos, int kv_head, int head_dim,
+                                                 int num_kv_heads, int block_size,
+                                                 int max_blocks_per_req,
+                                                 const int32_t* __restrict__ req_blocks) {
+    const int lb = ctx_pos / block_size;
+    const int off = ctx_pos - lb * block_size;
+    if (lb < 0 || lb >= max_blocks_per_req) return -1;
+    const int pb = req_blocks[lb];
+    if (pb < 0) return -1;
+    const int64_t slot = static_cast<int64_t>(pb) * block_size + off;
+    return (slot * num_kv_heads + kv_head) * static_cast<int64_t>(head_dim);
+}
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Round-to-nearest-even fp32 -> bf16 pair (gfx950 has a native packed convert).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    using bf16x2 = __bf16 __attribute__((ext_vector_type(2)));
+    bf16x2 v;
+    v[0] = static_cast<__bf16>(lo);
+    v[1] = static_cast<__bf16>(hi);
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+// Select the 16-bit half `half` of a and b and pack {a.half, b.half}.
+__device__ __forceinline__ uint32_t pick_halves(uint32_t a, uint32_t b, int half) {
+    // v_perm_b32: bytes 0-3 of the selector index src1 (a), 4-7 index src0 (b).
+    return __builtin_amdgcn_perm(b, a, half ? 0x07060302u : 0x05040100u);
+}
+
+__device__ __forceinline__ float wave_max_xor16_32(float v) {
+    v = fmaxf(v, __shfl_xor(v, 16));
+    v = fmaxf(v, __shfl_xor(v, 32));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum_xor16_32(float v) {
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    return v;
+}
+
+__device__ __forceinline__ f32x4 mfma16x16x32(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ u32x4 load16(const void* p) {
+    return *reinterpret_cast<const u32x4*>(p);
+}
+
+}  // namespace ccinfer::hipk

@@ -1,0 +1,201 @@
+// C ABI of the paged-attention hot path: argument validation, shape dispatch and
+// error-code mapping. Declarations and contracts: include/ccinfer_attn.h.
+//
+// Validation mirrors the reference's two layers:
+//   - DeviceBackend::{write_kv_cache, decode_attention, prefill_attention}
+//     (src/backend/backend.h:172-223): null pointers, non-positive sizes, Hq % Hkv != 0
+//     -> InvalidArgument;
+//   - the launchers: decode requires cache_block_size == 16 and a supported head_dim
+//     (src/kernel/attention/decode_attn.cu:488, :521-569), prefill requires
+//     head_dim <= 256 (src/kernel/attention/prefill_attn.cu:257-259).
+// Device errors map as in src/backend/cuda/cuda_utils.h:13-36.
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cstdint>
+
+#include "ccinfer_attn.h"
+#include "kernels.hpp"
+
+namespace {
+
+using namespace ccinfer::hipk;
+
+int map_hip_error(hipError_t err) {
+    switch (err) {
+        case hipSuccess:
+            return CCINFER_OK;
+        case hipErrorOutOfMemory:
+            return CCINFER_ERR_DEVICE_OUT_OF_MEMORY;
+        case hipErrorInvalidValue:
+        case hipErrorInvalidDevice:
+        case hipErrorInvalidDevicePointer:
+        case hipErrorInvalidConfiguration:
+            return CCINFER_ERR_DEVICE_INVALID_VALUE;
+        case hipErrorLaunchFailure:
+        case hipErrorLaunchOutOfResources:
+        case hipErrorIllegalAddress:
+            return CCINFER_ERR_LAUNCH_FAILED;
+        default:
+            return CCINFER_ERR_DEVICE_RUNTIME;
+    }
+}
+
+bool decode_head_dim_ok(int d) {
+    switch (d) {
+        case 32: case 64: case 80: case 96: case 112: case 120: case 128: case 192: case 256:
+            return true;
+        default:
+            return false;
+    }
+}
+
+bool fits_int(int64_t v) { return v >= 0 && v <= INT_MAX; }
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+bool decode_shape_ok(int batch_size, int max_blocks_per_req, int num_q_heads, int num_kv_heads,
+                     int head_dim, int cache_block_size) {
+    if (batch_size <= 0 || max_blocks_per_req <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 ||
+        head_dim <= 0 || cache_block_size <= 0)
+        return false;
+    if (num_q_heads % num_kv_heads != 0) return false;
+    if (cache_block_size != 16 || !decode_head_dim_ok(head_dim)) return false;
+    return fits_int(static_cast<int64_t>(max_blocks_per_req) * cache_block_size) &&
+           fits_int(static_cast<int64_t>(batch_size) * num_q_heads);
+}
+
+bool prefill_shape_ok(int batch_size, int total_query_tokens, int max_blocks_per_req,
+                      int num_q_heads, int num_kv_heads, int head_dim, int cache_block_size) {
+    if (batch_size <= 0 || total_query_tokens <= 0 || max_blocks_per_req <= 0 ||
+        num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || cache_block_size <= 0)
+        return false;
+    if (num_q_heads % num_kv_heads != 0 || head_dim > 256) return false;
+    return fits_int(static_cast<int64_t>(max_blocks_per_req) * cache_block_size) &&
+           fits_int(static_cast<int64_t>(total_query_tokens) * num_q_heads);
+}
+
+bool prefill_uses_fast(int batch_size, int num_q_heads, int num_kv_heads, int head_dim,
+                       int cache_block_size) {
+    return cache_block_size == 16 && batch_size <= 4096 &&
+           prefill_fast_supported(num_q_heads, num_kv_heads, head_dim) &&
+           decode_fast_supported(num_q_heads, num_kv_heads, head_dim, cache_block_size);
+}
+
+}  // namespace
+
+extern "C" {
+
+int ccinfer_write_kv_cache(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                           const int32_t* slot_mapping, int total_tokens, int n_kv_heads,
+                           int head_dim, int max_slots, void* stream) {
+    if (!k_new || !v_new || !k_cache || !v_cache || !slot_mapping)
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    if (total_tokens <= 0 || n_kv_heads <= 0 || head_dim <= 0 || max_slots <= 0)
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    if (!fits_int(static_cast<int64_t>(n_kv_heads) * head_dim * 2))
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    return map_hip_error(write_kv_cache(k_new, v_new, k_cache, v_cache, slot_mapping,
+                                        total_tokens, n_kv_heads, head_dim, max_slots,
+                                        as_stream(stream)));
+}
+
+size_t ccinfer_decode_workspace_size(int batch_size, int max_blocks_per_req, int num_q_heads,
+                                     int num_kv_heads, int head_dim, int cache_block_size) {
+    if (!decode_shape_ok(batch_size, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
+                         cache_block_size))
+        return 0;
+    if (!decode_fast_supported(num_q_heads, num_kv_heads, head_dim, cache_block_size)) return 0;
+    const DecodePlan plan =
+        plan_decode(batch_size, num_kv_heads, max_blocks_per_req * cache_block_size);
+    return decode_workspace_bytes(batch_size, num_q_heads, head_dim, plan);
+}
+
+int ccinfer_decode_attention(const void* q, const void* k_cache, const void* v_cache,
+                             const int32_t* block_table, const int32_t* context_lens,
+                             void* output, int batch_size, int max_blocks_per_req,
+                             int num_q_heads, int num_kv_heads, int head_dim,
+                             int cache_block_size, void* workspace, size_t workspace_bytes,
+                             void* stream) {
+    if (!q || !k_cache || !v_cache || !block_table || !context_lens || !output)
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    if (!decode_shape_ok(batch_size, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
+                         cache_block_size))
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    if (!decode_fast_supported(num_q_heads, num_kv_heads, head_dim, cache_block_size)) {
+        return map_hip_error(generic_decode_attention(
+            q, k_cache, v_cache, block_table, context_lens, output, batch_size,
+            max_blocks_per_req, num_q_heads, num_kv_heads, head_dim, cache_block_size,
+            as_stream(stream)));
+    }
+    const DecodePlan plan =
+        plan_decode(batch_size, num_kv_heads, max_blocks_per_req * cache_block_size);
+    const size_t need = decode_workspace_bytes(batch_size, num_q_heads, head_dim, plan);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    DecodeItems items;
+    items.num_items = batch_size;
+    return map_hip_error(decode_attention(q, k_cache, v_cache, block_table, context_lens, output,
+                                          items, max_blocks_per_req, num_q_heads, num_kv_heads,
+                                          head_dim, cache_block_size, plan, workspace,
+                                          as_stream(stream)));
+}
+
+size_t ccinfer_prefill_workspace_size(int batch_size, int total_query_tokens,
+                                      int max_blocks_per_req, int num_q_heads,
+                                      int num_kv_heads, int head_dim, int cache_block_size) {
+    if (!prefill_shape_ok(batch_size, total_query_tokens, max_blocks_per_req, num_q_heads,
+                          num_kv_heads, head_dim, cache_block_size))
+        return 0;
+    if (!prefill_uses_fast(batch_size, num_q_heads, num_kv_heads, head_dim, cache_block_size))
+        return 0;
+    return prefill_workspace_bytes(batch_size, total_query_tokens, max_blocks_per_req,
+                                   num_q_heads, num_kv_heads, head_dim, cache_block_size);
+}
+
+int ccinfer_prefill_attention(const void* q, const void* k_cache, const void* v_cache,
+                              const int32_t* block_table, const int32_t* query_start_loc,
+                              const int32_t* context_lens, void* output, int batch_size,
+                              int total_query_tokens, int max_blocks_per_req, int num_q_heads,
+                              int num_kv_heads, int head_dim, int cache_block_size,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+    if (!q || !k_cache || !v_cache || !block_table || !query_start_loc || !context_lens ||
+        !output)
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    if (!prefill_shape_ok(batch_size, total_query_tokens, max_blocks_per_req, num_q_heads,
+                          num_kv_heads, head_dim, cache_block_size))
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    if (!prefill_uses_fast(batch_size, num_q_heads, num_kv_heads, head_dim, cache_block_size)) {
+        return map_hip_error(generic_prefill_attention(
+            q, k_cache, v_cache, block_table, query_start_loc, context_lens, output, batch_size,
+            total_query_tokens, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
+            cache_block_size, as_stream(stream)));
+    }
+    const size_t need =
+        prefill_workspace_bytes(batch_size, total_query_tokens, max_blocks_per_req,
+                                num_q_heads, num_kv_heads, head_dim, cache_block_size);
+    if (workspace == nullptr || workspace_bytes < need) return CCINFER_ERR_INVALID_ARGUMENT;
+    return map_hip_error(prefill_attention(q, k_cache, v_cache, block_table, query_start_loc,
+                                           context_lens, output, batch_size, total_query_tokens,
+                                           max_blocks_per_req, num_q_heads, num_kv_heads,
+                                           head_dim, cache_block_size, workspace,
+                                           as_stream(stream)));
+}
+
+const char* ccinfer_error_message(int code) {
+    switch (code) {
+        case CCINFER_OK: return "ok";
+        case CCINFER_ERR_DEVICE_OUT_OF_MEMORY: return "device out of memory";
+        case CCINFER_ERR_LAUNCH_FAILED: return "kernel launch failed";
+        case CCINFER_ERR_DEVICE_INVALID_VALUE: return "device invalid value";
+        case CCINFER_ERR_DEVICE_RUNTIME: return "device runtime error";
+        case CCINFER_ERR_INVALID_ARGUMENT: return "invalid argument";
+        case CCINFER_ERR_UNSUPPORTED: return "unsupported operation";
+        case CCINFER_ERR_INTERNAL: return "internal error";
+        default: return "unknown error";
+    }
+}
+
+const char* ccinfer_version(void) { return "0.1.0"; }
+
+}  // extern "C"

@@ -1,0 +1,57 @@
+// HipBackend: the MI355X implementation of the hot-path backend ops (the reference's
+// CudaBackend::{prefill,decode}_attention_impl / write_kv_cache_impl,
+// src/backend/cuda/cuda_backend.cpp:162-187). It owns one HIP stream (default priority)
+// and one device workspace for the split-KV partials and the prefill work list; the
+// workspace grows on demand and is reused across calls.
+#pragma once
+
+#include <hip/hip_bf16.h>
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <memory>
+
+#include "backend/backend.h"
+
+namespace ccinfer {
+
+class HipBackend : public DeviceBackend<HipBackend> {
+public:
+    // Creates a backend bound to `device_id` with its own stream.
+    static Result<std::unique_ptr<HipBackend>> create(int device_id);
+    ~HipBackend();
+    HipBackend(const HipBackend&) = delete;
+    HipBackend& operator=(const HipBackend&) = delete;
+
+    hipStream_t stream() const { return stream_; }
+    int device_id() const { return device_id_; }
+    Result<void> synchronize();
+
+    template <typename DType>
+    Result<void> prefill_attention_impl(const PrefillAttnParams& p);
+    template <typename DType>
+    Result<void> decode_attention_impl(const DecodeAttnParams& p);
+    template <typename DType>
+    Result<void> write_kv_cache_impl(const WriteKVCacheParams& p);
+
+private:
+    HipBackend() = default;
+    Result<void*> workspace(size_t bytes);
+
+    int device_id_ = 0;
+    hipStream_t stream_ = nullptr;
+    void* workspace_ = nullptr;
+    size_t workspace_bytes_ = 0;
+};
+
+template <>
+Result<void> HipBackend::prefill_attention_impl<__hip_bfloat16>(const PrefillAttnParams& p);
+template <>
+Result<void> HipBackend::decode_attention_impl<__hip_bfloat16>(const DecodeAttnParams& p);
+template <>
+Result<void> HipBackend::write_kv_cache_impl<__hip_bfloat16>(const WriteKVCacheParams& p);
+
+// The reference's DefaultBackend alias (src/backend/default_backend.h).
+using DefaultBackend = HipBackend;
+
+}  // namespace ccinfer

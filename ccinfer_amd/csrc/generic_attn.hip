@@ -1,0 +1,159 @@
+// Generic paged attention (any head_dim <= 256, any GQA ratio, any cache block size).
+//
+// Coverage path for the shapes the MFMA kernels do not specialise (head_dim 32/80/96/
+// 112/120/192, GQA groups above 16, non-16 cache blocks for prefill). Same semantics as the
+// reference launchers (decode_attn.cu:364-473, prefill_attn.cu:43-242): one wavefront per
+// (query row, q_head); 64 positions per step, one per lane, scores reduced with
+// cross-lane max/sum; each lane accumulates up to 4 output dims over the step's positions
+// with an online softmax. Scalar fp32, not tuned.
+#include "attn_common.hpp"
+#include "kernels.hpp"
+
+namespace ccinfer::hipk {
+namespace {
+
+constexpr int kMaxDims = 256;
+constexpr int kDimsPerLane = kMaxDims / kWave;
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+// Attends q_vec over positions [0, visible) of one block-table row. Writes bf16 output.
+__device__ void attend_row(const __bf16* __restrict__ q_vec, const __bf16* __restrict__ k_cache,
+                           const __bf16* __restrict__ v_cache,
+                           const int32_t* __restrict__ req_blocks, int visible, int kv_head,
+                           int head_dim, int hkv, int block_size, int mbpr, float scale_log2,
+                           float eps, __bf16* __restrict__ out_vec) {
+    const int lane = threadIdx.x & 63;
+    float m = kNegInf, l = 0.f;
+    float acc[kDimsPerLane];
+#pragma unroll
+    for (int x = 0; x < kDimsPerLane; ++x) acc[x] = 0.f;
+    for (int base = 0; base < visible; base += kWave) {
+        const int pos = base + lane;
+        int64_t off = -1;
+        float s = kNegInf;
+        if (pos < visible) {
+            off = kv_row_offset(pos, kv_head, head_dim, hkv, block_size, mbpr, req_blocks);
+            if (off >= 0) {
+                float dot = 0.f;
+                for (int d = 0; d < head_dim; ++d)
+                    dot += static_cast<float>(q_vec[d]) * static_cast<float>(k_cache[off + d]);
+                s = dot * scale_log2;
+            }
+        }
+        const float m_new = fmaxf(m, wave_max(s));
+        const float m_use = m_new == kNegInf ? 0.f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m - m_use);
+        const float p = off >= 0 ? __builtin_amdgcn_exp2f(s - m_use) : 0.f;
+        l = l * alpha + wave_sum(p);
+        m = m_new;
+#pragma unroll
+        for (int x = 0; x < kDimsPerLane; ++x) acc[x] *= alpha;
+        const int n = min(kWave, visible - base);
+        for (int t = 0; t < n; ++t) {
+            const float pt = __shfl(p, t);
+            const int64_t ot = __shfl(off, t);
+            if (ot < 0) continue;
+#pragma unroll
+            for (int x = 0; x < kDimsPerLane; ++x) {
+                const int d = lane + x * kWave;
+                if (d < head_dim) acc[x] += pt * static_cast<float>(v_cache[ot + d]);
+            }
+        }
+    }
+    const float inv = l > 0.f ? 1.f / (l + eps) : 0.f;
+#pragma unroll
+    for (int x = 0; x < kDimsPerLane; ++x) {
+        const int d = lane + x * kWave;
+        if (d < head_dim) out_vec[d] = static_cast<__bf16>(acc[x] * inv);
+    }
+}
+
+__global__ __launch_bounds__(64) void generic_decode_kernel(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ k_cache,
+    const __bf16* __restrict__ v_cache, const int32_t* __restrict__ block_table,
+    const int32_t* __restrict__ context_lens, __bf16* __restrict__ out, int mbpr, int hq,
+    int hkv, int head_dim, int block_size, float scale_log2) {
+    const int b = blockIdx.x / hq;
+    const int qh = blockIdx.x % hq;
+    __bf16* o = out + (static_cast<int64_t>(b) * hq + qh) * head_dim;
+    const int ctx = context_lens[b];
+    if (ctx <= 0 || (ctx + block_size - 1) / block_size > mbpr) {
+        for (int d = threadIdx.x; d < head_dim; d += kWave) o[d] = static_cast<__bf16>(0.f);
+        return;
+    }
+    const int kvh = qh / (hq / hkv);
+    attend_row(q + (static_cast<int64_t>(b) * hq + qh) * head_dim, k_cache, v_cache,
+               block_table + static_cast<int64_t>(b) * mbpr, ctx, kvh, head_dim, hkv,
+               block_size, mbpr, scale_log2, 1e-6f, o);
+}
+
+__global__ __launch_bounds__(64) void generic_prefill_kernel(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ k_cache,
+    const __bf16* __restrict__ v_cache, const int32_t* __restrict__ block_table,
+    const int32_t* __restrict__ qsl, const int32_t* __restrict__ context_lens,
+    __bf16* __restrict__ out, int batch_size, int mbpr, int hq, int hkv, int head_dim,
+    int block_size, float scale_log2) {
+    const int gq = blockIdx.x / hq;
+    const int qh = blockIdx.x % hq;
+    int req = 0;
+    while (req + 1 < batch_size && qsl[req + 1] <= gq) ++req;
+    const int qb = qsl[req];
+    const int qlen = qsl[req + 1] - qb;
+    const int local = gq - qb;
+    if (qlen <= 0 || local < 0 || local >= qlen) return;
+    const int ctx = context_lens[req];
+    const int prefix = ctx - qlen;
+    if (prefix < 0) return;
+    const int visible = prefix + local + 1;
+    const int kvh = qh / (hq / hkv);
+    attend_row(q + (static_cast<int64_t>(gq) * hq + qh) * head_dim, k_cache, v_cache,
+               block_table + static_cast<int64_t>(req) * mbpr, visible, kvh, head_dim, hkv,
+               block_size, mbpr, scale_log2, 0.f,
+               out + (static_cast<int64_t>(gq) * hq + qh) * head_dim);
+}
+
+}  // namespace
+
+hipError_t generic_decode_attention(const void* q, const void* k_cache, const void* v_cache,
+                                    const int32_t* block_table, const int32_t* context_lens,
+                                    void* output, int batch_size, int max_blocks_per_req,
+                                    int num_q_heads, int num_kv_heads, int head_dim,
+                                    int block_size, hipStream_t stream) {
+    const float scale_log2 = kLog2e / sqrtf(static_cast<float>(head_dim));
+    const int64_t grid = static_cast<int64_t>(batch_size) * num_q_heads;
+    generic_decode_kernel<<<static_cast<unsigned>(grid), kWave, 0, stream>>>(
+        static_cast<const __bf16*>(q), static_cast<const __bf16*>(k_cache),
+        static_cast<const __bf16*>(v_cache), block_table, context_lens,
+        static_cast<__bf16*>(output), max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
+        block_size, scale_log2);
+    return hipGetLastError();
+}
+
+hipError_t generic_prefill_attention(const void* q, const void* k_cache, const void* v_cache,
+                                     const int32_t* block_table,
+                                     const int32_t* query_start_loc,
+                                     const int32_t* context_lens, void* output, int batch_size,
+                                     int total_query_tokens, int max_blocks_per_req,
+                                     int num_q_heads, int num_kv_heads, int head_dim,
+                                     int block_size, hipStream_t stream) {
+    const float scale_log2 = kLog2e / sqrtf(static_cast<float>(head_dim));
+    const int64_t grid = static_cast<int64_t>(total_query_tokens) * num_q_heads;
+    generic_prefill_kernel<<<static_cast<unsigned>(grid), kWave, 0, stream>>>(
+        static_cast<const __bf16*>(q), static_cast<const __bf16*>(k_cache),
+        static_cast<const __bf16*>(v_cache), block_table, query_start_loc, context_lens,
+        static_cast<__bf16*>(output), batch_size, max_blocks_per_req, num_q_heads,
+        num_kv_heads, head_dim, block_size, scale_log2);
+    return hipGetLastError();
+}
+
+}  // namespace ccinfer::hipk

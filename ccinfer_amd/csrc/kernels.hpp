@@ -1,0 +1,80 @@
+// Host-side entry points of the HIP kernels, used by the C ABI (capi.cpp).
+// Every function only enqueues work on `stream`; none allocates memory or syncs.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace ccinfer::hipk {
+
+// ---- KV-cache write --------------------------------------------------------
+hipError_t write_kv_cache(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                          const int32_t* slot_mapping, int total_tokens, int n_kv_heads,
+                          int head_dim, int max_slots, hipStream_t stream);
+
+// ---- decode ---------------------------------------------------------------
+// Split-KV plan: `splits` partitions of `split_tokens` tokens per (request, kv_head).
+struct DecodePlan {
+    int splits = 1;
+    int split_tokens = 0;  // multiple of 32
+};
+
+// Returns the plan for a batch whose longest context is max_ctx tokens.
+DecodePlan plan_decode(int num_items, int num_kv_heads, int max_ctx);
+
+// Scratch bytes the split-KV decode needs for `num_items` query rows.
+size_t decode_workspace_bytes(int num_items, int num_q_heads, int head_dim,
+                              const DecodePlan& plan);
+
+// Whether the MFMA split-KV decode kernel supports this shape.
+bool decode_fast_supported(int num_q_heads, int num_kv_heads, int head_dim, int block_size);
+
+// Query rows to attend, described either densely (item i is request i, query row i)
+// or through a device list written by the prefill planner.
+struct DecodeItems {
+    int num_items = 0;                    // upper bound on items (grid size)
+    const int32_t* item_count = nullptr;  // device: actual count (nullptr -> num_items)
+    const int32_t* item_req = nullptr;    // device: request of item i (nullptr -> i)
+    const int32_t* query_start_loc = nullptr;  // device: q row = qsl[req] (nullptr -> req)
+    float denom_eps = 1e-6f;              // decode adds 1e-6 to the softmax sum; prefill 0
+    bool zero_invalid = true;             // decode writes zeros for bad ctx; prefill skips
+};
+
+hipError_t decode_attention(const void* q, const void* k_cache, const void* v_cache,
+                            const int32_t* block_table, const int32_t* context_lens, void* output,
+                            const DecodeItems& items, int max_blocks_per_req, int num_q_heads,
+                            int num_kv_heads, int head_dim, int block_size,
+                            const DecodePlan& plan, void* workspace, hipStream_t stream);
+
+// ---- prefill --------------------------------------------------------------
+bool prefill_fast_supported(int num_q_heads, int num_kv_heads, int head_dim);
+
+size_t prefill_workspace_bytes(int batch_size, int total_query_tokens, int max_blocks_per_req,
+                               int num_q_heads, int num_kv_heads, int head_dim,
+                               int block_size);
+
+hipError_t prefill_attention(const void* q, const void* k_cache, const void* v_cache,
+                             const int32_t* block_table, const int32_t* query_start_loc,
+                             const int32_t* context_lens, void* output, int batch_size,
+                             int total_query_tokens, int max_blocks_per_req, int num_q_heads,
+                             int num_kv_heads, int head_dim, int block_size, void* workspace,
+                             hipStream_t stream);
+
+// ---- generic (any head_dim / GQA ratio / block size) ----------------------
+hipError_t generic_decode_attention(const void* q, const void* k_cache, const void* v_cache,
+                                    const int32_t* block_table, const int32_t* context_lens,
+                                    void* output, int batch_size, int max_blocks_per_req,
+                                    int num_q_heads, int num_kv_heads, int head_dim,
+                                    int block_size, hipStream_t stream);
+
+hipError_t generic_prefill_attention(const void* q, const void* k_cache, const void* v_cache,
+                                     const int32_t* block_table,
+                                     const int32_t* query_start_loc,
+                                     const int32_t* context_lens, void* output, int batch_size,
+                                     int total_query_tokens, int max_blocks_per_req,
+                                     int num_q_heads, int num_kv_heads, int head_dim,
+                                     int block_size, hipStream_t stream);
+
+}  // namespace ccinfer::hipk

@@ -1,0 +1,573 @@
+// Paged causal prefill attention for gfx950 (bf16 MFMA, fp32 accumulation).
+//
+// Semantics follow the reference prefill (src/kernel/attention/prefill_attn.cu:80-241 and
+// the contract in src/backend/params.h:140-146):
+//   request r owns query rows [query_start_loc[r], query_start_loc[r+1]); prefix =
+//   context_lens[r] - qlen; local query i attends to cache positions [0, prefix + i]
+//   through the block table (negative ids / positions past the table are skipped);
+//   rows of requests with prefix < 0 are left unwritten; out = sum(p v) / sum(p) (0 if
+//   nothing is visible).
+//
+// Launch plan (all on the caller's stream, no host sync, no allocation):
+//   1. plan kernel (one workgroup): reads query_start_loc / context_lens, emits the list of
+//      query tiles sorted longest-first (counting sort on the number of visible keys), and
+//      the list of single-token requests (decode items of a mixed batch).
+//   2. tile kernel: one workgroup (4 wavefronts) per (query tile, kv_head, head group).
+//      Each wavefront owns QW = 64 query rows of one q-head (32 for head_dim 256); the
+//      workgroup covers Hq/Hkv heads that share one KV head so every K/V tile staged in LDS
+//      serves all of them. K/V tiles of 64 positions are gathered through the block table
+//      into LDS (double-buffered: the next tile's global loads are in flight while MFMAs run
+//      on the current one). Scores are formed transposed, S^T = K . Q^T, so the softmax'd
+//      probabilities are already in the lane layout of the P^T operand of O^T = V^T . P^T,
+//      and every O accumulator of a lane belongs to one query row (lane-local rescale).
+//      Tiles entirely above the causal diagonal are skipped; masking only runs on the
+//      diagonal / ragged tiles.
+//   3. single-token requests go through the split-KV decode kernel (decode_attn.hip) with
+//      prefill semantics (no 1e-6 in the denominator, bad rows left untouched).
+#include "attn_common.hpp"
+#include "kernels.hpp"
+
+namespace ccinfer::hipk {
+namespace {
+
+constexpr int kKeysPerTile = 64;
+constexpr int kThreads = 256;
+constexpr int kBuckets = 1024;
+constexpr int kMaxPlanRequests = 4096;
+
+template <int D>
+struct PrefillShape {
+    static constexpr int kQT = D <= 128 ? 4 : 2;     // 16-row query tiles per wavefront
+    static constexpr int kQW = 16 * kQT;             // query rows per wavefront
+    static constexpr int kSteps = D / 32;            // QK k-steps
+    static constexpr int kNV = D / 16;               // PV MFMAs per query tile
+    static constexpr int kCPR = D / 8;               // 16-byte chunks per K/V row
+    static constexpr int kSwz = kCPR < 16 ? kCPR - 1 : 15;
+    static constexpr int kLoadsPerThread = kKeysPerTile * kCPR / kThreads;  // per K or V
+};
+
+// Heads per workgroup: 4 wavefronts split as HPW heads x (4/HPW) row groups.
+__host__ __device__ inline int heads_per_wg(int G) {
+    return (G % 4 == 0) ? 4 : ((G % 2 == 0) ? 2 : 1);
+}
+
+struct TileEntry {
+    int req;
+    int t0;
+};
+
+// In-place inclusive prefix sum of a[0..n) (n <= 4 * blockDim.x) by a 1024-thread block.
+// Each thread scans up to 4 consecutive entries, then a Hillis-Steele pass over the
+// per-thread totals adds the carries. Must be called by every thread of the block.
+__device__ void block_inclusive_scan(int* a, int n, int* part) {
+    const int tid = threadIdx.x;
+    const int nt = blockDim.x;
+    const int per = (n + nt - 1) / nt;
+    const int lo = tid * per;
+    const int hi = min(n, lo + per);
+    int run = 0;
+    for (int x = lo; x < hi; ++x) {
+        run += a[x];
+        a[x] = run;
+    }
+    part[tid] = run;
+    __syncthreads();
+    for (int off = 1; off < nt; off <<= 1) {
+        const int v = tid >= off ? part[tid - off] : 0;
+        __syncthreads();
+        part[tid] += v;
+        __syncthreads();
+    }
+    const int carry = tid > 0 ? part[tid - 1] : 0;
+    for (int x = lo; x < hi; ++x) a[x] += carry;
+    __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// Planner: one workgroup of 1024 threads.
+// ws layout: counts[0] = #tiles, counts[1] = #decode items; tiles[max_tiles]; dec[B].
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(1024) void prefill_plan_kernel(
+    const int32_t* __restrict__ qsl, const int32_t* __restrict__ context_lens, int batch_size,
+    int total_tokens, int tile_tokens, int32_t* __restrict__ counts,
+    TileEntry* __restrict__ tiles, int32_t* __restrict__ dec_req) {
+    __shared__ int s_ntiles[kMaxPlanRequests];
+    __shared__ int s_scan[kMaxPlanRequests];
+    __shared__ int s_hist[kBuckets];
+    __shared__ int s_hscan[kBuckets];
+    __shared__ int s_part[1024];
+    __shared__ int s_ndec;
+    __shared__ int s_total;
+    const int tid = threadIdx.x;
+    for (int i = tid; i < kBuckets; i += blockDim.x) s_hist[i] = 0;
+    if (tid == 0) s_ndec = 0;
+    __syncthreads();
+
+    // Per-request tile counts; single-token requests become decode items.
+    for (int b = tid; b < batch_size; b += blockDim.x) {
+        const int qb = qsl[b];
+        const int qe_raw = qsl[b + 1];
+        const int qlen = qe_raw - qb;
+        const int qe = qe_raw < total_tokens ? qe_raw : total_tokens;
+        const int rows = qe - (qb > 0 ? qb : 0);
+        const int prefix = context_lens[b] - qlen;
+        int n = 0;
+        if (qlen > 0 && prefix >= 0 && qb >= 0 && rows > 0) {
+            if (qlen == 1) {
+                const int slot = atomicAdd(&s_ndec, 1);
+                dec_req[slot] = b;
+            } else {
+                n = (rows + tile_tokens - 1) / tile_tokens;
+            }
+        }
+        s_ntiles[b] = n;
+    }
+    __syncthreads();
+    for (int b = tid; b < batch_size; b += blockDim.x) s_scan[b] = s_ntiles[b];
+    __syncthreads();
+    block_inclusive_scan(s_scan, batch_size, s_part);
+    if (tid == 0) s_total = batch_size > 0 ? s_scan[batch_size - 1] : 0;
+    __syncthreads();
+    const int total = s_total;
+    auto locate = [&](int t, int* b_out, int* r_out) {
+        int lo = 0, hi = batch_size - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (s_scan[mid] > t) hi = mid; else lo = mid + 1;
+        }
+        *b_out = lo;
+        *r_out = t - (s_scan[lo] - s_ntiles[lo]);
+    };
+    auto bucket_of = [&](int b, int r) {
+        const int qlen = qsl[b + 1] - qsl[b];
+        const int prefix = context_lens[b] - qlen;
+        int last = (r + 1) * tile_tokens;
+        if (last > qlen) last = qlen;
+        const int cost = (prefix + last) >> 6;
+        return kBuckets - 1 - (cost < kBuckets - 1 ? cost : kBuckets - 1);
+    };
+    for (int t = tid; t < total; t += blockDim.x) {
+        int b, r;
+        locate(t, &b, &r);
+        atomicAdd(&s_hist[bucket_of(b, r)], 1);
+    }
+    __syncthreads();
+    // Exclusive scan of the histogram -> first slot of each bucket.
+    for (int i = tid; i < kBuckets; i += blockDim.x) s_hscan[i] = s_hist[i];
+    __syncthreads();
+    block_inclusive_scan(s_hscan, kBuckets, s_part);
+    for (int i = tid; i < kBuckets; i += blockDim.x) s_hist[i] = s_hscan[i] - s_hist[i];
+    __syncthreads();
+    for (int t = tid; t < total; t += blockDim.x) {
+        int b, r;
+        locate(t, &b, &r);
+        const int pos = atomicAdd(&s_hist[bucket_of(b, r)], 1);
+        tiles[pos] = TileEntry{b, r * tile_tokens};
+    }
+    if (tid == 0) {
+        counts[0] = total;
+        counts[1] = s_ndec;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Tile kernel.
+// ---------------------------------------------------------------------------
+template <int D>
+struct StageRegs {
+    u32x4 k[PrefillShape<D>::kLoadsPerThread];
+    u32x4 v[PrefillShape<D>::kLoadsPerThread];
+    int valid[PrefillShape<D>::kLoadsPerThread];
+};
+
+template <int D>
+__device__ __forceinline__ int lds_off(int row, int chunk) {
+    // Element offset of logical 16-byte chunk `chunk` of key row `row` (XOR swizzle so
+    // 16 lanes reading one chunk column of 16 rows hit distinct banks).
+    return row * D + ((chunk ^ (row & PrefillShape<D>::kSwz)) << 3);
+}
+
+template <int D>
+__device__ __forceinline__ void stage_load(StageRegs<D>& st, const __bf16* __restrict__ k_cache,
+                                           const __bf16* __restrict__ v_cache,
+                                           const int32_t* __restrict__ req_blocks, int key_base,
+                                           int ctx, int mbpr, int block_size, int kv_head,
+                                           int hkv) {
+    constexpr int CPR = PrefillShape<D>::kCPR;
+#pragma unroll
+    for (int x = 0; x < PrefillShape<D>::kLoadsPerThread; ++x) {
+        const int linear = threadIdx.x + kThreads * x;
+        const int row = linear / CPR;
+        const int chunk = linear % CPR;
+        const int key = key_base + row;
+        int64_t base = -1;
+        if (key < ctx) base = kv_row_offset(key, kv_head, D, hkv, block_size, mbpr, req_blocks);
+        st.valid[x] = base >= 0;
+        if (base >= 0) {
+            st.k[x] = load16(k_cache + base + chunk * 8);
+            st.v[x] = load16(v_cache + base + chunk * 8);
+        } else {
+            st.k[x] = u32x4{0, 0, 0, 0};
+            st.v[x] = u32x4{0, 0, 0, 0};
+        }
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void stage_store(const StageRegs<D>& st, __bf16* lk, __bf16* lv,
+                                            uint8_t* lvalid) {
+    constexpr int CPR = PrefillShape<D>::kCPR;
+#pragma unroll
+    for (int x = 0; x < PrefillShape<D>::kLoadsPerThread; ++x) {
+        const int linear = threadIdx.x + kThreads * x;
+        const int row = linear / CPR;
+        const int chunk = linear % CPR;
+        const int off = lds_off<D>(row, chunk);
+        *reinterpret_cast<u32x4*>(lk + off) = st.k[x];
+        *reinterpret_cast<u32x4*>(lv + off) = st.v[x];
+        if (chunk == 0) lvalid[row] = static_cast<uint8_t>(st.valid[x]);
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ k_cache,
+    const __bf16* __restrict__ v_cache, const int32_t* __restrict__ block_table,
+    const int32_t* __restrict__ qsl, const int32_t* __restrict__ context_lens,
+    __bf16* __restrict__ out, const int32_t* __restrict__ counts,
+    const TileEntry* __restrict__ tiles, int total_tokens, int mbpr, int hq, int hkv,
+    int block_size, float scale_log2) {
+    using Sh = PrefillShape<D>;
+    constexpr int QT = Sh::kQT;
+    constexpr int QW = Sh::kQW;
+    constexpr int S = Sh::kSteps;
+    constexpr int NV = Sh::kNV;
+    __shared__ __attribute__((aligned(16))) __bf16 lds_k[2][kKeysPerTile * D];
+    __shared__ __attribute__((aligned(16))) __bf16 lds_v[2][kKeysPerTile * D];
+    __shared__ uint8_t lds_valid[2][kKeysPerTile];
+
+    const int G = hq / hkv;
+    const int HPW = heads_per_wg(G);
+    const int WPH = 4 / HPW;
+    const int U = hkv * (G / HPW);
+    const int tile_idx = blockIdx.x / U;
+    if (tile_idx >= counts[0]) return;
+    const int u = blockIdx.x % U;
+    const int kvh = u / (G / HPW);
+    const int hg = u % (G / HPW);
+    const TileEntry te = tiles[tile_idx];
+    const int req = te.req;
+    const int t0 = te.t0;
+
+    const int qb = qsl[req];
+    const int qlen = qsl[req + 1] - qb;
+    const int ctx = context_lens[req];
+    const int prefix = ctx - qlen;
+    const int qe = min(qb + qlen, total_tokens);
+    const int rows = qe - qb;  // rows of this request that exist in q/out
+    const int TT = WPH * QW;
+    const int kv_end = prefix + min(t0 + TT, rows);
+    const int ntiles = (kv_end + kKeysPerTile - 1) / kKeysPerTile;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int head_local = wave / WPH;
+    const int tw = t0 + (wave % WPH) * QW;  // first local token of this wavefront
+    const int q_head = kvh * G + hg * HPW + head_local;
+    const int j = lane & 15;
+    const int g = lane >> 4;
+    const int i = lane & 15;
+    const int wave_rows = max(0, min(QW, rows - tw));
+    const int wave_max_key = prefix + tw + wave_rows - 1;  // last key any row here sees
+    const int32_t* req_blocks = block_table + static_cast<int64_t>(req) * mbpr;
+
+    // Q^T operands: lane (query j, grp g) holds dims (kk*4+g)*8.. of row tw + qt*16 + j.
+    bf16x8 qop[QT][S];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        const int tq = tw + qt * 16 + j;
+        const bool live = tq < rows;
+        const __bf16* qv = q + (static_cast<int64_t>(qb + (live ? tq : 0)) * hq + q_head) * D;
+#pragma unroll
+        for (int kk = 0; kk < S; ++kk) {
+            u32x4 w = load16(qv + (kk * 4 + g) * 8);
+            if (!live) w = u32x4{0, 0, 0, 0};
+            qop[qt][kk] = __builtin_bit_cast(bf16x8, w);
+        }
+    }
+
+    f32x4 acc[QT][NV];
+    float m[QT], l[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        m[qt] = kNegInf;
+        l[qt] = 0.f;
+#pragma unroll
+        for (int n = 0; n < NV; ++n) acc[qt][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    StageRegs<D> stg;
+    stage_load<D>(stg, k_cache, v_cache, req_blocks, 0, ctx, mbpr, block_size, kvh, hkv);
+    stage_store<D>(stg, lds_k[0], lds_v[0], lds_valid[0]);
+    __syncthreads();
+
+    for (int t = 0; t < ntiles; ++t) {
+        const int cur = t & 1;
+        const bool more = t + 1 < ntiles;
+        if (more) {
+            stage_load<D>(stg, k_cache, v_cache, req_blocks, (t + 1) * kKeysPerTile, ctx, mbpr,
+                          block_size, kvh, hkv);
+        }
+        const __bf16* lk = lds_k[cur];
+        const __bf16* lv = lds_v[cur];
+        const uint64_t vmask = __builtin_amdgcn_ballot_w64(lds_valid[cur][lane] != 0);
+
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+            const int key0 = t * kKeysPerTile + h2 * 32;
+            if (key0 > wave_max_key) continue;  // above the diagonal for every row here
+            const uint32_t hmask = static_cast<uint32_t>(vmask >> (h2 * 32));
+            const bool need_mask = (key0 + 31 > prefix + tw) || hmask != 0xffffffffu;
+
+            f32x4 st[2][QT];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt) st[kb][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kk = 0; kk < S; ++kk) {
+                    const int row = h2 * 32 + kb * 16 + i;
+                    const bf16x8 kop = __builtin_bit_cast(
+                        bf16x8, *reinterpret_cast<const u32x4*>(lk + lds_off<D>(row, kk * 4 + g)));
+#pragma unroll
+                    for (int qt = 0; qt < QT; ++qt)
+                        st[kb][qt] = mfma16x16x32(kop, qop[qt][kk], st[kb][qt]);
+                }
+            }
+
+            // V^T operand rows: lane (dim row i, grp g) reads key rows T(g, e).
+            uint32_t vr[8][NV / 2];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int row = h2 * 32 + (e >> 2) * 16 + g * 4 + (e & 3);
+                if constexpr (NV == 8) {
+                    const u32x4 w = *reinterpret_cast<const u32x4*>(lv + lds_off<D>(row, i));
+#pragma unroll
+                    for (int x = 0; x < 4; ++x) vr[e][x] = w[x];
+                } else if constexpr (NV == 4) {
+                    const u32x2 w = *reinterpret_cast<const u32x2*>(
+                        lv + lds_off<D>(row, i >> 1) + (i & 1) * 4);
+                    vr[e][0] = w[0];
+                    vr[e][1] = w[1];
+                } else {
+                    const u32x4 w0 = *reinterpret_cast<const u32x4*>(lv + lds_off<D>(row, 2 * i));
+                    const u32x4 w1 =
+                        *reinterpret_cast<const u32x4*>(lv + lds_off<D>(row, 2 * i + 1));
+#pragma unroll
+                    for (int x = 0; x < 4; ++x) {
+                        vr[e][x] = w0[x];
+                        vr[e][4 + x] = w1[x];
+                    }
+                }
+            }
+
+            bf16x8 pop[QT];
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) {
+                float sc[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) sc[e] = st[e >> 2][qt][e & 3] * scale_log2;
+                if (need_mask) {
+                    const int limit = prefix + tw + qt * 16 + j;  // last visible key of row
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const int kt = h2 * 32 + (e >> 2) * 16 + g * 4 + (e & 3);
+                        const int key = t * kKeysPerTile + kt;
+                        const bool ok = key <= limit && ((vmask >> kt) & 1ull);
+                        if (!ok) sc[e] = kNegInf;
+                    }
+                }
+                float mloc = sc[0];
+#pragma unroll
+                for (int e = 1; e < 8; ++e) mloc = fmaxf(mloc, sc[e]);
+                mloc = wave_max_xor16_32(mloc);
+                const float m_new = fmaxf(m[qt], mloc);
+                const float m_use = (m_new == kNegInf) ? 0.f : m_new;
+                const float alpha = __builtin_amdgcn_exp2f(m[qt] - m_use);
+                float p[8];
+                float psum = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    p[e] = __builtin_amdgcn_exp2f(sc[e] - m_use);
+                    psum += p[e];
+                }
+                l[qt] = l[qt] * alpha + psum;
+                m[qt] = m_new;
+#pragma unroll
+                for (int n = 0; n < NV; ++n) acc[qt][n] = acc[qt][n] * alpha;
+                u32x4 pw;
+#pragma unroll
+                for (int x = 0; x < 4; ++x) pw[x] = pack_bf16x2(p[2 * x], p[2 * x + 1]);
+                pop[qt] = __builtin_bit_cast(bf16x8, pw);
+            }
+
+#pragma unroll
+            for (int n = 0; n < NV; ++n) {
+                u32x4 vw;
+#pragma unroll
+                for (int x = 0; x < 4; ++x)
+                    vw[x] = pick_halves(vr[2 * x][n >> 1], vr[2 * x + 1][n >> 1], n & 1);
+                const bf16x8 vop = __builtin_bit_cast(bf16x8, vw);
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt) acc[qt][n] = mfma16x16x32(vop, pop[qt], acc[qt][n]);
+            }
+        }
+
+        if (more) stage_store<D>(stg, lds_k[cur ^ 1], lds_v[cur ^ 1], lds_valid[cur ^ 1]);
+        __syncthreads();
+    }
+
+    // Epilogue: lane (j, g) holds O[row][NV*(4g + r) + n] = acc[qt][n][r].
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        const float l_tot = wave_sum_xor16_32(l[qt]);
+        const int tq = tw + qt * 16 + j;
+        if (tq >= rows) continue;
+        const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+        __bf16* o = out + (static_cast<int64_t>(qb + tq) * hq + q_head) * D;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            uint32_t w[NV / 2];
+#pragma unroll
+            for (int x = 0; x < NV / 2; ++x)
+                w[x] = pack_bf16x2(acc[qt][2 * x][r] * inv, acc[qt][2 * x + 1][r] * inv);
+            uint32_t* dst = reinterpret_cast<uint32_t*>(o + NV * (4 * g + r));
+#pragma unroll
+            for (int x = 0; x < NV / 2; ++x) dst[x] = w[x];
+        }
+    }
+}
+
+struct PrefillLayout {
+    size_t counts_off, tiles_off, dec_off, decode_ws_off, total;
+    int max_tiles;
+    int tile_tokens;
+    DecodePlan plan;
+};
+
+size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+int tile_tokens_for(int head_dim, int G) {
+    const int qw = head_dim <= 128 ? 64 : 32;
+    return (4 / heads_per_wg(G)) * qw;
+}
+
+PrefillLayout prefill_layout(int batch_size, int total_query_tokens, int max_blocks_per_req,
+                             int num_q_heads, int num_kv_heads, int head_dim, int block_size) {
+    PrefillLayout L{};
+    const int G = num_q_heads / num_kv_heads;
+    L.tile_tokens = tile_tokens_for(head_dim, G);
+    L.max_tiles = total_query_tokens / L.tile_tokens + batch_size;
+    L.plan = plan_decode(batch_size, num_kv_heads, max_blocks_per_req * block_size);
+    size_t off = 0;
+    L.counts_off = off;
+    off = align256(off + 2 * sizeof(int32_t));
+    L.tiles_off = off;
+    off = align256(off + static_cast<size_t>(L.max_tiles) * sizeof(TileEntry));
+    L.dec_off = off;
+    off = align256(off + static_cast<size_t>(batch_size) * sizeof(int32_t));
+    L.decode_ws_off = off;
+    off = align256(off + decode_workspace_bytes(batch_size, num_q_heads, head_dim, L.plan));
+    L.total = off;
+    return L;
+}
+
+template <int D>
+hipError_t launch_tiles(const void* q, const void* k_cache, const void* v_cache,
+                        const int32_t* block_table, const int32_t* qsl,
+                        const int32_t* context_lens, void* output, int total_query_tokens,
+                        int mbpr, int hq, int hkv, int block_size, const int32_t* counts,
+                        const TileEntry* tiles, int max_tiles, hipStream_t stream) {
+    const int G = hq / hkv;
+    const int U = hkv * (G / heads_per_wg(G));
+    const int64_t grid = static_cast<int64_t>(max_tiles) * U;
+    const float scale_log2 = kLog2e / sqrtf(static_cast<float>(D));
+    prefill_tile_kernel<D><<<static_cast<unsigned>(grid), kThreads, 0, stream>>>(
+        static_cast<const __bf16*>(q), static_cast<const __bf16*>(k_cache),
+        static_cast<const __bf16*>(v_cache), block_table, qsl, context_lens,
+        static_cast<__bf16*>(output), counts, tiles, total_query_tokens, mbpr, hq, hkv,
+        block_size, scale_log2);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool prefill_fast_supported(int num_q_heads, int num_kv_heads, int head_dim) {
+    if (num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0) return false;
+    const int G = num_q_heads / num_kv_heads;
+    return G <= 16 && (head_dim == 64 || head_dim == 128 || head_dim == 256);
+}
+
+size_t prefill_workspace_bytes(int batch_size, int total_query_tokens, int max_blocks_per_req,
+                               int num_q_heads, int num_kv_heads, int head_dim,
+                               int block_size) {
+    return prefill_layout(batch_size, total_query_tokens, max_blocks_per_req, num_q_heads,
+                          num_kv_heads, head_dim, block_size)
+        .total;
+}
+
+hipError_t prefill_attention(const void* q, const void* k_cache, const void* v_cache,
+                             const int32_t* block_table, const int32_t* query_start_loc,
+                             const int32_t* context_lens, void* output, int batch_size,
+                             int total_query_tokens, int max_blocks_per_req, int num_q_heads,
+                             int num_kv_heads, int head_dim, int block_size, void* workspace,
+                             hipStream_t stream) {
+    if (batch_size > kMaxPlanRequests) return hipErrorInvalidValue;
+    const PrefillLayout L = prefill_layout(batch_size, total_query_tokens, max_blocks_per_req,
+                                           num_q_heads, num_kv_heads, head_dim, block_size);
+    char* ws = static_cast<char*>(workspace);
+    int32_t* counts = reinterpret_cast<int32_t*>(ws + L.counts_off);
+    TileEntry* tiles = reinterpret_cast<TileEntry*>(ws + L.tiles_off);
+    int32_t* dec = reinterpret_cast<int32_t*>(ws + L.dec_off);
+    prefill_plan_kernel<<<1, 1024, 0, stream>>>(query_start_loc, context_lens, batch_size,
+                                                total_query_tokens, L.tile_tokens, counts, tiles,
+                                                dec);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    switch (head_dim) {
+        case 64:
+            err = launch_tiles<64>(q, k_cache, v_cache, block_table, query_start_loc,
+                                   context_lens, output, total_query_tokens, max_blocks_per_req,
+                                   num_q_heads, num_kv_heads, block_size, counts, tiles,
+                                   L.max_tiles, stream);
+            break;
+        case 128:
+            err = launch_tiles<128>(q, k_cache, v_cache, block_table, query_start_loc,
+                                    context_lens, output, total_query_tokens, max_blocks_per_req,
+                                    num_q_heads, num_kv_heads, block_size, counts, tiles,
+                                    L.max_tiles, stream);
+            break;
+        case 256:
+            err = launch_tiles<256>(q, k_cache, v_cache, block_table, query_start_loc,
+                                    context_lens, output, total_query_tokens, max_blocks_per_req,
+                                    num_q_heads, num_kv_heads, block_size, counts, tiles,
+                                    L.max_tiles, stream);
+            break;
+        default:
+            return hipErrorInvalidValue;
+    }
+    if (err != hipSuccess) return err;
+    // Single-token requests of a mixed batch: split-KV decode with prefill semantics.
+    DecodeItems items;
+    items.num_items = batch_size;
+    items.item_count = counts + 1;
+    items.item_req = dec;
+    items.query_start_loc = query_start_loc;
+    items.denom_eps = 0.0f;
+    items.zero_invalid = false;
+    return decode_attention(q, k_cache, v_cache, block_table, context_lens, output, items,
+                            max_blocks_per_req, num_q_heads, num_kv_heads, head_dim, block_size,
+                            L.plan, ws + L.decode_ws_off, stream);
+}
+
+}  // namespace ccinfer::hipk

@@ -1,0 +1,171 @@
+"""Torch-facing operators over the C ABI, mirroring the reference's backend ops.
+
+Reference interface: DeviceBackend::{write_kv_cache, decode_attention, prefill_attention}
+(src/backend/backend.h:172-223) with the parameter structs of src/backend/params.h:148-211.
+Argument names, meaning and error behaviour follow it: invalid arguments raise
+CcinferError with code ErrorCode::InvalidArgument (6), the same value the reference returns.
+
+Tensors are device tensors (torch on ROCm: "cuda" is the HIP device). Layouts:
+  q, output (decode)   [batch, num_q_heads, head_dim]            bf16
+  q, output (prefill)  [total_query_tokens, num_q_heads, head_dim] bf16
+  k_cache, v_cache     [num_slots, num_kv_heads, head_dim] bf16 (one layer), or
+                       [num_blocks, block_size, num_kv_heads, head_dim]
+  block_table          [batch, max_blocks_per_req] int32, -1 padded
+  context_lens         [batch] int32; query_start_loc [batch + 1] int32
+  slot_mapping         [total_tokens] int32
+Work is enqueued on torch's current stream; workspaces come from torch's caching
+allocator unless passed in.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+INVALID_ARGUMENT = 6
+
+
+class CcinferError(RuntimeError):
+    """A non-zero status from the C ABI (value of the reference's ErrorCode)."""
+
+    def __init__(self, code: int, op: str):
+        msg = _lib.load().ccinfer_error_message(code).decode()
+        super().__init__(f"{op}: {msg} (code {code})")
+        self.code = code
+
+
+def _check(code: int, op: str) -> None:
+    if code != 0:
+        raise CcinferError(code, op)
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _require(cond: bool, op: str) -> None:
+    if not cond:
+        raise CcinferError(INVALID_ARGUMENT, op)
+
+
+def _dev_tensor(t: Optional[torch.Tensor], dtype: torch.dtype, op: str) -> None:
+    _require(t is not None and t.is_cuda and t.dtype == dtype and t.is_contiguous(), op)
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _kv_shape(k_cache: torch.Tensor):
+    """(num_slots, num_kv_heads, head_dim) of a 3-D or 4-D cache tensor."""
+    if k_cache.dim() == 4:
+        nb, bs, h, d = k_cache.shape
+        return nb * bs, h, d
+    s, h, d = k_cache.shape
+    return s, h, d
+
+
+def write_kv_cache(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor,
+                   v_cache: torch.Tensor, slot_mapping: torch.Tensor,
+                   max_slots: Optional[int] = None) -> None:
+    """cache[slot_mapping[t]] = new[t] for K and V (write_kv_cache.cu:12-34)."""
+    op = "write_kv_cache"
+    for t in (k_new, v_new, k_cache, v_cache):
+        _dev_tensor(t, torch.bfloat16, op)
+    _dev_tensor(slot_mapping, torch.int32, op)
+    slots, hkv, d = _kv_shape(k_cache)
+    _require(k_new.shape[-2:] == (hkv, d) and v_new.shape == k_new.shape, op)
+    _require(v_cache.numel() == k_cache.numel(), op)
+    total = k_new.numel() // (hkv * d)
+    _require(slot_mapping.numel() == total, op)
+    lib = _lib.load()
+    _check(lib.ccinfer_write_kv_cache(_ptr(k_new), _ptr(v_new), _ptr(k_cache), _ptr(v_cache),
+                                      _ptr(slot_mapping), total, hkv, d,
+                                      slots if max_slots is None else max_slots, _stream()), op)
+
+
+def decode_workspace_size(batch_size: int, max_blocks_per_req: int, num_q_heads: int,
+                          num_kv_heads: int, head_dim: int, cache_block_size: int = 16) -> int:
+    return int(_lib.load().ccinfer_decode_workspace_size(
+        batch_size, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim, cache_block_size))
+
+
+def prefill_workspace_size(batch_size: int, total_query_tokens: int, max_blocks_per_req: int,
+                           num_q_heads: int, num_kv_heads: int, head_dim: int,
+                           cache_block_size: int = 16) -> int:
+    return int(_lib.load().ccinfer_prefill_workspace_size(
+        batch_size, total_query_tokens, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
+        cache_block_size))
+
+
+def _workspace(nbytes: int, device, workspace: Optional[torch.Tensor]):
+    if nbytes == 0:
+        return None, 0
+    if workspace is not None:
+        _require(workspace.is_cuda and workspace.numel() * workspace.element_size() >= nbytes,
+                 "workspace")
+        return workspace, workspace.numel() * workspace.element_size()
+    return torch.empty(nbytes, dtype=torch.uint8, device=device), nbytes
+
+
+def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                     block_table: torch.Tensor, context_lens: torch.Tensor,
+                     output: Optional[torch.Tensor] = None, cache_block_size: int = 16,
+                     workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Paged decode attention (decode_attn.cu:364-473 semantics); returns output."""
+    op = "decode_attention"
+    for t in (q, k_cache, v_cache):
+        _dev_tensor(t, torch.bfloat16, op)
+    _dev_tensor(block_table, torch.int32, op)
+    _dev_tensor(context_lens, torch.int32, op)
+    _require(q.dim() == 3 and block_table.dim() == 2, op)
+    b, hq, d = q.shape
+    _, hkv, dk = _kv_shape(k_cache)
+    _require(dk == d and block_table.shape[0] == b and context_lens.numel() == b, op)
+    if output is None:
+        output = torch.empty_like(q)
+    _dev_tensor(output, torch.bfloat16, op)
+    _require(output.shape == q.shape, op)
+    mbpr = block_table.shape[1]
+    need = decode_workspace_size(b, mbpr, hq, hkv, d, cache_block_size)
+    ws, ws_bytes = _workspace(need, q.device, workspace)
+    _check(_lib.load().ccinfer_decode_attention(
+        _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(block_table), _ptr(context_lens),
+        _ptr(output), b, mbpr, hq, hkv, d, cache_block_size, _ptr(ws), ws_bytes, _stream()), op)
+    return output
+
+
+def prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                      block_table: torch.Tensor, query_start_loc: torch.Tensor,
+                      context_lens: torch.Tensor, output: Optional[torch.Tensor] = None,
+                      cache_block_size: int = 16,
+                      workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Paged causal prefill attention (prefill_attn.cu:43-242 semantics); returns output.
+
+    Rows the reference leaves unwritten (requests with context_len < query_len) keep the
+    contents of `output` (uninitialised when `output` is None).
+    """
+    op = "prefill_attention"
+    for t in (q, k_cache, v_cache):
+        _dev_tensor(t, torch.bfloat16, op)
+    for t in (block_table, query_start_loc, context_lens):
+        _dev_tensor(t, torch.int32, op)
+    _require(q.dim() == 3 and block_table.dim() == 2, op)
+    total, hq, d = q.shape
+    _, hkv, dk = _kv_shape(k_cache)
+    b = context_lens.numel()
+    _require(dk == d and block_table.shape[0] == b and query_start_loc.numel() == b + 1, op)
+    if output is None:
+        output = torch.empty_like(q)
+    _dev_tensor(output, torch.bfloat16, op)
+    _require(output.shape == q.shape, op)
+    mbpr = block_table.shape[1]
+    need = prefill_workspace_size(b, total, mbpr, hq, hkv, d, cache_block_size)
+    ws, ws_bytes = _workspace(need, q.device, workspace)
+    _check(_lib.load().ccinfer_prefill_attention(
+        _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(block_table), _ptr(query_start_loc),
+        _ptr(context_lens), _ptr(output), b, total, mbpr, hq, hkv, d, cache_block_size, _ptr(ws),
+        ws_bytes, _stream()), op)
+    return output

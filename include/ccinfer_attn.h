@@ -1,0 +1,101 @@
+/*
+ * ccinfer_attn.h -- C ABI of the MI355X (gfx950) paged-attention hot path.
+ *
+ * Drop-in for the three kernel launchers of 7QiC/ccInfer declared in
+ * src/kernel/cuda_kernels.h:61-84, with the same argument meaning, the same KV-cache layout
+ * ([slot][num_kv_heads][head_dim] bf16, slot = block_id * cache_block_size + offset,
+ * src/cache/kv_cache_storage.cpp:75-136) and the same block-table contract (int32
+ * [batch][max_blocks_per_req], -1 padding, src/worker/batch_translator.cpp:213-293).
+ *
+ * Plain pointers and sizes only. All pointers except `stream` are device pointers.
+ * `stream` is a hipStream_t (NULL = the default stream). Every call only enqueues work on
+ * `stream`: no host synchronisation and no device allocation. Split-KV partials and the
+ * prefill work list live in a caller-provided workspace sized by the *_workspace_size
+ * queries (the reference launchers take no workspace; the C++ drop-in wrappers in
+ * ccinfer_amd/csrc/dropin supply one owned per stream).
+ *
+ * Return value: 0 on success, otherwise the numeric value of the reference's
+ * ccinfer::ErrorCode (src/base/error_code.h:8-45) -- the same codes the reference returns
+ * through Result<void>.
+ *
+ * Thread safety: stateless and re-entrant; concurrent calls on different streams must use
+ * different workspaces.
+ */
+#ifndef CCINFER_ATTN_H
+#define CCINFER_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Numeric values of ccinfer::ErrorCode (src/base/error_code.h:8-45). */
+enum ccinfer_status {
+    CCINFER_OK = 0,
+    CCINFER_ERR_DEVICE_OUT_OF_MEMORY = 1,  /* ErrorCode::CudaOutOfMemory   */
+    CCINFER_ERR_LAUNCH_FAILED = 2,         /* ErrorCode::CudaLaunchFailed  */
+    CCINFER_ERR_DEVICE_INVALID_VALUE = 3,  /* ErrorCode::CudaInvalidValue  */
+    CCINFER_ERR_DEVICE_RUNTIME = 4,        /* ErrorCode::CudaRuntimeError  */
+    CCINFER_ERR_INVALID_ARGUMENT = 6,      /* ErrorCode::InvalidArgument   */
+    CCINFER_ERR_UNSUPPORTED = 26,          /* ErrorCode::Unsupported       */
+    CCINFER_ERR_INTERNAL = 27              /* ErrorCode::InternalError     */
+};
+
+/* Replaces launch_write_kv_cache (src/kernel/cuda_kernels.h:80-83,
+ * src/kernel/attention/write_kv_cache.cu:38-50).
+ * k_new/v_new: [total_tokens][n_kv_heads][head_dim] bf16; k_cache/v_cache: one layer,
+ * [max_slots][n_kv_heads][head_dim] bf16; slot_mapping: [total_tokens] int32. Tokens whose
+ * slot is outside [0, max_slots) are skipped. Bit-exact copy. */
+int ccinfer_write_kv_cache(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                           const int32_t* slot_mapping, int total_tokens, int n_kv_heads,
+                           int head_dim, int max_slots, void* stream);
+
+/* Workspace bytes ccinfer_decode_attention needs for this batch shape (may be 0). */
+size_t ccinfer_decode_workspace_size(int batch_size, int max_blocks_per_req, int num_q_heads,
+                                     int num_kv_heads, int head_dim, int cache_block_size);
+
+/* Replaces launch_decode_attention (src/kernel/cuda_kernels.h:72-77,
+ * src/kernel/attention/decode_attn.cu:515-570).
+ * q, output: [batch_size][num_q_heads][head_dim] bf16; block_table: [batch_size]
+ * [max_blocks_per_req] int32; context_lens: [batch_size] int32, including the current
+ * token (whose K/V must already be written). cache_block_size must be 16 and head_dim one
+ * of {32,64,80,96,112,120,128,192,256} (as in the reference). Unlike the reference, there
+ * is no context-length ceiling (split-KV). */
+int ccinfer_decode_attention(const void* q, const void* k_cache, const void* v_cache,
+                             const int32_t* block_table, const int32_t* context_lens,
+                             void* output, int batch_size, int max_blocks_per_req,
+                             int num_q_heads, int num_kv_heads, int head_dim,
+                             int cache_block_size, void* workspace, size_t workspace_bytes,
+                             void* stream);
+
+/* Workspace bytes ccinfer_prefill_attention needs for this batch shape. */
+size_t ccinfer_prefill_workspace_size(int batch_size, int total_query_tokens,
+                                      int max_blocks_per_req, int num_q_heads,
+                                      int num_kv_heads, int head_dim, int cache_block_size);
+
+/* Replaces launch_prefill_attention (src/kernel/cuda_kernels.h:61-66,
+ * src/kernel/attention/prefill_attn.cu:246-279).
+ * q, output: [total_query_tokens][num_q_heads][head_dim] bf16; query_start_loc:
+ * [batch_size + 1]; context_lens[r] = prefix_r + query_len_r; query i of request r sees
+ * cache positions [0, prefix_r + i]. Mixed batches (single-token decode items next to
+ * prompt chunks) are accepted, as in the reference. head_dim <= 256. */
+int ccinfer_prefill_attention(const void* q, const void* k_cache, const void* v_cache,
+                              const int32_t* block_table, const int32_t* query_start_loc,
+                              const int32_t* context_lens, void* output, int batch_size,
+                              int total_query_tokens, int max_blocks_per_req, int num_q_heads,
+                              int num_kv_heads, int head_dim, int cache_block_size,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
+/* Human-readable text for a status code (the reference's error_message()). */
+const char* ccinfer_error_message(int code);
+
+/* Library version, "major.minor.patch". */
+const char* ccinfer_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CCINFER_ATTN_H */

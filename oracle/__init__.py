@@ -1,0 +1,148 @@
+"""numpy front end of the CPU oracle (liboracle.so, built from attn_oracle.c by the Makefile).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the cpu_baseline
+leg of bench.py as the checker; the product path never imports it.
+bf16 arrays are numpy uint16 bit patterns. Citations of the reference functions each
+oracle routine restates are in attn_oracle.h.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+from typing import Optional
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle.so"
+
+_lib = None
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB_PATH
+
+
+def load() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        lib = ctypes.CDLL(str(LIB_PATH))
+        lib.orc_f32_to_bf16_array.argtypes = [_P, _P, ctypes.c_int64]
+        lib.orc_kv_base_offset.argtypes = [_I, _I, _I, _I, _I, _I, _P, _P]
+        lib.orc_kv_base_offset.restype = _I
+        lib.orc_write_kv_cache.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _I]
+        lib.orc_decode_attention.argtypes = [_P, _P, _P, _P, _P, _P] + [_I] * 7
+        lib.orc_decode_attention_pairs.argtypes = [_P, _P, _P, _P, _P, _P] + [_I] * 6 + [_P, _I, _I]
+        lib.orc_prefill_attention.argtypes = [_P] * 7 + [_I] * 8
+        lib.orc_prefill_attention_pairs.argtypes = [_P] * 7 + [_I] * 7 + [_P, _I, _I]
+        lib.orc_naive_attention.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I]
+        lib.orc_lcg_fill.argtypes = [_P, _I, ctypes.c_uint]
+        _lib = lib
+    return _lib
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(_P)
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+def default_threads() -> int:
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def f32_to_bf16(x) -> np.ndarray:
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    load().orc_f32_to_bf16_array(_p(x), _p(out), x.size)
+    return out
+
+
+def bf16_to_f32(h) -> np.ndarray:
+    h = _c(h, np.uint16)
+    return (h.astype(np.uint32) << 16).view(np.float32)
+
+
+def kv_base_offset(ctx_pos, kv_head, head_dim, num_kv_heads, block_size, req_blocks):
+    rb = _c(req_blocks, np.int32)
+    out = np.zeros(1, np.int64)
+    ok = load().orc_kv_base_offset(ctx_pos, kv_head, head_dim, num_kv_heads, block_size,
+                                   rb.size, _p(rb), _p(out))
+    return int(out[0]) if ok else None
+
+
+def write_kv_cache(k_new, v_new, k_cache, v_cache, slot_mapping, max_slots=None) -> None:
+    """In place on k_cache / v_cache (uint16 arrays [slots, Hkv, D])."""
+    assert k_cache.flags.c_contiguous and v_cache.flags.c_contiguous
+    kn, vn = _c(k_new, np.uint16), _c(v_new, np.uint16)
+    sm = _c(slot_mapping, np.int32)
+    slots, hkv, d = k_cache.shape
+    load().orc_write_kv_cache(_p(kn), _p(vn), _p(k_cache), _p(v_cache), _p(sm), sm.size, hkv, d,
+                              slots if max_slots is None else max_slots)
+
+
+def decode(q, k_cache, v_cache, block_table, context_lens, block_size: int = 16,
+           nthreads: Optional[int] = None, pairs=None) -> np.ndarray:
+    """fp32 [B, Hq, D]; with `pairs` ([(b, hq)...]) only those rows are computed (rest 0)."""
+    q, k, v = _c(q, np.uint16), _c(k_cache, np.uint16), _c(v_cache, np.uint16)
+    bt, cl = _c(block_table, np.int32), _c(context_lens, np.int32)
+    b, hq, d = q.shape
+    hkv = k.shape[-2]
+    out = np.zeros((b, hq, d), np.float32)
+    nt = default_threads() if nthreads is None else nthreads
+    if pairs is None:
+        load().orc_decode_attention(_p(q), _p(k), _p(v), _p(bt), _p(cl), _p(out), b, bt.shape[1],
+                                    hq, hkv, d, block_size, nt)
+    else:
+        pr = _c(pairs, np.int32).reshape(-1, 2)
+        load().orc_decode_attention_pairs(_p(q), _p(k), _p(v), _p(bt), _p(cl), _p(out), b,
+                                          bt.shape[1], hq, hkv, d, block_size, _p(pr),
+                                          pr.shape[0], nt)
+    return out
+
+
+def prefill(q, k_cache, v_cache, block_table, query_start_loc, context_lens,
+            block_size: int = 16, nthreads: Optional[int] = None, pairs=None,
+            out: Optional[np.ndarray] = None) -> np.ndarray:
+    """fp32 [T, Hq, D]; rows the reference leaves unwritten keep `out`'s values (0)."""
+    q, k, v = _c(q, np.uint16), _c(k_cache, np.uint16), _c(v_cache, np.uint16)
+    bt, qsl, cl = (_c(block_table, np.int32), _c(query_start_loc, np.int32),
+                   _c(context_lens, np.int32))
+    t, hq, d = q.shape
+    hkv = k.shape[-2]
+    if out is None:
+        out = np.zeros((t, hq, d), np.float32)
+    nt = default_threads() if nthreads is None else nthreads
+    if pairs is None:
+        load().orc_prefill_attention(_p(q), _p(k), _p(v), _p(bt), _p(qsl), _p(cl), _p(out),
+                                     cl.size, t, bt.shape[1], hq, hkv, d, block_size, nt)
+    else:
+        pr = _c(pairs, np.int32).reshape(-1, 2)
+        load().orc_prefill_attention_pairs(_p(q), _p(k), _p(v), _p(bt), _p(qsl), _p(cl), _p(out),
+                                           cl.size, t, bt.shape[1], hq, hkv, d, block_size,
+                                           _p(pr), pr.shape[0], nt)
+    return out
+
+
+def naive(q, k, v) -> np.ndarray:
+    """Dense causal attention on contiguous q [T,Hq,D], k/v [T,Hkv,D]; fp32 out."""
+    q, k, v = _c(q, np.uint16), _c(k, np.uint16), _c(v, np.uint16)
+    t, hq, d = q.shape
+    out = np.zeros((t, hq, d), np.float32)
+    load().orc_naive_attention(_p(q), _p(k), _p(v), _p(out), t, hq, k.shape[1], d)
+    return out
+
+
+def lcg_fill(n: int, seed: int) -> np.ndarray:
+    out = np.empty(n, np.uint16)
+    load().orc_lcg_fill(_p(out), n, seed)
+    return out

@@ -1,0 +1,347 @@
+/*
+ * CPU oracle for the paged-attention hot path. TEST INFRASTRUCTURE ONLY: loaded by
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg as the checker;
+ * the shipped library never links it. Function-by-function citations of the
+ * reference (7QiC/ccInfer) are in attn_oracle.h and on each function below.
+ *
+ * Accumulation is fp32 in the same order as the reference's scalar CPU code
+ * (sequential over head_dim, then over context positions).
+ */
+#include "attn_oracle.h"
+
+#include <float.h>
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------- */
+/* bf16 <-> fp32, round to nearest even on the 16 dropped mantissa bits.       */
+/* ------------------------------------------------------------------------- */
+uint16_t orc_f32_to_bf16(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu) != 0) {
+        return (uint16_t)((u >> 16) | 0x0040u); /* NaN stays NaN (quiet) */
+    }
+    const uint32_t lsb = (u >> 16) & 1u;
+    u += 0x7fffu + lsb;
+    return (uint16_t)(u >> 16);
+}
+
+float orc_bf16_to_f32(uint16_t h) {
+    uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+void orc_f32_to_bf16_array(const float* src, uint16_t* dst, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) dst[i] = orc_f32_to_bf16(src[i]);
+}
+
+/* src/kernel/attention/attn_common.cuh:7-27 */
+int orc_kv_base_offset(int ctx_pos, int kv_head, int head_dim, int num_kv_heads,
+                       int cache_block_size, int max_blocks_per_req, const int32_t* req_blocks,
+                       int64_t* out) {
+    const int logical_block = ctx_pos / cache_block_size;
+    const int offset_in_block = ctx_pos - logical_block * cache_block_size;
+    if (logical_block < 0 || logical_block >= max_blocks_per_req) return 0;
+    const int physical_block = req_blocks[logical_block];
+    if (physical_block < 0) return 0;
+    const int64_t slot = (int64_t)physical_block * cache_block_size + offset_in_block;
+    *out = (slot * num_kv_heads + kv_head) * (int64_t)head_dim;
+    return 1;
+}
+
+/* src/kernel/attention/write_kv_cache.cu:12-34 */
+void orc_write_kv_cache(const uint16_t* k_new, const uint16_t* v_new, uint16_t* k_cache,
+                        uint16_t* v_cache, const int32_t* slot_mapping, int total_tokens,
+                        int n_kv_heads, int head_dim, int max_slots) {
+    const int64_t row = (int64_t)n_kv_heads * head_dim;
+    for (int t = 0; t < total_tokens; ++t) {
+        const int slot = slot_mapping[t];
+        if (slot < 0 || slot >= max_slots) continue;
+        memcpy(k_cache + (int64_t)slot * row, k_new + (int64_t)t * row, (size_t)row * 2);
+        memcpy(v_cache + (int64_t)slot * row, v_new + (int64_t)t * row, (size_t)row * 2);
+    }
+}
+
+/* ------------------------------------------------------------------------- */
+/* One (query vector, kv_head) attention over positions [0, visible) of one    */
+/* request's block-table row. Invalid positions (logical block out of range or  */
+/* block id < 0) are skipped. `eps` is added to the softmax denominator:        */
+/* decode uses 1e-6 (decode_attn.cu:455), prefill uses 0 (prefill_attn.cu:238). */
+/* Writes zeros when no position is valid (both kernels end with 0 there).      */
+/* ------------------------------------------------------------------------- */
+static void attend_one(const uint16_t* qv, const uint16_t* k_cache, const uint16_t* v_cache,
+                       const int32_t* req_blocks, int visible, int kv_head, int head_dim,
+                       int num_kv_heads, int block_size, int mbpr, float scale, float eps,
+                       float* scores, int64_t* bases, float* out) {
+    float max_score = -INFINITY;
+    int any = 0;
+    for (int pos = 0; pos < visible; ++pos) {
+        int64_t base;
+        if (!orc_kv_base_offset(pos, kv_head, head_dim, num_kv_heads, block_size, mbpr,
+                                req_blocks, &base)) {
+            bases[pos] = -1;
+            continue;
+        }
+        bases[pos] = base;
+        float s = 0.0f;
+        for (int d = 0; d < head_dim; ++d) {
+            s += orc_bf16_to_f32(qv[d]) * orc_bf16_to_f32(k_cache[base + d]);
+        }
+        s *= scale;
+        scores[pos] = s;
+        if (s > max_score) max_score = s;
+        any = 1;
+    }
+    for (int d = 0; d < head_dim; ++d) out[d] = 0.0f;
+    if (!any) return;
+    float denom = 0.0f;
+    for (int pos = 0; pos < visible; ++pos) {
+        if (bases[pos] < 0) continue;
+        scores[pos] = expf(scores[pos] - max_score);
+        denom += scores[pos];
+    }
+    const float inv = 1.0f / (denom + eps);
+    for (int d = 0; d < head_dim; ++d) {
+        float acc = 0.0f;
+        for (int pos = 0; pos < visible; ++pos) {
+            if (bases[pos] < 0) continue;
+            acc += (scores[pos] * inv) * orc_bf16_to_f32(v_cache[bases[pos] + d]);
+        }
+        out[d] = acc;
+    }
+}
+
+/* ------------------------------------------------------------------------- */
+/* Thread pool helper: run fn(i, ctx) for i in [0, n) over nthreads workers.   */
+/* ------------------------------------------------------------------------- */
+typedef void (*work_fn)(int64_t i, void* ctx, float* scores, int64_t* bases);
+
+typedef struct {
+    work_fn fn;
+    void* ctx;
+    int64_t n;
+    int64_t begin, end;
+    int max_ctx;
+} worker_arg;
+
+static void* worker_main(void* p) {
+    worker_arg* a = (worker_arg*)p;
+    float* scores = (float*)malloc(sizeof(float) * (size_t)(a->max_ctx > 0 ? a->max_ctx : 1));
+    int64_t* bases = (int64_t*)malloc(sizeof(int64_t) * (size_t)(a->max_ctx > 0 ? a->max_ctx : 1));
+    for (int64_t i = a->begin; i < a->end; ++i) a->fn(i, a->ctx, scores, bases);
+    free(scores);
+    free(bases);
+    return NULL;
+}
+
+static void run_parallel(work_fn fn, void* ctx, int64_t n, int nthreads, int max_ctx) {
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > n) nthreads = (int)(n > 0 ? n : 1);
+    worker_arg* args = (worker_arg*)calloc((size_t)nthreads, sizeof(worker_arg));
+    pthread_t* th = (pthread_t*)calloc((size_t)nthreads, sizeof(pthread_t));
+    for (int t = 0; t < nthreads; ++t) {
+        args[t].fn = fn;
+        args[t].ctx = ctx;
+        args[t].n = n;
+        args[t].begin = n * t / nthreads;
+        args[t].end = n * (t + 1) / nthreads;
+        args[t].max_ctx = max_ctx;
+    }
+    if (nthreads == 1) {
+        worker_main(&args[0]);
+    } else {
+        for (int t = 0; t < nthreads; ++t) pthread_create(&th[t], NULL, worker_main, &args[t]);
+        for (int t = 0; t < nthreads; ++t) pthread_join(th[t], NULL);
+    }
+    free(args);
+    free(th);
+}
+
+/* ------------------------------------------------------------------------- */
+/* Paged decode. Math: tests/kernel/test_decode_attn.cu:24-86. Edge cases of    */
+/* the live kernel, src/kernel/attention/decode_attn.cu:384-473:                */
+/*   ctx <= 0 -> zeros (:399-404); ceil(ctx/16) > MBPR -> zeros (:406-412);     */
+/*   invalid block id -> position skipped (:423-440); denominator + 1e-6 (:455).*/
+/* ------------------------------------------------------------------------- */
+typedef struct {
+    const uint16_t *q, *k, *v;
+    const int32_t *bt, *ctx;
+    float* out;
+    int B, mbpr, hq, hkv, d, bs;
+    const int32_t* pairs;
+} decode_ctx;
+
+static void decode_one(int64_t i, void* p, float* scores, int64_t* bases) {
+    const decode_ctx* c = (const decode_ctx*)p;
+    int req, qh;
+    if (c->pairs) {
+        req = c->pairs[2 * i];
+        qh = c->pairs[2 * i + 1];
+    } else {
+        req = (int)(i / c->hq);
+        qh = (int)(i % c->hq);
+    }
+    float* o = c->out + ((int64_t)req * c->hq + qh) * c->d;
+    const int context_len = c->ctx[req];
+    const int num_blocks = context_len > 0 ? (context_len + c->bs - 1) / c->bs : 0;
+    if (context_len <= 0 || num_blocks > c->mbpr) {
+        for (int d = 0; d < c->d; ++d) o[d] = 0.0f;
+        return;
+    }
+    const int gqa = c->hq / c->hkv;
+    const int kvh = qh / gqa;
+    const float scale = 1.0f / sqrtf((float)c->d);
+    attend_one(c->q + ((int64_t)req * c->hq + qh) * c->d, c->k, c->v,
+               c->bt + (int64_t)req * c->mbpr, context_len, kvh, c->d, c->hkv, c->bs, c->mbpr,
+               scale, 1e-6f, scores, bases, o);
+}
+
+static int max_ctx_of(const int32_t* ctx, int B) {
+    int m = 1;
+    for (int b = 0; b < B; ++b)
+        if (ctx[b] > m) m = ctx[b];
+    return m;
+}
+
+void orc_decode_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                          const int32_t* block_table, const int32_t* context_lens, float* out,
+                          int batch_size, int max_blocks_per_req, int num_q_heads,
+                          int num_kv_heads, int head_dim, int cache_block_size, int nthreads) {
+    decode_ctx c = {q, k_cache, v_cache, block_table, context_lens, out, batch_size,
+                    max_blocks_per_req, num_q_heads, num_kv_heads, head_dim, cache_block_size,
+                    NULL};
+    run_parallel(decode_one, &c, (int64_t)batch_size * num_q_heads, nthreads,
+                 max_ctx_of(context_lens, batch_size));
+}
+
+void orc_decode_attention_pairs(const uint16_t* q, const uint16_t* k_cache,
+                                const uint16_t* v_cache, const int32_t* block_table,
+                                const int32_t* context_lens, float* out, int batch_size,
+                                int max_blocks_per_req, int num_q_heads, int num_kv_heads,
+                                int head_dim, int cache_block_size, const int32_t* pairs,
+                                int num_pairs, int nthreads) {
+    decode_ctx c = {q, k_cache, v_cache, block_table, context_lens, out, batch_size,
+                    max_blocks_per_req, num_q_heads, num_kv_heads, head_dim, cache_block_size,
+                    pairs};
+    run_parallel(decode_one, &c, num_pairs, nthreads, max_ctx_of(context_lens, batch_size));
+}
+
+/* ------------------------------------------------------------------------- */
+/* Paged causal prefill: src/kernel/attention/prefill_attn.cu:80-241.           */
+/*   request = last r with query_start_loc[r] <= token (linear scan, :83-86);  */
+/*   prefix = ctx - qlen; rows with prefix < 0 or an inconsistent range are     */
+/*   left unwritten (:92-113); query i sees positions [0, prefix + i] (:112);   */
+/*   invalid positions skipped; no valid position -> 0 (:238).                  */
+/* ------------------------------------------------------------------------- */
+typedef struct {
+    const uint16_t *q, *k, *v;
+    const int32_t *bt, *qsl, *ctx;
+    float* out;
+    int B, T, mbpr, hq, hkv, d, bs;
+    const int32_t* pairs;
+} prefill_ctx;
+
+static void prefill_one(int64_t i, void* p, float* scores, int64_t* bases) {
+    const prefill_ctx* c = (const prefill_ctx*)p;
+    int g, qh;
+    if (c->pairs) {
+        g = c->pairs[2 * i];
+        qh = c->pairs[2 * i + 1];
+    } else {
+        g = (int)(i / c->hq);
+        qh = (int)(i % c->hq);
+    }
+    int req = 0;
+    while (req + 1 < c->B && c->qsl[req + 1] <= g) ++req;
+    const int qbeg = c->qsl[req];
+    const int qlen = c->qsl[req + 1] - qbeg;
+    const int local = g - qbeg;
+    if (qlen <= 0 || local < 0 || local >= qlen) return;
+    const int context_len = c->ctx[req];
+    const int prefix = context_len - qlen;
+    if (prefix < 0) return;
+    const int visible = prefix + local + 1;
+    if (visible <= 0 || visible > context_len) return;
+    const int gqa = c->hq / c->hkv;
+    const int kvh = qh / gqa;
+    const float scale = 1.0f / sqrtf((float)c->d);
+    attend_one(c->q + ((int64_t)g * c->hq + qh) * c->d, c->k, c->v,
+               c->bt + (int64_t)req * c->mbpr, visible, kvh, c->d, c->hkv, c->bs, c->mbpr, scale,
+               0.0f, scores, bases, c->out + ((int64_t)g * c->hq + qh) * c->d);
+}
+
+void orc_prefill_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                           const int32_t* block_table, const int32_t* query_start_loc,
+                           const int32_t* context_lens, float* out, int batch_size,
+                           int total_query_tokens, int max_blocks_per_req, int num_q_heads,
+                           int num_kv_heads, int head_dim, int cache_block_size, int nthreads) {
+    prefill_ctx c = {q, k_cache, v_cache, block_table, query_start_loc, context_lens, out,
+                     batch_size, total_query_tokens, max_blocks_per_req, num_q_heads,
+                     num_kv_heads, head_dim, cache_block_size, NULL};
+    run_parallel(prefill_one, &c, (int64_t)total_query_tokens * num_q_heads, nthreads,
+                 max_ctx_of(context_lens, batch_size));
+}
+
+void orc_prefill_attention_pairs(const uint16_t* q, const uint16_t* k_cache,
+                                 const uint16_t* v_cache, const int32_t* block_table,
+                                 const int32_t* query_start_loc, const int32_t* context_lens,
+                                 float* out, int batch_size, int total_query_tokens,
+                                 int max_blocks_per_req, int num_q_heads, int num_kv_heads,
+                                 int head_dim, int cache_block_size, const int32_t* pairs,
+                                 int num_pairs, int nthreads) {
+    prefill_ctx c = {q, k_cache, v_cache, block_table, query_start_loc, context_lens, out,
+                     batch_size, total_query_tokens, max_blocks_per_req, num_q_heads,
+                     num_kv_heads, head_dim, cache_block_size, pairs};
+    run_parallel(prefill_one, &c, num_pairs, nthreads, max_ctx_of(context_lens, batch_size));
+}
+
+/* tests/kernel/test_naive_attn.cu:16-65: dense causal attention, row i sees keys
+ * 0..i, normalised by the plain sum. */
+void orc_naive_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, float* out,
+                         int num_tokens, int n_q_heads, int n_kv_heads, int head_dim) {
+    const int gqa = n_q_heads / n_kv_heads;
+    const float scale = 1.0f / sqrtf((float)head_dim);
+    const int qs = n_q_heads * head_dim, ks = n_kv_heads * head_dim;
+    float* sc = (float*)malloc(sizeof(float) * (size_t)(num_tokens > 0 ? num_tokens : 1));
+    for (int hq = 0; hq < n_q_heads; ++hq) {
+        const int hk = hq / gqa;
+        for (int i = 0; i < num_tokens; ++i) {
+            float mx = -1e30f;
+            for (int j = 0; j <= i; ++j) {
+                float s = 0.0f;
+                for (int d = 0; d < head_dim; ++d)
+                    s += orc_bf16_to_f32(q[i * qs + hq * head_dim + d]) *
+                         orc_bf16_to_f32(k[j * ks + hk * head_dim + d]);
+                sc[j] = s * scale;
+                mx = fmaxf(mx, sc[j]);
+            }
+            float sum = 0.0f;
+            for (int j = 0; j <= i; ++j) {
+                sc[j] = expf(sc[j] - mx);
+                sum += sc[j];
+            }
+            for (int j = 0; j <= i; ++j) sc[j] /= sum;
+            for (int d = 0; d < head_dim; ++d) {
+                float acc = 0.0f;
+                for (int j = 0; j <= i; ++j) acc += sc[j] * orc_bf16_to_f32(v[j * ks + hk * head_dim + d]);
+                out[i * qs + hq * head_dim + d] = acc;
+            }
+        }
+    }
+    free(sc);
+}
+
+/* tests/kernel/test_naive_attn.cu:67-74 */
+void orc_lcg_fill(uint16_t* data, int n, unsigned int seed) {
+    unsigned int s = seed;
+    for (int i = 0; i < n; ++i) {
+        s = s * 1103515245u + 12345u;
+        const float v = (float)((s >> 16) & 0x7FFF) / 32768.0f - 1.0f;
+        data[i] = orc_f32_to_bf16(v * 0.5f);
+    }
+}

@@ -1,0 +1,94 @@
+/*
+ * CPU oracle for the paged-attention hot path (TEST INFRASTRUCTURE ONLY).
+ *
+ * This library is the checker, never the product: only tests/, the smoke()
+ * entry of __graft_entry__.py and the cpu_baseline leg of bench.py may load it.
+ * The shipped path (libccinfer_attn.so) never links or calls it.
+ *
+ * It restates, in plain C with fp32 accumulation, the algorithm of the
+ * reference's attention path (7QiC/ccInfer):
+ *   - bf16 <-> fp32 conversion, round-to-nearest-even (the semantics of
+ *     __float2bfloat16_rn used throughout the reference kernels);
+ *   - orc_kv_base_offset      : src/kernel/attention/attn_common.cuh:7-27
+ *   - orc_write_kv_cache      : src/kernel/attention/write_kv_cache.cu:12-34
+ *   - orc_decode_attention    : tests/kernel/test_decode_attn.cu:24-86 (math) with the
+ *                               edge cases of src/kernel/attention/decode_attn.cu:384-473
+ *   - orc_prefill_attention   : src/kernel/attention/prefill_attn.cu:80-241 with the
+ *                               causal contract of src/backend/params.h:140-146
+ *   - orc_naive_attention     : tests/kernel/test_naive_attn.cu:16-65 (dense causal)
+ *   - orc_lcg_fill            : tests/kernel/test_naive_attn.cu:67-74
+ *
+ * Every function is pinned by tests/test_oracle.py (known-answer vectors from the
+ * reference tests, closed forms, torch's float64 scaled_dot_product_attention as an
+ * independent library routine, and cross-identities between the functions).
+ *
+ * bf16 values travel as uint16_t bit patterns.
+ */
+#ifndef CCINFER_ATTN_ORACLE_H
+#define CCINFER_ATTN_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+uint16_t orc_f32_to_bf16(float x);
+float orc_bf16_to_f32(uint16_t h);
+void orc_f32_to_bf16_array(const float* src, uint16_t* dst, int64_t n);
+
+/* Returns 1 and sets *out when ctx_pos maps to a valid cache row, else 0. */
+int orc_kv_base_offset(int ctx_pos, int kv_head, int head_dim, int num_kv_heads,
+                       int cache_block_size, int max_blocks_per_req,
+                       const int32_t* req_blocks, int64_t* out);
+
+/* Scatter k_new/v_new[t][h][d] into cache[slot_mapping[t]][h][d]; slots outside
+ * [0, max_slots) are skipped. */
+void orc_write_kv_cache(const uint16_t* k_new, const uint16_t* v_new, uint16_t* k_cache,
+                        uint16_t* v_cache, const int32_t* slot_mapping, int total_tokens,
+                        int n_kv_heads, int head_dim, int max_slots);
+
+/* out: fp32 [batch][num_q_heads][head_dim]. nthreads <= 1 runs single-threaded. */
+void orc_decode_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                          const int32_t* block_table, const int32_t* context_lens, float* out,
+                          int batch_size, int max_blocks_per_req, int num_q_heads,
+                          int num_kv_heads, int head_dim, int cache_block_size, int nthreads);
+
+/* Same as orc_decode_attention restricted to the (request, q_head) pairs listed in
+ * pairs[2*i], pairs[2*i+1] (used to time a bounded sample of a large batch). */
+void orc_decode_attention_pairs(const uint16_t* q, const uint16_t* k_cache,
+                                const uint16_t* v_cache, const int32_t* block_table,
+                                const int32_t* context_lens, float* out, int batch_size,
+                                int max_blocks_per_req, int num_q_heads, int num_kv_heads,
+                                int head_dim, int cache_block_size, const int32_t* pairs,
+                                int num_pairs, int nthreads);
+
+/* out: fp32 [total_query_tokens][num_q_heads][head_dim]; rows the reference leaves
+ * unwritten (malformed metadata) are left untouched. */
+void orc_prefill_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                           const int32_t* block_table, const int32_t* query_start_loc,
+                           const int32_t* context_lens, float* out, int batch_size,
+                           int total_query_tokens, int max_blocks_per_req, int num_q_heads,
+                           int num_kv_heads, int head_dim, int cache_block_size, int nthreads);
+
+/* Same as orc_prefill_attention restricted to the (query token, q_head) pairs listed. */
+void orc_prefill_attention_pairs(const uint16_t* q, const uint16_t* k_cache,
+                                 const uint16_t* v_cache, const int32_t* block_table,
+                                 const int32_t* query_start_loc, const int32_t* context_lens,
+                                 float* out, int batch_size, int total_query_tokens,
+                                 int max_blocks_per_req, int num_q_heads, int num_kv_heads,
+                                 int head_dim, int cache_block_size, const int32_t* pairs,
+                                 int num_pairs, int nthreads);
+
+/* Dense causal attention on contiguous q[T][Hq][D], k/v[T][Hkv][D]; out fp32. */
+void orc_naive_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, float* out,
+                         int num_tokens, int n_q_heads, int n_kv_heads, int head_dim);
+
+/* The reference tests' LCG fill: values in [-0.5, 0.5) rounded to bf16. */
+void orc_lcg_fill(uint16_t* data, int n, unsigned int seed);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,167 @@
+"""Paged decode attention on the GPU against the CPU oracle (and closed forms).
+
+Reference behaviour: src/kernel/attention/decode_attn.cu:364-473; reference tests:
+tests/kernel/test_decode_attn.cu (SingleDecodeStep :88-163, GQA :165-227,
+RandomPagedGQAMatchesCpuReference :229-311, NullPointers :313-325).
+Bar: max-abs <= 2e-2 and mean-abs <= 2e-3 against the fp32 oracle.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from ccinfer_amd import CcinferError, decode_attention, write_kv_cache
+from ccinfer_amd import workloads as W
+from tests._util import assert_attn_close, f32, from_u16, say, u16
+
+pytestmark = pytest.mark.gpu
+
+
+def run_decode(w: W.PagedWorkload, dev, block_size=16):
+    meta = w.device_meta(dev)
+    out = decode_attention(w.q, w.k_cache, w.v_cache, meta["block_table"],
+                           meta["context_lens"], cache_block_size=block_size)
+    torch.cuda.synchronize()
+    return out
+
+
+def oracle_decode(w: W.PagedWorkload, pairs=None, block_size=16):
+    return oracle.decode(u16(w.q), u16(w.k_cache), u16(w.v_cache), w.block_table,
+                         w.context_lens, block_size=block_size, pairs=pairs)
+
+
+def _kat(dev):
+    b, hq, hkv, d, nphys = 2, 8, 2, 64, 3
+    qi = np.arange(b * hq * d)
+    ki = np.arange(nphys * 16 * hkv * d)
+    q = oracle.f32_to_bf16((((qi * 17) % 23 - 11) * 0.03125).astype(np.float32))
+    k = oracle.f32_to_bf16((((ki * 13) % 29 - 14) * 0.025).astype(np.float32))
+    v = oracle.f32_to_bf16((((ki * 7) % 31 - 15) * 0.02).astype(np.float32))
+    return W.PagedWorkload(
+        "kat", hq, hkv, d, np.array([31, 17], np.int32),
+        np.array([[2, 0, 1], [1, 2, -1]], np.int32), nphys,
+        from_u16(q.reshape(b, hq, d), dev), from_u16(k.reshape(-1, hkv, d), dev),
+        from_u16(v.reshape(-1, hkv, d), dev))
+
+
+def test_reference_kat_random_paged_gqa(gpu):
+    say("decode KAT RandomPagedGQAMatchesCpuReference")
+    w = _kat(gpu)
+    got = f32(run_decode(w, gpu))
+    want = oracle_decode(w)
+    mx, _ = assert_attn_close(got, want, "KAT")
+    assert mx < 0.01  # the reference test's own bound
+
+
+def test_uniform_scores_give_mean_v(gpu):
+    say("decode closed form Q=K=0.1 V=0.2")
+    b, hq, hkv, d = 2, 4, 4, 64
+    q = torch.full((b, hq, d), 0.1, dtype=torch.bfloat16, device=gpu)
+    k = torch.full((32, hkv, d), 0.1, dtype=torch.bfloat16, device=gpu)
+    v = torch.full((32, hkv, d), 0.2, dtype=torch.bfloat16, device=gpu)
+    bt = torch.tensor([[0, 1], [0, 1]], dtype=torch.int32, device=gpu)
+    cl = torch.tensor([32, 32], dtype=torch.int32, device=gpu)
+    out = f32(decode_attention(q, k, v, bt, cl))
+    vbf = float(torch.tensor(0.2, dtype=torch.bfloat16))
+    assert np.allclose(out, vbf, atol=2e-3)
+    assert np.array_equal(out[0], out[1])
+
+
+def test_gqa_heads_equal(gpu):
+    say("decode GQA heads equal")
+    q = torch.full((1, 8, 64), 0.1, dtype=torch.bfloat16, device=gpu)
+    kv = torch.full((16, 2, 64), 0.1, dtype=torch.bfloat16, device=gpu)
+    out = f32(decode_attention(q, kv, kv, torch.zeros((1, 1), dtype=torch.int32, device=gpu),
+                               torch.tensor([16], dtype=torch.int32, device=gpu)))
+    assert np.abs(out - out[:, :1]).max() < 1e-2
+
+
+def test_config1_single_sequence(gpu):
+    say("decode config1 b1 ctx512")
+    w = W.decode_single(device=gpu)
+    assert_attn_close(f32(run_decode(w, gpu)), oracle_decode(w), "config1")
+
+
+def test_config2_batched_with_write(gpu):
+    say("decode config2 b64 ctx U[128,4096] + write")
+    w = W.decode_batched(device=gpu)
+    meta = w.device_meta(gpu)
+    write_kv_cache(w.k_new, w.v_new, w.k_cache, w.v_cache, meta["slot_mapping"])
+    got = f32(run_decode(w, gpu))
+    assert_attn_close(got, oracle_decode(w), "config2")
+
+
+def test_config5_long_context_sampled(gpu):
+    say("decode config5 b32 ctx32768 gqa4 (sampled rows)")
+    w = W.decode_long(device=gpu)
+    got = f32(run_decode(w, gpu))
+    rng = np.random.default_rng(11)
+    pairs = np.stack([rng.integers(0, w.batch, 48), rng.integers(0, w.hq, 48)], 1)
+    pairs = np.concatenate([pairs, [[0, 0], [w.batch - 1, w.hq - 1]]]).astype(np.int32)
+    want = oracle_decode(w, pairs=pairs)
+    assert_attn_close(got[pairs[:, 0], pairs[:, 1]], want[pairs[:, 0], pairs[:, 1]], "config5")
+    assert np.all(np.isfinite(got))
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(16, 8, 64), (16, 8, 256), (8, 8, 128), (32, 8, 128),
+                                      (64, 4, 128), (32, 1, 128),  # G=16 fast, G=32 generic
+                                      (16, 8, 80), (12, 4, 96), (8, 2, 32), (8, 4, 192),
+                                      (4, 2, 112), (4, 4, 120)])
+def test_head_shapes(gpu, hq, hkv, d):
+    say(f"decode shape hq={hq} hkv={hkv} d={d}")
+    w = W.decode_batched(device=gpu, seed=hq * 1000 + hkv * 10 + d, batch=5, ctx_lo=1,
+                         ctx_hi=700, hq=hq, hkv=hkv, d=d, with_write=False)
+    assert_attn_close(f32(run_decode(w, gpu)), oracle_decode(w), f"hq{hq}/hkv{hkv}/d{d}")
+
+
+def test_edge_cases_zero_ctx_overflow_and_holes(gpu):
+    say("decode edge cases")
+    w = W.decode_batched(device=gpu, seed=21, batch=6, ctx_lo=40, ctx_hi=300, with_write=False)
+    ctx = w.context_lens.copy()
+    bt = w.block_table.copy()
+    ctx[0] = 0                                   # -> zeros
+    ctx[1] = bt.shape[1] * 16 + 1                # more blocks than the row holds -> zeros
+    ctx[2] = int(np.count_nonzero(bt[2] >= 0)) * 16
+    bt[2, 1] = -1                                # hole: those 16 positions are skipped
+    ctx[3] = 1                                   # single position
+    w.context_lens, w.block_table = ctx.astype(np.int32), bt
+    got = f32(run_decode(w, gpu))
+    want = oracle_decode(w)
+    assert np.all(got[0] == 0) and np.all(got[1] == 0)
+    assert_attn_close(got, want, "edge")
+
+
+def test_unwritten_slots_holding_nan_do_not_leak(gpu):
+    say("decode NaN in unused slots")
+    w = W.decode_batched(device=gpu, seed=5, batch=8, ctx_lo=17, ctx_hi=200, with_write=False)
+    used = np.zeros(w.num_blocks * 16, bool)
+    for b in range(w.batch):
+        pos = np.arange(w.context_lens[b])
+        used[w.block_table[b, pos // 16] * 16 + pos % 16] = True
+    nan_rows = torch.from_numpy(np.nonzero(~used)[0]).to(gpu)
+    w.k_cache[nan_rows] = float("nan")
+    w.v_cache[nan_rows] = float("inf")
+    got = f32(run_decode(w, gpu))
+    assert np.all(np.isfinite(got))
+    assert_attn_close(got, oracle_decode(w), "nan-slots")
+
+
+def test_deterministic(gpu):
+    say("decode determinism")
+    w = W.decode_batched(device=gpu, seed=9, batch=16, with_write=False)
+    a = u16(run_decode(w, gpu))
+    b = u16(run_decode(w, gpu))
+    assert np.array_equal(a, b)
+
+
+def test_rejects_bad_arguments(gpu):
+    say("decode argument errors")
+    w = _kat(gpu)
+    meta = w.device_meta(gpu)
+    with pytest.raises(CcinferError) as e:
+        decode_attention(w.q, w.k_cache, w.v_cache, meta["block_table"], meta["context_lens"],
+                         cache_block_size=32)
+    assert e.value.code == 6
+    q7 = torch.zeros((2, 7, 64), dtype=torch.bfloat16, device=gpu)  # 7 % 2 != 0
+    with pytest.raises(CcinferError):
+        decode_attention(q7, w.k_cache, w.v_cache, meta["block_table"], meta["context_lens"])

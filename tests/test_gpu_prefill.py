@@ -1,0 +1,203 @@
+"""Paged causal prefill attention on the GPU against the CPU oracle.
+
+Reference behaviour: src/kernel/attention/prefill_attn.cu:43-242 and the causal contract of
+src/backend/params.h:140-146; reference tests: tests/kernel/test_prefill_attn.cu:24-105
+(paged prefill == dense causal attention for prefix 0 and an identity table, max-abs < 0.02),
+tests/integration/test_prefix_cache_e2e.cpp (shared prefix blocks drive prefill).
+Bar: max-abs <= 2e-2 and mean-abs <= 2e-3 against the fp32 oracle.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from ccinfer_amd import decode_attention, prefill_attention, write_kv_cache
+from ccinfer_amd import workloads as W
+from tests._util import assert_attn_close, f32, from_u16, say, u16
+
+pytestmark = pytest.mark.gpu
+
+
+def run_prefill(w, dev, out=None, block_size=16, total=None):
+    meta = w.device_meta(dev)
+    q = w.q if total is None else w.q[:total]
+    if out is not None and total is not None:
+        out = out[:total]
+    o = prefill_attention(q, w.k_cache, w.v_cache, meta["block_table"],
+                          meta["query_start_loc"], meta["context_lens"], output=out,
+                          cache_block_size=block_size)
+    torch.cuda.synchronize()
+    return o
+
+
+def oracle_prefill(w, pairs=None, block_size=16, out=None, total=None):
+    q = u16(w.q) if total is None else u16(w.q[:total])
+    return oracle.prefill(q, u16(w.k_cache), u16(w.v_cache), w.block_table,
+                          w.query_start_loc, w.context_lens, block_size=block_size,
+                          pairs=pairs, out=out)
+
+
+def write_new(w, dev):
+    write_kv_cache(w.k_new, w.v_new, w.k_cache, w.v_cache,
+                   torch.from_numpy(w.slot_mapping).to(dev))
+
+
+def sample_pairs(w, n, seed):
+    rng = np.random.default_rng(seed)
+    t = int(w.query_start_loc[-1])
+    rows = np.concatenate([rng.integers(0, t, n), w.query_start_loc[:-1],
+                           w.query_start_loc[1:] - 1])
+    heads = np.concatenate([rng.integers(0, w.hq, n), np.zeros(w.batch, np.int64),
+                            np.full(w.batch, w.hq - 1)])
+    return np.stack([rows, heads], 1).astype(np.int32)
+
+
+def test_reference_single_request_matches_dense(gpu):
+    """test_prefill_attn.cu:24-105 with the LCG fill of test_naive_attn.cu:67-74."""
+    say("prefill KAT single request vs dense causal")
+    t, h, d = 32, 4, 64
+    q = oracle.lcg_fill(t * h * d, 1).reshape(t, h, d)
+    kc = oracle.lcg_fill(4 * 16 * h * d, 2).reshape(64, h, d)
+    vc = oracle.lcg_fill(4 * 16 * h * d, 3).reshape(64, h, d)
+    w = W.PagedWorkload("kat", h, h, d, np.array([t], np.int32), np.array([[0, 1]], np.int32),
+                        4, from_u16(q, gpu), from_u16(kc, gpu), from_u16(vc, gpu),
+                        query_start_loc=np.array([0, t], np.int32))
+    got = f32(run_prefill(w, gpu))
+    dense = oracle.naive(q, kc[:t], vc[:t])
+    mx, _ = assert_attn_close(got, dense, "vs dense")
+    assert mx < 0.02
+    assert_attn_close(got, oracle_prefill(w), "vs paged oracle")
+
+
+def test_config3_prefix_cached(gpu):
+    say("prefill config3 8x(512+1536), shared prefix (sampled rows)")
+    w = W.prefill_prefix(device=gpu)
+    write_new(w, gpu)
+    got = f32(run_prefill(w, gpu))
+    pairs = sample_pairs(w, 384, 3)
+    want = oracle_prefill(w, pairs=pairs)
+    r, h = pairs[:, 0], pairs[:, 1]
+    assert_attn_close(got[r, h], want[r, h], "config3")
+    assert np.all(np.isfinite(got))
+
+
+def test_shared_prefix_equals_private_copy(gpu):
+    """Two sequences listing the same prefix blocks == one of them on a private copy."""
+    say("prefill shared prefix == private copy")
+    w = W.prefill_prefix(device=gpu, seed=8, n_seqs=3, prefix=64, new=100, hq=16, hkv=8)
+    write_new(w, gpu)
+    shared = u16(run_prefill(w, gpu))
+    # Give seq 1 private copies of its (shared) prefix blocks in fresh pool blocks.
+    pblk = 64 // 16
+    extra = w.num_blocks
+    kc = torch.cat([w.k_cache, torch.empty((pblk * 16,) + w.k_cache.shape[1:],
+                                           dtype=w.k_cache.dtype, device=gpu)])
+    vc = torch.cat([w.v_cache, torch.empty_like(kc[:pblk * 16])])
+    bt = w.block_table.copy()
+    for i in range(pblk):
+        src = int(bt[1, i])
+        kc[(extra + i) * 16:(extra + i + 1) * 16] = w.k_cache[src * 16:(src + 1) * 16]
+        vc[(extra + i) * 16:(extra + i + 1) * 16] = w.v_cache[src * 16:(src + 1) * 16]
+        bt[1, i] = extra + i
+    assert np.array_equal(w.block_table[0, :pblk], w.block_table[1, :pblk])
+    w2 = W.PagedWorkload("copy", w.hq, w.hkv, w.d, w.context_lens, bt, extra + pblk, w.q, kc, vc,
+                         query_start_loc=w.query_start_loc)
+    private = u16(run_prefill(w2, gpu))
+    assert np.array_equal(shared, private)
+
+
+def test_mixed_chunked_prefill_and_decode(gpu):
+    say("prefill mixed 4x512 chunks + 128 decodes (sampled rows)")
+    w = W.mixed_step(device=gpu)
+    write_new(w, gpu)
+    got = f32(run_prefill(w, gpu))
+    pairs = sample_pairs(w, 256, 4)
+    want = oracle_prefill(w, pairs=pairs)
+    r, h = pairs[:, 0], pairs[:, 1]
+    assert_attn_close(got[r, h], want[r, h], "mixed")
+    # Decode items through prefill == the decode operator on the same rows.
+    nc = w.info["n_chunks"]
+    rows = torch.from_numpy(w.query_start_loc[nc:-1].astype(np.int64)).to(gpu)
+    meta = w.device_meta(gpu)
+    dec = decode_attention(w.q[rows].contiguous(), w.k_cache, w.v_cache,
+                           meta["block_table"][nc:].contiguous(),
+                           meta["context_lens"][nc:].contiguous())
+    assert_attn_close(got[w.query_start_loc[nc:-1]], f32(dec), "mixed decode items")
+
+
+@pytest.mark.parametrize("hq,hkv,d,new,prefix", [
+    (16, 8, 128, 200, 48), (4, 4, 128, 70, 0), (16, 4, 128, 130, 32), (8, 8, 64, 90, 16),
+    (16, 8, 256, 75, 32), (6, 2, 128, 40, 16), (16, 8, 96, 37, 16), (4, 2, 80, 33, 0),
+    (32, 2, 128, 20, 16)])
+def test_head_shapes_and_ragged_lengths(gpu, hq, hkv, d, new, prefix):
+    say(f"prefill shape hq={hq} hkv={hkv} d={d} new={new} prefix={prefix}")
+    w = W.prefill_prefix(device=gpu, seed=hq + d + new, n_seqs=3, prefix=prefix, new=new,
+                         share_pairs=(), hq=hq, hkv=hkv, d=d)
+    write_new(w, gpu)
+    assert_attn_close(f32(run_prefill(w, gpu)), oracle_prefill(w), f"hq{hq}/hkv{hkv}/d{d}")
+
+
+def test_varlen_batch_edge_cases(gpu):
+    """qlen 1..3 items, prefix < 0 rows left untouched, holes and table overflow."""
+    say("prefill varlen edge cases")
+    rng = np.random.default_rng(12)
+    hq, hkv, d = 16, 8, 128
+    qlen = np.array([2, 1, 3, 5, 130, 1, 64], np.int32)
+    ctx = np.array([40, 17, 3, 2, 200, 1, 300], np.int32)   # seq 3: prefix < 0 (untouched)
+    mbpr = 16
+    pool = 128
+    perm = rng.permutation(pool).astype(np.int32)
+    bt = perm[:len(qlen) * mbpr].reshape(len(qlen), mbpr).copy()
+    bt[4, 3] = -1                      # hole inside a long prefill
+    bt[6, 15] = -1
+    qsl = np.concatenate([[0], np.cumsum(qlen)]).astype(np.int32)
+    total = int(qsl[-1])
+    g = torch.Generator(device=gpu)
+    g.manual_seed(5)
+    q = W.randn_bf16((total, hq, d), g, gpu)
+    kc = W.randn_bf16((pool * 16, hkv, d), g, gpu)
+    vc = W.randn_bf16((pool * 16, hkv, d), g, gpu)
+    w = W.PagedWorkload("edge", hq, hkv, d, ctx, bt, pool, q, kc, vc, query_start_loc=qsl)
+    sentinel = torch.full_like(q, 7.0)
+    got = f32(run_prefill(w, gpu, out=sentinel.clone()))
+    want = oracle_prefill(w, out=np.full((total, hq, d), 7.0, np.float32))
+    untouched = slice(qsl[3], qsl[4])
+    assert np.all(got[untouched] == 7.0)
+    assert_attn_close(got, want, "edge")
+
+
+def test_rows_past_total_tokens_not_processed(gpu):
+    say("prefill total_query_tokens < query_start_loc[B]")
+    w = W.prefill_prefix(device=gpu, seed=30, n_seqs=2, prefix=16, new=80, share_pairs=(),
+                         hq=8, hkv=4, d=128)
+    write_new(w, gpu)
+    total = 120
+    out = torch.full_like(w.q, 3.0)
+    got = f32(run_prefill(w, gpu, out=out, total=total))
+    want = oracle_prefill(w, total=total, out=np.full((total, w.hq, w.d), 3.0, np.float32))
+    assert_attn_close(got, want, "clipped")
+
+
+def test_generic_block_size(gpu):
+    """Non-16 cache blocks (accepted by the reference prefill launcher) on the generic path."""
+    say("prefill block_size 8")
+    rng = np.random.default_rng(3)
+    hq, hkv, d, bs = 8, 4, 128, 8
+    qlen, ctx, mbpr, pool = np.array([20, 9], np.int32), np.array([50, 9], np.int32), 8, 20
+    bt = rng.permutation(pool)[:16].reshape(2, 8).astype(np.int32)
+    qsl = np.array([0, 20, 29], np.int32)
+    g = torch.Generator(device=gpu)
+    g.manual_seed(2)
+    q = W.randn_bf16((29, hq, d), g, gpu)
+    kc = W.randn_bf16((pool * bs, hkv, d), g, gpu)
+    vc = W.randn_bf16((pool * bs, hkv, d), g, gpu)
+    w = W.PagedWorkload("bs8", hq, hkv, d, ctx, bt, pool, q, kc, vc, query_start_loc=qsl)
+    got = f32(run_prefill(w, gpu, block_size=bs))
+    assert_attn_close(got, oracle_prefill(w, block_size=bs), "bs8")
+
+
+def test_deterministic(gpu):
+    say("prefill determinism")
+    w = W.prefill_prefix(device=gpu, seed=4, n_seqs=2, prefix=32, new=300, share_pairs=())
+    write_new(w, gpu)
+    assert np.array_equal(u16(run_prefill(w, gpu)), u16(run_prefill(w, gpu)))
