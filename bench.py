@@ -1,0 +1,347 @@
+"""Benchmark of the paged-attention hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5] [--no-cpu]
+
+One "step" is one pass of the hot path over one batch of synthetic input already resident in
+HBM. The headline (the JSON `value`) is BASELINE.json's decode metric on configs[1]: batched
+paged decode, batch 64, Qwen3-0.6B heads (16 q / 8 kv, d=128), contexts U[128, 4096], one
+step = KV-cache write of the 64 new tokens + decode attention; value = algorithmic KV bytes
+read per step (K+V of every context position, once per (sequence, kv_head)) / step time.
+The other configurations are reported under "configs". rank 0 prints ONE JSON line.
+
+Timing: W untimed warm-up steps, then exactly K steps bracketed by device synchronisation;
+per-op kernel time is measured with HIP events recorded on the stream the kernels run on.
+cpu_baseline: the CPU oracle (a C restatement of the reference's CPU attention path) on the
+box's host cores, on the same workload. `--profile-op NAME` runs only that op in a loop (for
+rocprofv3 counter runs) and prints nothing else.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from ccinfer_amd import _lib  # noqa: E402
+from ccinfer_amd import workloads as W  # noqa: E402
+
+HBM_PEAK = 8.0e12          # B/s, MI355X HBM3E
+BF16_PEAK = 2.5e15         # FLOP/s, MI355X dense bf16 MFMA
+PROFILES = ROOT / "profiles"
+
+
+class Ops:
+    """Preallocated C-ABI calls on one stream (no allocation inside the timed loop)."""
+
+    def __init__(self, w: W.PagedWorkload, dev, stream: torch.cuda.Stream):
+        self.w, self.dev, self.stream = w, dev, stream
+        self.lib = _lib.load()
+        self.meta = w.device_meta(dev)
+        self.s = stream.cuda_stream
+        self.out = torch.empty_like(w.q)
+        if w.query_start_loc is None:
+            n = self.lib.ccinfer_decode_workspace_size(w.batch, w.mbpr, w.hq, w.hkv, w.d, 16)
+        else:
+            n = self.lib.ccinfer_prefill_workspace_size(w.batch, w.q.shape[0], w.mbpr, w.hq,
+                                                        w.hkv, w.d, 16)
+        self.ws_bytes = int(n)
+        self.ws = torch.empty(max(1, self.ws_bytes), dtype=torch.uint8, device=dev)
+
+    def write(self):
+        w = self.w
+        rc = self.lib.ccinfer_write_kv_cache(
+            w.k_new.data_ptr(), w.v_new.data_ptr(), w.k_cache.data_ptr(), w.v_cache.data_ptr(),
+            self.meta["slot_mapping"].data_ptr(), w.k_new.shape[0], w.hkv, w.d,
+            w.k_cache.shape[0], self.s)
+        assert rc == 0, rc
+
+    def decode(self):
+        w = self.w
+        rc = self.lib.ccinfer_decode_attention(
+            w.q.data_ptr(), w.k_cache.data_ptr(), w.v_cache.data_ptr(),
+            self.meta["block_table"].data_ptr(), self.meta["context_lens"].data_ptr(),
+            self.out.data_ptr(), w.batch, w.mbpr, w.hq, w.hkv, w.d, 16, self.ws.data_ptr(),
+            self.ws_bytes, self.s)
+        assert rc == 0, rc
+
+    def prefill(self):
+        w = self.w
+        rc = self.lib.ccinfer_prefill_attention(
+            w.q.data_ptr(), w.k_cache.data_ptr(), w.v_cache.data_ptr(),
+            self.meta["block_table"].data_ptr(), self.meta["query_start_loc"].data_ptr(),
+            self.meta["context_lens"].data_ptr(), self.out.data_ptr(), w.batch, w.q.shape[0],
+            w.mbpr, w.hq, w.hkv, w.d, 16, self.ws.data_ptr(), self.ws_bytes, self.s)
+        assert rc == 0, rc
+
+
+def time_loop(fn, steps: int, warmup: int, stream: torch.cuda.Stream):
+    """Returns (event ms per step, host-clock ms per step)."""
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        start.record(stream)
+        for _ in range(steps):
+            fn()
+        end.record(stream)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    return start.elapsed_time(end) / steps, (t1 - t0) * 1e3 / steps
+
+
+def traffic_from_profiles(kernel_tag: str):
+    """HBM bytes per dispatch recorded by the rocprofv3 --pmc runs (profiles/*.md)."""
+    f = PROFILES / f"{kernel_tag}.pmc.md"
+    if not f.exists():
+        return None
+    m = re.search(r"hbm_bytes_per_dispatch:\s*([0-9.eE+]+)", f.read_text())
+    return float(m.group(1)) if m else None
+
+
+def cpu_threads() -> int:
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def u16(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def cpu_decode_baseline(w: W.PagedWorkload, budget_s: float, pairs=None):
+    """Times the oracle decode on the host (all rows, or `pairs`); returns (s/step, reps)."""
+    import oracle  # test infrastructure: the baseline being reported, never the product
+    q, k, v = u16(w.q), u16(w.k_cache), u16(w.v_cache)
+    nt = cpu_threads()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.decode(q, k, v, w.block_table, w.context_lens, nthreads=nt, pairs=pairs)
+        reps += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    return (time.perf_counter() - t0) / reps, reps
+
+
+def cpu_prefill_baseline(w: W.PagedWorkload, pairs, budget_s: float):
+    import oracle
+    q, k, v = u16(w.q), u16(w.k_cache), u16(w.v_cache)
+    nt = cpu_threads()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.prefill(q, k, v, w.block_table, w.query_start_loc, w.context_lens, nthreads=nt,
+                       pairs=pairs)
+        reps += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    return (time.perf_counter() - t0) / reps, reps
+
+
+def prefill_pair_flops(w: W.PagedWorkload, pairs) -> int:
+    """FLOPs of the (query row, head) pairs: 4*D per visible key."""
+    qsl = w.query_start_loc
+    tot = 0
+    for r, _h in pairs:
+        b = int(np.searchsorted(qsl, r, side="right") - 1)
+        ql = int(qsl[b + 1] - qsl[b])
+        pre = int(w.context_lens[b]) - ql
+        tot += pre + (r - int(qsl[b])) + 1
+    return 4 * w.d * tot
+
+
+def bench_decode(w, dev, steps, warmup, with_write, stream):
+    ops = Ops(w, dev, stream)
+    step = (lambda: (ops.write(), ops.decode())) if with_write else ops.decode
+    ms, host_ms = time_loop(step, steps, warmup, stream)
+    dec_ms, _ = time_loop(ops.decode, steps, warmup, stream)
+    res = {"ms_per_step": ms, "host_ms_per_step": host_ms, "decode_ms": dec_ms,
+           "kv_bytes": w.kv_bytes()}
+    if with_write:
+        wr_ms, _ = time_loop(ops.write, steps, warmup, stream)
+        res["write_ms"] = wr_ms
+    res["kv_GBps"] = w.kv_bytes() / (ms * 1e-3) / 1e9
+    res["decode_kernel_GBps"] = w.kv_bytes() / (dec_ms * 1e-3) / 1e9
+    res["hbm_frac"] = res["decode_kernel_GBps"] * 1e9 / HBM_PEAK
+    return res
+
+
+def run(args):
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream(device=dev)  # default priority
+    configs = [int(c) for c in args.configs.split(",") if c]
+    out = {}
+    head = None
+    nt = cpu_threads()
+
+    if 1 in configs:
+        w = W.decode_single(device=dev)
+        r = bench_decode(w, dev, max(args.steps, 50), args.warmup, False, stream)
+        if not args.no_cpu:
+            s, reps = cpu_decode_baseline(w, 1.0)
+            r["cpu_GBps"] = w.kv_bytes() / s / 1e9
+        out["1_decode_b1_ctx512"] = r
+        del w
+
+    if 2 in configs:
+        w = W.decode_batched(device=dev)
+        r = bench_decode(w, dev, args.steps, args.warmup, True, stream)
+        if not args.no_cpu:
+            s, reps = cpu_decode_baseline(w, args.cpu_budget)
+            r["cpu_GBps"] = w.kv_bytes() / s / 1e9
+            r["cpu_reps"] = reps
+        head = (w, r)
+        out["2_decode_b64_ctx128-4096"] = r
+
+    if 3 in configs:
+        w = W.prefill_prefix(device=dev)
+        ops = Ops(w, dev, stream)
+        ms, host_ms = time_loop(ops.prefill, args.steps, args.warmup, stream)
+        wr_ms, _ = time_loop(ops.write, args.steps, args.warmup, stream)
+        flops = W.prefill_flops(w)
+        r = {"ms_per_step": ms, "host_ms_per_step": host_ms, "write_ms": wr_ms, "flops": flops,
+             "TFLOPs": flops / (ms * 1e-3) / 1e12}
+        r["mfma_frac"] = r["TFLOPs"] * 1e12 / BF16_PEAK
+        if not args.no_cpu:
+            rng = np.random.default_rng(0)
+            pairs = np.stack([rng.integers(0, w.q.shape[0], 256), rng.integers(0, w.hq, 256)],
+                             1).astype(np.int32)
+            s, reps = cpu_prefill_baseline(w, pairs, 1.0)
+            r["cpu_TFLOPs"] = prefill_pair_flops(w, pairs) / s / 1e12
+            r["cpu_sample"] = "256 random (query row, q_head) pairs"
+        out["3_prefill_8x(512+1536)"] = r
+        del w, ops
+
+    if 4 in configs:
+        w = W.mixed_step(device=dev)
+        ops = Ops(w, dev, stream)
+        ms, host_ms = time_loop(ops.prefill, args.steps, args.warmup, stream)
+        flops = W.prefill_flops(w)
+        dbytes = W.decode_items_kv_bytes(w)
+        roof_s = dbytes / HBM_PEAK + flops / BF16_PEAK
+        r = {"ms_per_step": ms, "host_ms_per_step": host_ms, "decode_kv_bytes": dbytes,
+             "prefill_flops": flops, "roofline_ms": roof_s * 1e3,
+             "roofline_frac": roof_s / (ms * 1e-3)}
+        out["4_mixed_4x512+128dec"] = r
+        del w, ops
+
+    if 5 in configs:
+        w = W.decode_long(device=dev)
+        r = bench_decode(w, dev, max(5, args.steps // 2), args.warmup, False, stream)
+        if not args.no_cpu:
+            pairs = np.array([[0, h] for h in range(w.hq)], np.int32)
+            s, reps = cpu_decode_baseline(w, 1.0, pairs=pairs)
+            r["cpu_GBps"] = int(w.context_lens[0]) * w.hkv * w.d * 4 / s / 1e9
+            r["cpu_sample"] = "sequence 0, all 32 q-heads"
+        out["5_decode_b32_ctx32768_gqa4"] = r
+        del w
+
+    torch.cuda.synchronize()
+    return head, out, nt
+
+
+COPY_BYTES = 1 << 30
+
+
+def profile(op: str, iters: int) -> None:
+    """Runs one op `iters` times on its benchmark workload (for rocprofv3 runs)."""
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream(device=dev)
+    if op == "copy":  # calibration: a plain copy of known size (1 GiB read + 1 GiB written)
+        src = torch.ones(COPY_BYTES // 2, dtype=torch.bfloat16, device=dev)
+        dst = torch.empty_like(src)
+        fn = lambda: dst.copy_(src)  # noqa: E731
+    else:
+        w = {"decode": W.decode_batched, "write": W.decode_batched, "prefill": W.prefill_prefix,
+             "mixed": W.mixed_step, "long": W.decode_long}[op](device=dev)
+        ops = Ops(w, dev, stream)
+        fn = {"decode": ops.decode, "write": ops.write, "prefill": ops.prefill,
+              "mixed": ops.prefill, "long": ops.decode}[op]
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        for _ in range(iters):
+            fn()
+    torch.cuda.synchronize()
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--configs", default="1,2,3,4,5")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=5.0)
+    ap.add_argument("--profile-op", choices=["decode", "write", "prefill", "mixed", "long",
+                                             "copy"], default=None)
+    ap.add_argument("--profile-iters", type=int, default=5)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
+              "(the attention path shards by (sequence, kv_head) with no exchange, see "
+              "DESIGN.md).", file=sys.stderr)
+        sys.exit(2)
+    if args.profile_op:
+        profile(args.profile_op, args.profile_iters)
+        return
+    if 2 not in [int(c) for c in args.configs.split(",") if c]:
+        args.configs = "2," + args.configs
+    head, out, nt = run(args)
+    w, r = head
+    ms = r["ms_per_step"]
+    value = r["kv_GBps"]
+    dec_ms = r["decode_ms"]
+    traffic = traffic_from_profiles("decode_split_b64")
+    line = {
+        "metric": "paged-decode KV GB/s (% HBM peak) + paged-prefill TFLOPS (% bf16 MFMA peak)",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) bf16 Q/K/V, random block tables)",
+        "config": {"workload": "configs[1]: batched paged decode, batch 64, 16q/8kv heads, "
+                               "d=128, ctx U[128,4096], block 16, + KV write of 64 new tokens",
+                   "batch": w.batch, "num_q_heads": w.hq, "num_kv_heads": w.hkv,
+                   "head_dim": w.d, "block_size": 16, "sum_ctx": int(w.context_lens.sum()),
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": "decode (split-KV kernel + LSE merge)",
+                     "achieved": round(w.kv_bytes() / (dec_ms * 1e-3) / 1e9, 2),
+                     "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                     "frac": round(w.kv_bytes() / (dec_ms * 1e-3) / HBM_PEAK, 4),
+                     "traffic": traffic},
+        "cpu_baseline": None if "cpu_GBps" not in r else {
+            "value": round(r["cpu_GBps"], 3), "unit": "GB/s", "cores": nt, "kind": "port",
+            "sample": f"full configs[1] batch (all 1024 (seq, q_head) rows), {r['cpu_reps']} "
+                      f"repetition(s), oracle/attn_oracle.c over {nt} threads, {cpu_model()}"},
+        "configs": {k: {kk: (round(vv, 5) if isinstance(vv, float) else vv)
+                        for kk, vv in v.items()} for k, v in out.items()},
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

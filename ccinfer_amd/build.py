@@ -73,9 +73,23 @@ def build(verbose: bool = True) -> Path:
     if res.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
     os.replace(tmp, LIB)
+    _build_cpp_tests()
     if verbose:
         print(f"[ccinfer_amd] built {LIB}")
     return LIB
+
+
+CPP_TEST = BUILD / "test_dropin"
+
+
+def _build_cpp_tests() -> None:
+    """The C++ drop-in test program (tests/cpp/test_dropin.cpp), linked against the library."""
+    src = ROOT / "tests" / "cpp" / "test_dropin.cpp"
+    cmd = [HIPCC, *HIP_FLAGS, "-x", "hip", str(src), "-o", str(CPP_TEST), f"-L{LIBDIR}",
+           "-lccinfer_attn", f"-Wl,-rpath,{LIBDIR}", "-Wl,-rpath,$ORIGIN/../lib"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"test build failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
 
 
 def build_oracle(verbose: bool = True) -> Path:

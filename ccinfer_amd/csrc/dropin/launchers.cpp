@@ -69,6 +69,9 @@ Result<void> launch_prefill_attention(const __hip_bfloat16* q, const __hip_bfloa
                                       int total_query_tokens, int max_blocks_per_req,
                                       int num_q_heads, int num_kv_heads, int head_dim,
                                       int cache_block_size, hipStream_t stream) {
+    if (!q || !k_cache || !v_cache || !block_table || !query_start_loc || !context_lens ||
+        !output)
+        return unexpected(ErrorCode::InvalidArgument);
     const size_t need = ccinfer_prefill_workspace_size(batch_size, total_query_tokens,
                                                        max_blocks_per_req, num_q_heads,
                                                        num_kv_heads, head_dim, cache_block_size);
@@ -86,6 +89,8 @@ Result<void> launch_decode_attention(const __hip_bfloat16* q, const __hip_bfloat
                                      int batch_size, int max_blocks_per_req, int num_q_heads,
                                      int num_kv_heads, int head_dim, int cache_block_size,
                                      hipStream_t stream) {
+    if (!q || !k_cache || !v_cache || !block_table || !context_lens || !output)
+        return unexpected(ErrorCode::InvalidArgument);
     const size_t need = ccinfer_decode_workspace_size(batch_size, max_blocks_per_req,
                                                       num_q_heads, num_kv_heads, head_dim,
                                                       cache_block_size);

@@ -1,0 +1,128 @@
+"""The C-ABI library on the CPU: it loads, exports every symbol include/ccinfer_attn.h
+declares, and rejects invalid arguments before touching a device (the reference's
+DeviceBackend / launcher validation, src/backend/backend.h:172-223,
+src/kernel/attention/decode_attn.cu:488,568, prefill_attn.cu:257-259)."""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from ccinfer_amd import _lib
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "ccinfer_attn.h"
+INVALID = 6
+FAKE = 0x1000  # never dereferenced: every call below fails validation first
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ccinfer_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_exports_every_declared_symbol(lib):
+    names = declared_functions()
+    assert len(names) >= 7
+    for n in names:
+        assert hasattr(lib, n), n
+    nm = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
+                        text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (ccinfer_\w+)", nm))
+    assert set(names) <= exported
+    assert set(names) == set(_lib.SIGNATURES), "ctypes table out of sync with the header"
+
+
+def test_version_and_messages(lib):
+    assert lib.ccinfer_version().decode().count(".") == 2
+    assert lib.ccinfer_error_message(0) == b"ok"
+    assert lib.ccinfer_error_message(INVALID) == b"invalid argument"
+
+
+def test_write_kv_cache_validation(lib):
+    f = lib.ccinfer_write_kv_cache
+    assert f(None, FAKE, FAKE, FAKE, FAKE, 4, 2, 4, 64, None) == INVALID
+    assert f(FAKE, FAKE, FAKE, FAKE, None, 4, 2, 4, 64, None) == INVALID
+    for bad in [(0, 2, 4, 64), (4, 0, 4, 64), (4, 2, 0, 64), (4, 2, 4, 0), (-1, 2, 4, 64)]:
+        assert f(FAKE, FAKE, FAKE, FAKE, FAKE, *bad, None) == INVALID
+
+
+def _decode(lib, **kw):
+    a = dict(q=FAKE, k=FAKE, v=FAKE, bt=FAKE, ctx=FAKE, out=FAKE, b=2, mbpr=4, hq=8, hkv=2,
+             d=128, bs=16, ws=None, wsb=0)
+    a.update(kw)
+    return lib.ccinfer_decode_attention(a["q"], a["k"], a["v"], a["bt"], a["ctx"], a["out"],
+                                        a["b"], a["mbpr"], a["hq"], a["hkv"], a["d"], a["bs"],
+                                        a["ws"], a["wsb"], None)
+
+
+def test_decode_validation(lib):
+    for ptr in ["q", "k", "v", "bt", "ctx", "out"]:
+        assert _decode(lib, **{ptr: None}) == INVALID, ptr
+    for field in ["b", "mbpr", "hq", "hkv", "d", "bs"]:
+        assert _decode(lib, **{field: 0}) == INVALID, field
+    assert _decode(lib, hq=7) == INVALID              # Hq % Hkv != 0
+    assert _decode(lib, bs=32) == INVALID             # decode_attn.cu:488
+    assert _decode(lib, d=100) == INVALID             # decode_attn.cu:568
+    # split-KV needs a workspace for this shape; a missing one is rejected, not allocated
+    need = lib.ccinfer_decode_workspace_size(64, 256, 16, 8, 128, 16)
+    assert need > 0
+    assert _decode(lib, b=64, mbpr=256, hq=16, hkv=8, ws=None, wsb=0) == INVALID
+    assert _decode(lib, b=64, mbpr=256, hq=16, hkv=8, ws=FAKE, wsb=need - 1) == INVALID
+
+
+def test_decode_workspace_size(lib):
+    f = lib.ccinfer_decode_workspace_size
+    assert f(0, 4, 8, 2, 128, 16) == 0            # invalid shape -> 0
+    assert f(1, 1, 8, 2, 128, 16) == 0            # one 16-token block: single split, no scratch
+    n = f(32, 2048, 32, 8, 128, 16)
+    assert n > 0 and n % (32 * 32 * 130 * 4) == 0  # B * Hq * splits * (D + 2) floats
+    assert f(32, 2048, 32, 8, 80, 16) == 0        # generic head_dim path uses no scratch
+
+
+def _prefill(lib, **kw):
+    a = dict(q=FAKE, k=FAKE, v=FAKE, bt=FAKE, qsl=FAKE, ctx=FAKE, out=FAKE, b=2, t=64, mbpr=8,
+             hq=16, hkv=8, d=128, bs=16, ws=None, wsb=0)
+    a.update(kw)
+    return lib.ccinfer_prefill_attention(a["q"], a["k"], a["v"], a["bt"], a["qsl"], a["ctx"],
+                                         a["out"], a["b"], a["t"], a["mbpr"], a["hq"], a["hkv"],
+                                         a["d"], a["bs"], a["ws"], a["wsb"], None)
+
+
+def test_prefill_validation(lib):
+    for ptr in ["q", "k", "v", "bt", "qsl", "ctx", "out"]:
+        assert _prefill(lib, **{ptr: None}) == INVALID, ptr
+    for field in ["b", "t", "mbpr", "hq", "hkv", "d", "bs"]:
+        assert _prefill(lib, **{field: 0}) == INVALID, field
+    assert _prefill(lib, hq=12) == INVALID             # 12 % 8 != 0
+    assert _prefill(lib, d=264) == INVALID             # prefill_attn.cu:257-259
+    need = lib.ccinfer_prefill_workspace_size(2, 64, 8, 16, 8, 128, 16)
+    assert need > 0
+    assert _prefill(lib) == INVALID                     # workspace missing
+    assert _prefill(lib, ws=FAKE, wsb=need - 1) == INVALID
+
+
+def test_error_code_values_match_reference_enum():
+    """The C ABI returns the reference's ErrorCode numbering (src/base/error_code.h:8-45)."""
+    text = (ROOT / "ccinfer_amd" / "csrc" / "dropin" / "base" / "error_code.h").read_text()
+    body = text[text.index("enum class ErrorCode"):]
+    body = body[body.index("{") + 1:body.index("};")]
+    names = [n.strip().split("=")[0].strip() for n in body.split(",") if n.strip()]
+    hdr = HEADER.read_text()
+    for code, ename in [("CCINFER_ERR_DEVICE_OUT_OF_MEMORY", "CudaOutOfMemory"),
+                        ("CCINFER_ERR_LAUNCH_FAILED", "CudaLaunchFailed"),
+                        ("CCINFER_ERR_DEVICE_INVALID_VALUE", "CudaInvalidValue"),
+                        ("CCINFER_ERR_DEVICE_RUNTIME", "CudaRuntimeError"),
+                        ("CCINFER_ERR_INVALID_ARGUMENT", "InvalidArgument"),
+                        ("CCINFER_ERR_UNSUPPORTED", "Unsupported"),
+                        ("CCINFER_ERR_INTERNAL", "InternalError")]:
+        val = int(re.search(rf"{code}\s*=\s*(\d+)", hdr).group(1))
+        assert names.index(ename) == val, (code, ename)
+    assert ctypes.sizeof(ctypes.c_size_t) == 8
