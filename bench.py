@@ -54,7 +54,7 @@ class Ops:
             n = self.lib.ccinfer_prefill_workspace_size(w.batch, w.q.shape[0], w.mbpr, w.hq,
                                                         w.hkv, w.d, 16)
         self.ws_bytes = int(n)
-        self.ws = torch.empty(max(1, self.ws_bytes), dtype=torch.uint8, device=dev)
+        self.ws = torch.zeros(max(1, self.ws_bytes), dtype=torch.uint8, device=dev)
 
     def write(self):
         w = self.w

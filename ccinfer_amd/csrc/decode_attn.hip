@@ -7,8 +7,9 @@
 //
 // Work decomposition (one wavefront = one work item):
 //   item = (query row, kv_head, split). A split covers `split_tokens` consecutive context
-//   positions (a multiple of 32). All Hq/Hkv query heads of the GQA group are handled by the
-//   same wavefront, so every K/V byte of a (request, kv_head) is read from HBM exactly once.
+//   positions (a multiple of 32, at most 2048). All Hq/Hkv query heads of the GQA group are
+//   handled by the same wavefront, so every K/V byte of a (request, kv_head) is read from
+//   HBM exactly once.
 //
 // Per 32-token chunk (two 16-token cache blocks) the wavefront computes
 //   S^T[token][head] = K[token][:] . Q^T           (v_mfma_f32_16x16x32_bf16, D/32 steps/block)
@@ -23,9 +24,17 @@
 // transposes in registers with v_perm_b32. O^T lands with every accumulator of a lane
 // belonging to one head, so the online-softmax rescale is lane-local.
 //
-// Partial results (unnormalised O, running max m, sum l) go to a workspace and a second
-// kernel merges the splits with a log-sum-exp weighting. With a single split the first
-// kernel writes the output directly.
+// Memory pipeline: chunks are double-buffered in registers with a branch-free prefetch (the
+// chunk index is clamped instead of skipping the load) so the compiler's wait counts only
+// ever wait for the chunk being consumed. The split's block-table entries are loaded once
+// into lanes and broadcast with readlane, so no scalar load sits between two chunks.
+//
+// Split merge: each split writes (unnormalised O, running max m, sum l) to the workspace and
+// a second kernel merges the splits of every row with a log-sum-exp weighting (the kernel
+// boundary orders the partial writes before the merge reads; an in-kernel last-arrival merge
+// would need agent-scope release/acquire fences, which on gfx950 write back and invalidate
+// the whole L2 and cost far more than the extra launch). A row whose context fits one split
+// is written directly by the first kernel and skipped by the merge.
 #include "attn_common.hpp"
 #include "kernels.hpp"
 
@@ -35,6 +44,9 @@ namespace {
 constexpr int kBlock = 16;        // tokens per KV block (the reference's kKVBlockSize)
 constexpr int kChunk = 32;        // tokens per PV MFMA
 constexpr int kWavesPerGroup = 4;
+constexpr int kMaxSplitTokens = 2048;  // 128 blocks: two table entries per lane
+// Wavefronts the split plan aims for: two resident per SIMD on 1024 SIMDs, two rounds.
+constexpr int64_t kTargetWaves = 4096;
 
 struct ItemArgs {
     int num_items;
@@ -124,22 +136,135 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<D>& c, const __bf16* __rest
     }
 }
 
+// Online-softmax state of one wavefront: lane (head j, grp g) holds O[j][NV*(4g+r)+n] in
+// acc[n][r], the running max m (base-2 domain, per head, replicated over the 4 grp lanes)
+// and a per-lane partial sum l.
 template <int D>
-__global__ __launch_bounds__(256) void decode_split_kernel(
+struct SoftmaxState {
+    f32x4 acc[DecodeShape<D>::kNV];
+    float m;
+    float l;
+};
+
+template <int D>
+__device__ __forceinline__ void consume_chunk(SoftmaxState<D>& st, ChunkRegs<D>& c,
+                                              const bf16x8 (&qop)[DecodeShape<D>::kSteps],
+                                              int cb, int end, int pb0, int pb1,
+                                              float scale_log2, int g) {
+    constexpr int S = DecodeShape<D>::kSteps;
+    constexpr int NV = DecodeShape<D>::kNV;
+    float sc[8];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+        f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < S; ++kk)
+            s4 = mfma16x16x32(__builtin_bit_cast(bf16x8, c.k[kb][kk]), qop[kk], s4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sc[kb * 4 + r] = s4[r] * scale_log2;
+    }
+    // Masking (context end, negative block ids) is branch-free: the selects are cheap in
+    // this memory-bound loop, and a wave-uniform branch around them would merge every V
+    // register through a phi (which the gfx950 backend of this toolchain has been seen to
+    // miscompile). Masked V rows are zeroed so NaN/Inf garbage in unwritten slots cannot
+    // reach the PV product.
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int kb = e >> 2;
+        const int pos = cb + kb * kBlock + g * 4 + (e & 3);
+        const bool ok = pos < end && (kb == 0 ? pb0 : pb1) >= 0;
+        sc[e] = ok ? sc[e] : kNegInf;
+#pragma unroll
+        for (int x = 0; x < DecodeShape<D>::kVWords; ++x) c.v[e][x] = ok ? c.v[e][x] : 0u;
+    }
+    float mloc = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])),
+                       fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+    mloc = wave_max_xor16_32(mloc);
+    const float m_new = fmaxf(st.m, mloc);
+    const float m_use = (m_new == kNegInf) ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(st.m - m_use);
+    float p[8];
+    float psum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        p[e] = __builtin_amdgcn_exp2f(sc[e] - m_use);
+        psum += p[e];
+    }
+    st.l = st.l * alpha + psum;
+    st.m = m_new;
+    u32x4 pw;
+#pragma unroll
+    for (int x = 0; x < 4; ++x) pw[x] = pack_bf16x2(p[2 * x], p[2 * x + 1]);
+    const bf16x8 pop = __builtin_bit_cast(bf16x8, pw);
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+        u32x4 vw;
+#pragma unroll
+        for (int x = 0; x < 4; ++x)
+            vw[x] = pick_halves(c.v[2 * x][n >> 1], c.v[2 * x + 1][n >> 1], n & 1);
+        st.acc[n] = st.acc[n] * alpha;
+        st.acc[n] = mfma16x16x32(__builtin_bit_cast(bf16x8, vw), pop, st.acc[n]);
+    }
+}
+
+// Log-sum-exp merge of the ns splits of one (item, head) row by one wavefront; writes bf16.
+// Split weights are computed 64 at a time, one split per lane, and broadcast with readlane;
+// every lane then accumulates its D/64 dims over the splits (independent loads).
+template <int D>
+__device__ void merge_row(const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
+                          int64_t base, int ns, float eps, __bf16* __restrict__ o, int lane) {
+    constexpr int kPer = D / 64;
+    float mmax = kNegInf;
+    for (int s = lane; s < ns; s += 64) mmax = fmaxf(mmax, ws_ml[(base + s) * 2]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, off));
+    float acc[kPer];
+#pragma unroll
+    for (int x = 0; x < kPer; ++x) acc[x] = 0.f;
+    float lsum = 0.f;
+    if (mmax != kNegInf) {
+        for (int sb = 0; sb < ns; sb += 64) {
+            const int s = sb + lane;
+            float w = 0.f;
+            if (s < ns) {
+                w = __builtin_amdgcn_exp2f(ws_ml[(base + s) * 2] - mmax);
+                lsum += ws_ml[(base + s) * 2 + 1] * w;
+            }
+            const int nt = min(64, ns - sb);
+            const float* po = ws_o + (base + sb) * D + lane * kPer;
+            for (int t = 0; t < nt; ++t) {
+                const float wt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), t));
+#pragma unroll
+                for (int x = 0; x < kPer; ++x) acc[x] += po[t * D + x] * wt;
+            }
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) lsum += __shfl_xor(lsum, off);
+    const float inv = lsum > 0.f ? 1.f / (lsum + eps) : 0.f;
+#pragma unroll
+    for (int x = 0; x < kPer; ++x) o[lane * kPer + x] = static_cast<__bf16>(acc[x] * inv);
+}
+
+template <int D>
+__global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k_cache,
     const __bf16* __restrict__ v_cache, const int32_t* __restrict__ block_table,
     const int32_t* __restrict__ context_lens, __bf16* __restrict__ out, float* __restrict__ ws_o,
     float* __restrict__ ws_ml, ItemArgs items, int mbpr, int hq, int hkv, int splits,
-    int split_tokens, float scale_log2, int direct_out) {
+    int split_tokens, float scale_log2) {
     constexpr int S = DecodeShape<D>::kSteps;
     constexpr int NV = DecodeShape<D>::kNV;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wi = blockIdx.x * kWavesPerGroup + wave;
-    const int s = wi % splits;
-    const int rest = wi / splits;
-    const int h = rest % hkv;
-    const int item = rest / hkv;
+    // kv_head fastest: the Hkv wavefronts of one (item, split) run side by side and read
+    // interleaved 256-byte pieces of the same cache blocks (the layout puts the heads of a
+    // slot next to each other), which measured 10-20% faster than split-fastest ordering.
+    const int h = wi % hkv;
+    const int rest = wi / hkv;
+    const int s = rest % splits;
+    const int item = rest / splits;
 
     int req, qrow;
     if (!resolve_item(items, item, &req, &qrow)) return;
@@ -150,16 +275,27 @@ __global__ __launch_bounds__(256) void decode_split_kernel(
 
     if (ctx < 0) {
         // Decode semantics: invalid context -> zeros (written once, by split 0).
-        if (direct_out && items.zero_invalid && s == 0 && j < G && g == 0) {
-            __bf16* o = out + (static_cast<int64_t>(qrow) * hq + h * G + j) * D;
-            for (int d = 0; d < D; ++d) o[d] = static_cast<__bf16>(0.0f);
+        if (items.zero_invalid && s == 0) {
+            for (int x = lane; x < G * D; x += 64) {
+                out[(static_cast<int64_t>(qrow) * hq + h * G) * D + x] = static_cast<__bf16>(0.0f);
+            }
         }
         return;
     }
     const int begin = s * split_tokens;
     if (begin >= ctx) return;
     const int end = min(ctx, begin + split_tokens);
+    const int ns = (ctx + split_tokens - 1) / split_tokens;  // splits with work for this row
     const int32_t* req_blocks = block_table + static_cast<int64_t>(req) * mbpr;
+
+    // Block ids of this split, one per lane (two registers cover 128 blocks).
+    const int lb0 = begin / kBlock;
+    const int nblk = (end - begin + kBlock - 1) / kBlock;
+    const int bt_lo = (lane < nblk && lb0 + lane < mbpr) ? req_blocks[lb0 + lane] : -1;
+    const int bt_hi = (lane + 64 < nblk && lb0 + lane + 64 < mbpr) ? req_blocks[lb0 + lane + 64] : -1;
+    auto block_id = [&](int jb) -> int {  // jb: wave-uniform block index within the split
+        return __builtin_amdgcn_readlane(jb < 64 ? bt_lo : bt_hi, jb & 63);
+    };
 
     // Q^T operand: lane (head j, grp g) holds dims (kk*4+g)*8 .. +8 of head j.
     bf16x8 qop[S];
@@ -174,102 +310,38 @@ __global__ __launch_bounds__(256) void decode_split_kernel(
         }
     }
 
-    f32x4 acc[NV];
+    SoftmaxState<D> st;
 #pragma unroll
-    for (int n = 0; n < NV; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m = kNegInf;
-    float l = 0.f;
+    for (int n = 0; n < NV; ++n) st.acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    st.m = kNegInf;
+    st.l = 0.f;
 
-    auto table = [&](int lb) -> int { return lb < mbpr ? req_blocks[lb] : -1; };
-
-    int cb = begin;
-    int pb0 = table(cb / kBlock);
-    int pb1 = (cb + kBlock < end) ? table(cb / kBlock + 1) : -1;
-    ChunkRegs<D> cur;
-    load_chunk<D>(cur, k_cache, v_cache, pb0, pb1, h, hkv, lane);
-
-    for (; cb < end; cb += kChunk) {
-        // Prefetch the next chunk while this one is consumed.
-        const int nb = cb + kChunk;
-        int npb0 = -1, npb1 = -1;
-        ChunkRegs<D> nxt;
-        if (nb < end) {
-            npb0 = table(nb / kBlock);
-            npb1 = (nb + kBlock < end) ? table(nb / kBlock + 1) : -1;
-            load_chunk<D>(nxt, k_cache, v_cache, npb0, npb1, h, hkv, lane);
-        }
-
-        // S^T = K . Q^T for the two 16-token blocks.
-        float sc[8];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            f32x4 st = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int kk = 0; kk < S; ++kk)
-                st = mfma16x16x32(__builtin_bit_cast(bf16x8, cur.k[kb][kk]), qop[kk], st);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) sc[kb * 4 + r] = st[r] * scale_log2;
-        }
-
-        const bool full = (cb + kChunk <= end) && pb0 >= 0 && pb1 >= 0;
-        if (!full) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int kb = e >> 2;
-                const int pos = cb + kb * kBlock + g * 4 + (e & 3);
-                const bool ok = pos < end && (kb == 0 ? pb0 : pb1) >= 0;
-                if (!ok) {
-                    sc[e] = kNegInf;
-#pragma unroll
-                    for (int x = 0; x < DecodeShape<D>::kVWords; ++x) cur.v[e][x] = 0u;
-                }
-            }
-        }
-
-        // Online softmax (base-2 domain); rows of a head live in lanes j, j+16, j+32, j+48.
-        float mloc = sc[0];
-#pragma unroll
-        for (int e = 1; e < 8; ++e) mloc = fmaxf(mloc, sc[e]);
-        mloc = wave_max_xor16_32(mloc);
-        const float m_new = fmaxf(m, mloc);
-        const float m_use = (m_new == kNegInf) ? 0.f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m - m_use);
-        float p[8];
-        float psum = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            p[e] = __builtin_amdgcn_exp2f(sc[e] - m_use);
-            psum += p[e];
-        }
-        l = l * alpha + psum;
-        m = m_new;
-        u32x4 pw;
-#pragma unroll
-        for (int x = 0; x < 4; ++x) pw[x] = pack_bf16x2(p[2 * x], p[2 * x + 1]);
-        const bf16x8 pop = __builtin_bit_cast(bf16x8, pw);
-
-#pragma unroll
-        for (int n = 0; n < NV; ++n) {
-            u32x4 vw;
-#pragma unroll
-            for (int x = 0; x < 4; ++x)
-                vw[x] = pick_halves(cur.v[2 * x][n >> 1], cur.v[2 * x + 1][n >> 1], n & 1);
-            acc[n] = acc[n] * alpha;
-            acc[n] = mfma16x16x32(__builtin_bit_cast(bf16x8, vw), pop, acc[n]);
-        }
-
-        if (nb < end) {
-            cur = nxt;
-            pb0 = npb0;
-            pb1 = npb1;
-        }
+    const int nchunks = (end - begin + kChunk - 1) / kChunk;
+    // Block ids of chunk c (clamped to the last chunk so prefetches are unconditional).
+    auto chunk_blocks = [&](int c, int* p0, int* p1) {
+        c = c < nchunks ? c : nchunks - 1;
+        *p0 = block_id(2 * c);
+        *p1 = (2 * c + 1 < nblk) ? block_id(2 * c + 1) : -1;
+    };
+    ChunkRegs<D> ra, rb;
+    int a0, a1, b0, b1;
+    chunk_blocks(0, &a0, &a1);
+    load_chunk<D>(ra, k_cache, v_cache, a0, a1, h, hkv, lane);
+    for (int c = 0; c < nchunks; c += 2) {
+        chunk_blocks(c + 1, &b0, &b1);
+        load_chunk<D>(rb, k_cache, v_cache, b0, b1, h, hkv, lane);
+        consume_chunk<D>(st, ra, qop, begin + c * kChunk, end, a0, a1, scale_log2, g);
+        if (c + 1 >= nchunks) break;
+        chunk_blocks(c + 2, &a0, &a1);
+        load_chunk<D>(ra, k_cache, v_cache, a0, a1, h, hkv, lane);
+        consume_chunk<D>(st, rb, qop, begin + (c + 1) * kChunk, end, b0, b1, scale_log2, g);
     }
 
-    const float l_tot = wave_sum_xor16_32(l);
-    if (j >= G) return;
+    const float l_tot = wave_sum_xor16_32(st.l);
+    const bool live = j < G;
     const int head = h * G + j;
-    // Lane (j, g) holds O[head][NV*(4g+r) + n] = acc[n][r].
-    if (direct_out) {
+    if (ns == 1) {
+        if (!live) return;
         const float inv = l_tot > 0.f ? 1.f / (l_tot + items.eps) : 0.f;
         __bf16* o = out + (static_cast<int64_t>(qrow) * hq + head) * D;
 #pragma unroll
@@ -277,27 +349,40 @@ __global__ __launch_bounds__(256) void decode_split_kernel(
             uint32_t w[NV / 2];
 #pragma unroll
             for (int x = 0; x < NV / 2; ++x)
-                w[x] = pack_bf16x2(acc[2 * x][r] * inv, acc[2 * x + 1][r] * inv);
+                w[x] = pack_bf16x2(st.acc[2 * x][r] * inv, st.acc[2 * x + 1][r] * inv);
             uint32_t* dst = reinterpret_cast<uint32_t*>(o + NV * (4 * g + r));
 #pragma unroll
             for (int x = 0; x < NV / 2; ++x) dst[x] = w[x];
         }
-    } else {
-        const int64_t slot = (static_cast<int64_t>(item) * hq + head) * splits + s;
-        float* po = ws_o + slot * D;
+        return;
+    }
+
+    // Partial of this split; decode_merge_kernel combines the splits.
+    if (!live) return;
+    const int64_t slot = (static_cast<int64_t>(item) * hq + head) * splits + s;
+    float* po = ws_o + slot * D;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < 4; ++r) {
+        if constexpr (NV == 4) {
+            *reinterpret_cast<f32x4*>(po + NV * (4 * g + r)) =
+                f32x4{st.acc[0][r], st.acc[1][r], st.acc[2][r], st.acc[3][r]};
+        } else if constexpr (NV == 8) {
+            *reinterpret_cast<f32x4*>(po + NV * (4 * g + r)) =
+                f32x4{st.acc[0][r], st.acc[1][r], st.acc[2][r], st.acc[3][r]};
+            *reinterpret_cast<f32x4*>(po + NV * (4 * g + r) + 4) =
+                f32x4{st.acc[4][r], st.acc[5][r], st.acc[6][r], st.acc[7][r]};
+        } else {
 #pragma unroll
-            for (int n = 0; n < NV; ++n) po[NV * (4 * g + r) + n] = acc[n][r];
+            for (int n = 0; n < NV; ++n) po[NV * (4 * g + r) + n] = st.acc[n][r];
         }
-        if (g == 0) {
-            ws_ml[slot * 2 + 0] = m;
-            ws_ml[slot * 2 + 1] = l_tot;
-        }
+    }
+    if (g == 0) {
+        ws_ml[slot * 2 + 0] = st.m;
+        ws_ml[slot * 2 + 1] = l_tot;
     }
 }
 
-// One wavefront per (item, q_head): log-sum-exp merge of the valid splits.
+// One wavefront per (item, q_head) row with more than one split: log-sum-exp merge.
 template <int D>
 __global__ __launch_bounds__(256) void decode_merge_kernel(
     const int32_t* __restrict__ context_lens, __bf16* __restrict__ out,
@@ -311,38 +396,28 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(
     int req, qrow;
     if (!resolve_item(items, item, &req, &qrow)) return;
     const int ctx = effective_ctx(context_lens[req], mbpr, items.zero_invalid);
-    constexpr int kPer = D / 64;
-    __bf16* o = out + (static_cast<int64_t>(qrow) * hq + head) * D;
-    if (ctx < 0) {
-        if (items.zero_invalid) {
-#pragma unroll
-            for (int x = 0; x < kPer; ++x) o[lane * kPer + x] = static_cast<__bf16>(0.0f);
-        }
-        return;
-    }
+    if (ctx < 0) return;  // zeros already written (decode) / row untouched (prefill)
     const int ns = (ctx + split_tokens - 1) / split_tokens;
-    const int64_t base = (static_cast<int64_t>(item) * hq + head) * splits;
-    float mmax = kNegInf;
-    for (int s = lane; s < ns; s += 64) mmax = fmaxf(mmax, ws_ml[(base + s) * 2]);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, off));
-    float acc[kPer];
-#pragma unroll
-    for (int x = 0; x < kPer; ++x) acc[x] = 0.f;
-    float lsum = 0.f;
-    if (mmax != kNegInf) {
-        for (int s = 0; s < ns; ++s) {
-            const float ms = ws_ml[(base + s) * 2];
-            const float w = __builtin_amdgcn_exp2f(ms - mmax);
-            lsum += ws_ml[(base + s) * 2 + 1] * w;
-            const float* po = ws_o + (base + s) * D + lane * kPer;
-#pragma unroll
-            for (int x = 0; x < kPer; ++x) acc[x] += po[x] * w;
-        }
-    }
-    const float inv = lsum > 0.f ? 1.f / (lsum + items.eps) : 0.f;
-#pragma unroll
-    for (int x = 0; x < kPer; ++x) o[lane * kPer + x] = static_cast<__bf16>(acc[x] * inv);
+    if (ns <= 1) return;  // written directly by the split kernel
+    merge_row<D>(ws_o, ws_ml, (static_cast<int64_t>(item) * hq + head) * splits, ns, items.eps,
+                 out + (static_cast<int64_t>(qrow) * hq + head) * D, lane);
+}
+
+struct DecodeWs {
+    float* o;
+    float* ml;
+};
+
+DecodeWs carve(void* workspace, int num_items, int hq, int hkv, int d, int splits) {
+    DecodeWs w{};
+    char* p = static_cast<char*>(workspace);
+    const size_t o_bytes = static_cast<size_t>(num_items) * hq * splits * d * sizeof(float);
+    const size_t ml_bytes = static_cast<size_t>(num_items) * hq * splits * 2 * sizeof(float);
+    w.o = reinterpret_cast<float*>(p);
+    w.ml = reinterpret_cast<float*>(p + o_bytes);
+    (void)ml_bytes;
+    (void)hkv;
+    return w;
 }
 
 template <int D>
@@ -353,22 +428,19 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
     const float scale_log2 = kLog2e / sqrtf(static_cast<float>(D));
     const int64_t waves = static_cast<int64_t>(it.num_items) * hkv * plan.splits;
     const int grid = static_cast<int>((waves + kWavesPerGroup - 1) / kWavesPerGroup);
-    const bool direct = plan.splits == 1;
-    float* ws_o = static_cast<float*>(workspace);
-    float* ws_ml = direct ? nullptr
-                          : ws_o + static_cast<int64_t>(it.num_items) * hq * plan.splits * D;
+    DecodeWs w{};
+    if (plan.splits > 1) w = carve(workspace, it.num_items, hq, hkv, D, plan.splits);
     decode_split_kernel<D><<<grid, 256, 0, stream>>>(
         static_cast<const __bf16*>(q), static_cast<const __bf16*>(k_cache),
         static_cast<const __bf16*>(v_cache), block_table, context_lens,
-        static_cast<__bf16*>(output), ws_o, ws_ml, it, mbpr, hq, hkv, plan.splits,
-        plan.split_tokens, scale_log2, direct ? 1 : 0);
+        static_cast<__bf16*>(output), w.o, w.ml, it, mbpr, hq, hkv, plan.splits,
+        plan.split_tokens, scale_log2);
     hipError_t err = hipGetLastError();
-    if (err != hipSuccess || direct) return err;
-    const int64_t mw = static_cast<int64_t>(it.num_items) * hq;
-    const int mgrid = static_cast<int>((mw + kWavesPerGroup - 1) / kWavesPerGroup);
-    decode_merge_kernel<D><<<mgrid, 256, 0, stream>>>(context_lens,
-                                                      static_cast<__bf16*>(output), ws_o, ws_ml,
-                                                      it, mbpr, hq, plan.splits,
+    if (err != hipSuccess || plan.splits == 1) return err;
+    const int64_t rows = static_cast<int64_t>(it.num_items) * hq;
+    const int mgrid = static_cast<int>((rows + kWavesPerGroup - 1) / kWavesPerGroup);
+    decode_merge_kernel<D><<<mgrid, 256, 0, stream>>>(context_lens, static_cast<__bf16*>(output),
+                                                      w.o, w.ml, it, mbpr, hq, plan.splits,
                                                       plan.split_tokens);
     return hipGetLastError();
 }
@@ -378,11 +450,11 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
 DecodePlan plan_decode(int num_items, int num_kv_heads, int max_ctx) {
     DecodePlan p;
     const int chunks = max_ctx > 0 ? (max_ctx + kChunk - 1) / kChunk : 1;
-    // Aim for ~16 wavefronts per CU (256 CUs) of work so ragged batches still balance.
-    const int64_t target_waves = 4096;
+    const int64_t target_waves = kTargetWaves;
     const int64_t total = static_cast<int64_t>(num_items) * num_kv_heads * chunks;
     int64_t cpw = (total + target_waves - 1) / target_waves;
     if (cpw < 1) cpw = 1;
+    if (cpw > kMaxSplitTokens / kChunk) cpw = kMaxSplitTokens / kChunk;
     if (cpw > chunks) cpw = chunks;
     p.split_tokens = static_cast<int>(cpw) * kChunk;
     p.splits = (chunks + static_cast<int>(cpw) - 1) / static_cast<int>(cpw);
@@ -392,8 +464,8 @@ DecodePlan plan_decode(int num_items, int num_kv_heads, int max_ctx) {
 size_t decode_workspace_bytes(int num_items, int num_q_heads, int head_dim,
                               const DecodePlan& plan) {
     if (plan.splits <= 1) return 0;
-    return static_cast<size_t>(num_items) * num_q_heads * plan.splits * (head_dim + 2) *
-           sizeof(float);
+    const size_t rows = static_cast<size_t>(num_items) * num_q_heads * plan.splits;
+    return rows * (head_dim + 2) * sizeof(float);  // partial O + (m, l) per row and split
 }
 
 bool decode_fast_supported(int num_q_heads, int num_kv_heads, int head_dim, int block_size) {

@@ -1,8 +1,7 @@
 // The reference-signature launchers (kernel/hip_kernels.h) on top of the C ABI.
 //
 // The reference launchers take no workspace argument, so the split-KV partials / prefill
-// work list come from a buffer kept per (device, stream): allocated on first use, grown
-// when a larger shape arrives (after synchronising that stream, since queued kernels may
+// work list come from a buffer kept per (device, stream): allocated on first use, grown when a larger shape arrives (after synchronising that stream, since queued kernels may
 // still read the old buffer), reused otherwise. A mutex guards the map only; launches on
 // different streams use different buffers, so the launchers stay re-entrant.
 #include <hip/hip_runtime.h>

@@ -14,7 +14,7 @@ Tensors are device tensors (torch on ROCm: "cuda" is the HIP device). Layouts:
   context_lens         [batch] int32; query_start_loc [batch + 1] int32
   slot_mapping         [total_tokens] int32
 Work is enqueued on torch's current stream; workspaces come from torch's caching
-allocator unless passed in.
+allocator unless passed in (scratch: no initialisation needed).
 """
 from __future__ import annotations
 
@@ -107,7 +107,7 @@ def _workspace(nbytes: int, device, workspace: Optional[torch.Tensor]):
         _require(workspace.is_cuda and workspace.numel() * workspace.element_size() >= nbytes,
                  "workspace")
         return workspace, workspace.numel() * workspace.element_size()
-    return torch.empty(nbytes, dtype=torch.uint8, device=device), nbytes
+    return torch.zeros(nbytes, dtype=torch.uint8, device=device), nbytes
 
 
 def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,

@@ -12,7 +12,8 @@
  * `stream`: no host synchronisation and no device allocation. Split-KV partials and the
  * prefill work list live in a caller-provided workspace sized by the *_workspace_size
  * queries (the reference launchers take no workspace; the C++ drop-in wrappers in
- * ccinfer_amd/csrc/dropin supply one owned per stream).
+ * ccinfer_amd/csrc/dropin supply one owned per stream). Workspace contents need no
+ * initialisation and are scratch between calls.
  *
  * Return value: 0 on success, otherwise the numeric value of the reference's
  * ccinfer::ErrorCode (src/base/error_code.h:8-45) -- the same codes the reference returns

@@ -165,3 +165,22 @@ def test_rejects_bad_arguments(gpu):
     q7 = torch.zeros((2, 7, 64), dtype=torch.bfloat16, device=gpu)  # 7 % 2 != 0
     with pytest.raises(CcinferError):
         decode_attention(q7, w.k_cache, w.v_cache, meta["block_table"], meta["context_lens"])
+
+
+def test_workspace_reuse_across_shapes(gpu):
+    """One workspace (deliberately filled with garbage first) reused across calls with
+    different contexts: the split-KV scratch needs no initialisation."""
+    say("decode workspace reuse")
+    from ccinfer_amd import decode_workspace_size
+    w = W.decode_long(device=gpu, seed=31, batch=6, ctx=3000, hq=16, hkv=8)
+    need = decode_workspace_size(w.batch, w.mbpr, w.hq, w.hkv, w.d)
+    assert need > 0
+    ws = torch.full((need,), 0x7f, dtype=torch.uint8, device=gpu)
+    rng = np.random.default_rng(2)
+    for it in range(4):
+        w.context_lens = rng.integers(1, 3001, w.batch).astype(np.int32)
+        meta = w.device_meta(gpu)
+        out = decode_attention(w.q, w.k_cache, w.v_cache, meta["block_table"],
+                               meta["context_lens"], workspace=ws)
+        torch.cuda.synchronize()
+        assert_attn_close(f32(out), oracle_decode(w), f"reuse {it}")
