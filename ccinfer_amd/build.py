@@ -29,6 +29,9 @@ HIP_FLAGS = [
     "-fPIC",
     "-Wall",
     "-Wno-unused-command-line-argument",
+    # Kernels mask with -inf and never rely on NaN semantics; this drops the NaN
+    # canonicalisation fmaxf would otherwise emit in the softmax max reductions.
+    "-fno-honor-nans",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{ROOT / 'include'}",
     f"-I{CSRC}",

@@ -31,13 +31,15 @@ namespace ccinfer::hipk {
 namespace {
 
 constexpr int kKeysPerTile = 64;
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;     // tile kernel: 8 wavefronts, 2 per SIMD
+constexpr int kWaves = kThreads / 64;
+constexpr int kBlock = 16;        // cache block size of the fast path
 constexpr int kBuckets = 1024;
 constexpr int kMaxPlanRequests = 4096;
 
 template <int D>
 struct PrefillShape {
-    static constexpr int kQT = D <= 128 ? 4 : 2;     // 16-row query tiles per wavefront
+    static constexpr int kQT = D <= 128 ? 2 : 1;     // 16-row query tiles per wavefront
     static constexpr int kQW = 16 * kQT;             // query rows per wavefront
     static constexpr int kSteps = D / 32;            // QK k-steps
     static constexpr int kNV = D / 16;               // PV MFMAs per query tile
@@ -46,7 +48,7 @@ struct PrefillShape {
     static constexpr int kLoadsPerThread = kKeysPerTile * kCPR / kThreads;  // per K or V
 };
 
-// Heads per workgroup: 4 wavefronts split as HPW heads x (4/HPW) row groups.
+// Heads per workgroup: the 8 wavefronts split as HPW heads x (8/HPW) row groups.
 __host__ __device__ inline int heads_per_wg(int G) {
     return (G % 4 == 0) ? 4 : ((G % 2 == 0) ? 2 : 1);
 }
@@ -191,8 +193,7 @@ template <int D>
 __device__ __forceinline__ void stage_load(StageRegs<D>& st, const __bf16* __restrict__ k_cache,
                                            const __bf16* __restrict__ v_cache,
                                            const int32_t* __restrict__ req_blocks, int key_base,
-                                           int ctx, int mbpr, int block_size, int kv_head,
-                                           int hkv) {
+                                           int ctx, int mbpr, int kv_head, int hkv) {
     constexpr int CPR = PrefillShape<D>::kCPR;
 #pragma unroll
     for (int x = 0; x < PrefillShape<D>::kLoadsPerThread; ++x) {
@@ -200,10 +201,13 @@ __device__ __forceinline__ void stage_load(StageRegs<D>& st, const __bf16* __res
         const int row = linear / CPR;
         const int chunk = linear % CPR;
         const int key = key_base + row;
-        int64_t base = -1;
-        if (key < ctx) base = kv_row_offset(key, kv_head, D, hkv, block_size, mbpr, req_blocks);
-        st.valid[x] = base >= 0;
-        if (base >= 0) {
+        const int lb = key >> 4;  // 16-token blocks (the fast path's contract)
+        int pb = -1;
+        if (key < ctx && lb < mbpr) pb = req_blocks[lb];
+        st.valid[x] = pb >= 0;
+        if (pb >= 0) {
+            const int64_t base =
+                ((static_cast<int64_t>(pb) * kBlock + (key & (kBlock - 1))) * hkv + kv_head) * D;
             st.k[x] = load16(k_cache + base + chunk * 8);
             st.v[x] = load16(v_cache + base + chunk * 8);
         } else {
@@ -229,6 +233,38 @@ __device__ __forceinline__ void stage_store(const StageRegs<D>& st, __bf16* lk, 
     }
 }
 
+// V^T MFMA operand for dim tile n of a 32-key half, read transposed straight out of the
+// row-major [key][dim] LDS tile with ds_read_b64_tr_b16 (gfx950). Within a 16-lane group g,
+// result lane i gets element e from the lane (4e + i/4) of the group, 16-bit word i%4.
+// Pointing source lane s at V[key 4g + s/4][dims 16n + 4(s%4) ..+3] therefore hands lane
+// (dim i, group g) the 4 consecutive keys 4g..4g+3 of dim 16n+i; a second read covers keys
+// 16+4g..16+4g+3. Those 8 keys are exactly T(g, e) = 16*(e/4) + 4g + e%4, the keys the
+// P^T operand of the same lane carries, so no register transpose is needed.
+template <int D>
+__device__ __forceinline__ bf16x8 load_vt(const __bf16* lv, int h2, int n, int lane) {
+    using v4s = short __attribute__((ext_vector_type(4)));
+    const int s = lane & 15;
+    const int g = lane >> 4;
+    const int row = h2 * 32 + 4 * g + (s >> 2);
+    const int dim = 16 * n + 4 * (s & 3);
+    const int chunk = dim >> 3;
+    const int within = dim & 7;
+    const __bf16* p0 = lv + lds_off<D>(row, chunk) + within;
+    const __bf16* p1 = lv + lds_off<D>(row + 16, chunk) + within;
+    const v4s a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) v4s*)(p0));
+    const v4s b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) v4s*)(p1));
+    using v8s = short __attribute__((ext_vector_type(8)));
+    const v8s ab = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    return __builtin_bit_cast(bf16x8, ab);
+}
+
+// Max growth (log2 units) tolerated before the accumulators are rescaled. Probabilities
+// stay <= 2^8 and sums of them fit fp32 comfortably; acc and l always share one reference
+// max, so the final acc / l is exact whatever the reference.
+constexpr float kRescaleSlack = 8.0f;
+
 template <int D>
 __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k_cache,
@@ -237,18 +273,19 @@ __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
     __bf16* __restrict__ out, const int32_t* __restrict__ counts,
     const TileEntry* __restrict__ tiles, int total_tokens, int mbpr, int hq, int hkv,
     int block_size, float scale_log2) {
+    (void)block_size;  // the fast path is specialised for 16-token blocks
     using Sh = PrefillShape<D>;
     constexpr int QT = Sh::kQT;
     constexpr int QW = Sh::kQW;
     constexpr int S = Sh::kSteps;
-    constexpr int NV = Sh::kNV;
+    constexpr int NT = D / 16;  // PV dim tiles
     __shared__ __attribute__((aligned(16))) __bf16 lds_k[2][kKeysPerTile * D];
     __shared__ __attribute__((aligned(16))) __bf16 lds_v[2][kKeysPerTile * D];
     __shared__ uint8_t lds_valid[2][kKeysPerTile];
 
     const int G = hq / hkv;
     const int HPW = heads_per_wg(G);
-    const int WPH = 4 / HPW;
+    const int WPH = kWaves / HPW;
     const int U = hkv * (G / HPW);
     const int tile_idx = blockIdx.x / U;
     if (tile_idx >= counts[0]) return;
@@ -276,7 +313,6 @@ __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
     const int q_head = kvh * G + hg * HPW + head_local;
     const int j = lane & 15;
     const int g = lane >> 4;
-    const int i = lane & 15;
     const int wave_rows = max(0, min(QW, rows - tw));
     const int wave_max_key = prefix + tw + wave_rows - 1;  // last key any row here sees
     const int32_t* req_blocks = block_table + static_cast<int64_t>(req) * mbpr;
@@ -296,18 +332,19 @@ __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
         }
     }
 
-    f32x4 acc[QT][NV];
+    // O^T accumulators: acc[qt][n] lane (query j, grp g) = O[row][16n + 4g + r].
+    f32x4 acc[QT][NT];
     float m[QT], l[QT];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-        m[qt] = kNegInf;
+        m[qt] = kNegInf;  // reference max (log2 units, already scaled)
         l[qt] = 0.f;
 #pragma unroll
-        for (int n = 0; n < NV; ++n) acc[qt][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int n = 0; n < NT; ++n) acc[qt][n] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
     StageRegs<D> stg;
-    stage_load<D>(stg, k_cache, v_cache, req_blocks, 0, ctx, mbpr, block_size, kvh, hkv);
+    stage_load<D>(stg, k_cache, v_cache, req_blocks, 0, ctx, mbpr, kvh, hkv);
     stage_store<D>(stg, lds_k[0], lds_v[0], lds_valid[0]);
     __syncthreads();
 
@@ -316,118 +353,111 @@ __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
         const bool more = t + 1 < ntiles;
         if (more) {
             stage_load<D>(stg, k_cache, v_cache, req_blocks, (t + 1) * kKeysPerTile, ctx, mbpr,
-                          block_size, kvh, hkv);
+                          kvh, hkv);
         }
         const __bf16* lk = lds_k[cur];
         const __bf16* lv = lds_v[cur];
-        const uint64_t vmask = __builtin_amdgcn_ballot_w64(lds_valid[cur][lane] != 0);
-
+        const int key0 = t * kKeysPerTile;
+        if (key0 <= wave_max_key) {
+            const uint64_t vmask = __builtin_amdgcn_ballot_w64(lds_valid[cur][lane] != 0);
 #pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2) {
-            const int key0 = t * kKeysPerTile + h2 * 32;
-            if (key0 > wave_max_key) continue;  // above the diagonal for every row here
-            const uint32_t hmask = static_cast<uint32_t>(vmask >> (h2 * 32));
-            const bool need_mask = (key0 + 31 > prefix + tw) || hmask != 0xffffffffu;
-
-            f32x4 st[2][QT];
+            for (int h2 = 0; h2 < 2; ++h2) {
+                const int hkey0 = key0 + 32 * h2;
+                if (hkey0 > wave_max_key) break;  // above the diagonal for every row here
+                // S^T for the 32 keys of this half: st[kb][qt] lane (query j, g) holds keys
+                // hkey0 + 16kb + 4g + r.
+                f32x4 st[2][QT];
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+                for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-                for (int qt = 0; qt < QT; ++qt) st[kb][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    for (int qt = 0; qt < QT; ++qt) st[kb][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int kk = 0; kk < S; ++kk) {
-                    const int row = h2 * 32 + kb * 16 + i;
-                    const bf16x8 kop = __builtin_bit_cast(
-                        bf16x8, *reinterpret_cast<const u32x4*>(lk + lds_off<D>(row, kk * 4 + g)));
+                    for (int kk = 0; kk < S; ++kk) {
+                        const bf16x8 kop = __builtin_bit_cast(
+                            bf16x8, *reinterpret_cast<const u32x4*>(
+                                        lk + lds_off<D>(32 * h2 + kb * 16 + j, kk * 4 + g)));
 #pragma unroll
-                    for (int qt = 0; qt < QT; ++qt)
-                        st[kb][qt] = mfma16x16x32(kop, qop[qt][kk], st[kb][qt]);
-                }
-            }
-
-            // V^T operand rows: lane (dim row i, grp g) reads key rows T(g, e).
-            uint32_t vr[8][NV / 2];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int row = h2 * 32 + (e >> 2) * 16 + g * 4 + (e & 3);
-                if constexpr (NV == 8) {
-                    const u32x4 w = *reinterpret_cast<const u32x4*>(lv + lds_off<D>(row, i));
-#pragma unroll
-                    for (int x = 0; x < 4; ++x) vr[e][x] = w[x];
-                } else if constexpr (NV == 4) {
-                    const u32x2 w = *reinterpret_cast<const u32x2*>(
-                        lv + lds_off<D>(row, i >> 1) + (i & 1) * 4);
-                    vr[e][0] = w[0];
-                    vr[e][1] = w[1];
-                } else {
-                    const u32x4 w0 = *reinterpret_cast<const u32x4*>(lv + lds_off<D>(row, 2 * i));
-                    const u32x4 w1 =
-                        *reinterpret_cast<const u32x4*>(lv + lds_off<D>(row, 2 * i + 1));
-#pragma unroll
-                    for (int x = 0; x < 4; ++x) {
-                        vr[e][x] = w0[x];
-                        vr[e][4 + x] = w1[x];
+                        for (int qt = 0; qt < QT; ++qt)
+                            st[kb][qt] = mfma16x16x32(kop, qop[qt][kk], st[kb][qt]);
                     }
                 }
-            }
-
-            bf16x8 pop[QT];
-#pragma unroll
-            for (int qt = 0; qt < QT; ++qt) {
-                float sc[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) sc[e] = st[e >> 2][qt][e & 3] * scale_log2;
+                // Causal / validity mask, only where needed (diagonal, ragged end, holes).
+                const uint32_t hmask = static_cast<uint32_t>(vmask >> (32 * h2));
+                const bool need_mask = (hkey0 + 31 > prefix + tw) || hmask != 0xffffffffu;
                 if (need_mask) {
-                    const int limit = prefix + tw + qt * 16 + j;  // last visible key of row
+#pragma unroll
+                    for (int qt = 0; qt < QT; ++qt) {
+                        const int limit = prefix + tw + qt * 16 + j;  // last visible key
+#pragma unroll
+                        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                const int kt = kb * 16 + g * 4 + r;
+                                const bool ok = hkey0 + kt <= limit && ((hmask >> kt) & 1u);
+                                st[kb][qt][r] = ok ? st[kb][qt][r] : kNegInf;
+                            }
+                        }
+                    }
+                }
+                // Row max; rescale only when some row's max grew past the slack.
+                float mt[QT];
+                bool grow = false;
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt) {
+                    float x = fmaxf(fmaxf(fmaxf(st[0][qt][0], st[0][qt][1]),
+                                          fmaxf(st[0][qt][2], st[0][qt][3])),
+                                    fmaxf(fmaxf(st[1][qt][0], st[1][qt][1]),
+                                          fmaxf(st[1][qt][2], st[1][qt][3])));
+                    x = wave_max_xor16_32(x) * scale_log2;
+                    mt[qt] = x;
+                    grow |= x > m[qt] + kRescaleSlack;
+                }
+                if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+#pragma unroll
+                    for (int qt = 0; qt < QT; ++qt) {
+                        const float m_new = fmaxf(m[qt], mt[qt]);
+                        const float alpha =
+                            m_new == kNegInf ? 1.f : __builtin_amdgcn_exp2f(m[qt] - m_new);
+                        l[qt] *= alpha;
+#pragma unroll
+                        for (int n = 0; n < NT; ++n) acc[qt][n] = acc[qt][n] * alpha;
+                        m[qt] = m_new;
+                    }
+                }
+                // P = exp2(s * scale - m) as the bf16 P^T operand of each query tile.
+                bf16x8 pop[QT];
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt) {
+                    const float mneg = m[qt] == kNegInf ? 0.f : -m[qt];
+                    float p[8];
+                    float psum = 0.f;
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
-                        const int kt = h2 * 32 + (e >> 2) * 16 + g * 4 + (e & 3);
-                        const int key = t * kKeysPerTile + kt;
-                        const bool ok = key <= limit && ((vmask >> kt) & 1ull);
-                        if (!ok) sc[e] = kNegInf;
+                        p[e] = __builtin_amdgcn_exp2f(
+                            __builtin_fmaf(st[e >> 2][qt][e & 3], scale_log2, mneg));
+                        psum += p[e];
                     }
+                    l[qt] += psum;
+                    u32x4 pw;
+#pragma unroll
+                    for (int x = 0; x < 4; ++x) pw[x] = pack_bf16x2(p[2 * x], p[2 * x + 1]);
+                    pop[qt] = __builtin_bit_cast(bf16x8, pw);
                 }
-                float mloc = sc[0];
+                // O^T += V^T . P^T.
 #pragma unroll
-                for (int e = 1; e < 8; ++e) mloc = fmaxf(mloc, sc[e]);
-                mloc = wave_max_xor16_32(mloc);
-                const float m_new = fmaxf(m[qt], mloc);
-                const float m_use = (m_new == kNegInf) ? 0.f : m_new;
-                const float alpha = __builtin_amdgcn_exp2f(m[qt] - m_use);
-                float p[8];
-                float psum = 0.f;
+                for (int n = 0; n < NT; ++n) {
+                    const bf16x8 vop = load_vt<D>(lv, h2, n, lane);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    p[e] = __builtin_amdgcn_exp2f(sc[e] - m_use);
-                    psum += p[e];
+                    for (int qt = 0; qt < QT; ++qt)
+                        acc[qt][n] = mfma16x16x32(vop, pop[qt], acc[qt][n]);
                 }
-                l[qt] = l[qt] * alpha + psum;
-                m[qt] = m_new;
-#pragma unroll
-                for (int n = 0; n < NV; ++n) acc[qt][n] = acc[qt][n] * alpha;
-                u32x4 pw;
-#pragma unroll
-                for (int x = 0; x < 4; ++x) pw[x] = pack_bf16x2(p[2 * x], p[2 * x + 1]);
-                pop[qt] = __builtin_bit_cast(bf16x8, pw);
-            }
-
-#pragma unroll
-            for (int n = 0; n < NV; ++n) {
-                u32x4 vw;
-#pragma unroll
-                for (int x = 0; x < 4; ++x)
-                    vw[x] = pick_halves(vr[2 * x][n >> 1], vr[2 * x + 1][n >> 1], n & 1);
-                const bf16x8 vop = __builtin_bit_cast(bf16x8, vw);
-#pragma unroll
-                for (int qt = 0; qt < QT; ++qt) acc[qt][n] = mfma16x16x32(vop, pop[qt], acc[qt][n]);
             }
         }
-
         if (more) stage_store<D>(stg, lds_k[cur ^ 1], lds_v[cur ^ 1], lds_valid[cur ^ 1]);
         __syncthreads();
     }
 
-    // Epilogue: lane (j, g) holds O[row][NV*(4g + r) + n] = acc[qt][n][r].
+    // Epilogue: lane (j, g) holds O[row][16n + 4g + r] = acc[qt][n][r].
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
         const float l_tot = wave_sum_xor16_32(l[qt]);
@@ -436,14 +466,11 @@ __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
         const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
         __bf16* o = out + (static_cast<int64_t>(qb + tq) * hq + q_head) * D;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            uint32_t w[NV / 2];
-#pragma unroll
-            for (int x = 0; x < NV / 2; ++x)
-                w[x] = pack_bf16x2(acc[qt][2 * x][r] * inv, acc[qt][2 * x + 1][r] * inv);
-            uint32_t* dst = reinterpret_cast<uint32_t*>(o + NV * (4 * g + r));
-#pragma unroll
-            for (int x = 0; x < NV / 2; ++x) dst[x] = w[x];
+        for (int n = 0; n < NT; ++n) {
+            u32x2 w;
+            w[0] = pack_bf16x2(acc[qt][n][0] * inv, acc[qt][n][1] * inv);
+            w[1] = pack_bf16x2(acc[qt][n][2] * inv, acc[qt][n][3] * inv);
+            *reinterpret_cast<u32x2*>(o + 16 * n + 4 * g) = w;
         }
     }
 }
@@ -458,8 +485,8 @@ struct PrefillLayout {
 size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
 int tile_tokens_for(int head_dim, int G) {
-    const int qw = head_dim <= 128 ? 64 : 32;
-    return (4 / heads_per_wg(G)) * qw;
+    const int qw = head_dim <= 128 ? 32 : 16;
+    return (kWaves / heads_per_wg(G)) * qw;
 }
 
 PrefillLayout prefill_layout(int batch_size, int total_query_tokens, int max_blocks_per_req,
