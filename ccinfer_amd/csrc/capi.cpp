@@ -75,10 +75,10 @@ bool prefill_shape_ok(int batch_size, int total_query_tokens, int max_blocks_per
            fits_int(static_cast<int64_t>(total_query_tokens) * num_q_heads);
 }
 
-bool prefill_uses_fast(int batch_size, int num_q_heads, int num_kv_heads, int head_dim,
-                       int cache_block_size) {
+bool prefill_uses_fast(int batch_size, int max_blocks_per_req, int num_q_heads,
+                       int num_kv_heads, int head_dim, int cache_block_size) {
     return cache_block_size == 16 && batch_size <= 4096 &&
-           prefill_fast_supported(num_q_heads, num_kv_heads, head_dim) &&
+           prefill_fast_supported(num_q_heads, num_kv_heads, head_dim, max_blocks_per_req) &&
            decode_fast_supported(num_q_heads, num_kv_heads, head_dim, cache_block_size);
 }
 
@@ -147,7 +147,8 @@ size_t ccinfer_prefill_workspace_size(int batch_size, int total_query_tokens,
     if (!prefill_shape_ok(batch_size, total_query_tokens, max_blocks_per_req, num_q_heads,
                           num_kv_heads, head_dim, cache_block_size))
         return 0;
-    if (!prefill_uses_fast(batch_size, num_q_heads, num_kv_heads, head_dim, cache_block_size))
+    if (!prefill_uses_fast(batch_size, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
+                           cache_block_size))
         return 0;
     return prefill_workspace_bytes(batch_size, total_query_tokens, max_blocks_per_req,
                                    num_q_heads, num_kv_heads, head_dim, cache_block_size);
@@ -165,7 +166,8 @@ int ccinfer_prefill_attention(const void* q, const void* k_cache, const void* v_
     if (!prefill_shape_ok(batch_size, total_query_tokens, max_blocks_per_req, num_q_heads,
                           num_kv_heads, head_dim, cache_block_size))
         return CCINFER_ERR_INVALID_ARGUMENT;
-    if (!prefill_uses_fast(batch_size, num_q_heads, num_kv_heads, head_dim, cache_block_size)) {
+    if (!prefill_uses_fast(batch_size, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
+                           cache_block_size)) {
         return map_hip_error(generic_prefill_attention(
             q, k_cache, v_cache, block_table, query_start_loc, context_lens, output, batch_size,
             total_query_tokens, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,

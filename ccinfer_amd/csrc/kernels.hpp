@@ -49,7 +49,8 @@ hipError_t decode_attention(const void* q, const void* k_cache, const void* v_ca
                             const DecodePlan& plan, void* workspace, hipStream_t stream);
 
 // ---- prefill --------------------------------------------------------------
-bool prefill_fast_supported(int num_q_heads, int num_kv_heads, int head_dim);
+bool prefill_fast_supported(int num_q_heads, int num_kv_heads, int head_dim,
+                            int max_blocks_per_req);
 
 size_t prefill_workspace_bytes(int batch_size, int total_query_tokens, int max_blocks_per_req,
                                int num_q_heads, int num_kv_heads, int head_dim,

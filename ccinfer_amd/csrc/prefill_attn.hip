@@ -24,6 +24,8 @@
 //      diagonal / ragged tiles.
 //   3. single-token requests go through the split-KV decode kernel (decode_attn.hip) with
 //      prefill semantics (no 1e-6 in the denominator, bad rows left untouched).
+#include <type_traits>
+
 #include "attn_common.hpp"
 #include "kernels.hpp"
 
@@ -34,6 +36,7 @@ constexpr int kKeysPerTile = 64;
 constexpr int kThreads = 512;     // tile kernel: 8 wavefronts, 2 per SIMD
 constexpr int kWaves = kThreads / 64;
 constexpr int kBlock = 16;        // cache block size of the fast path
+constexpr int kMaxTableLds = 4096;  // block-table entries staged in LDS (64K-token context)
 constexpr int kBuckets = 1024;
 constexpr int kMaxPlanRequests = 4096;
 
@@ -44,7 +47,6 @@ struct PrefillShape {
     static constexpr int kSteps = D / 32;            // QK k-steps
     static constexpr int kNV = D / 16;               // PV MFMAs per query tile
     static constexpr int kCPR = D / 8;               // 16-byte chunks per K/V row
-    static constexpr int kSwz = kCPR < 16 ? kCPR - 1 : 15;
     static constexpr int kLoadsPerThread = kKeysPerTile * kCPR / kThreads;  // per K or V
 };
 
@@ -92,7 +94,8 @@ __device__ void block_inclusive_scan(int* a, int n, int* part) {
 __global__ __launch_bounds__(1024) void prefill_plan_kernel(
     const int32_t* __restrict__ qsl, const int32_t* __restrict__ context_lens, int batch_size,
     int total_tokens, int tile_tokens, int32_t* __restrict__ counts,
-    TileEntry* __restrict__ tiles, int32_t* __restrict__ dec_req) {
+    TileEntry* __restrict__ tiles, int32_t* __restrict__ dec_req, uint32_t* __restrict__ zero_row,
+    int zero_words) {
     __shared__ int s_ntiles[kMaxPlanRequests];
     __shared__ int s_scan[kMaxPlanRequests];
     __shared__ int s_hist[kBuckets];
@@ -101,6 +104,7 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(
     __shared__ int s_ndec;
     __shared__ int s_total;
     const int tid = threadIdx.x;
+    for (int i = tid; i < zero_words; i += blockDim.x) zero_row[i] = 0u;  // staging's zero row
     for (int i = tid; i < kBuckets; i += blockDim.x) s_hist[i] = 0;
     if (tid == 0) s_ndec = 0;
     __syncthreads();
@@ -175,61 +179,62 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(
 // ---------------------------------------------------------------------------
 // Tile kernel.
 // ---------------------------------------------------------------------------
-template <int D>
-struct StageRegs {
-    u32x4 k[PrefillShape<D>::kLoadsPerThread];
-    u32x4 v[PrefillShape<D>::kLoadsPerThread];
-    int valid[PrefillShape<D>::kLoadsPerThread];
-};
+
+// Swizzle of the 16-byte chunk index of K/V row `row` in LDS. f is a permutation of 0..15
+// over any 16 consecutive rows, so the K operand read (16 rows, one logical chunk) hits 16
+// distinct chunk positions, and for any 4 rows 4g..4g+3 and chunk pair {2n, 2n+1} -- one
+// transposing V read -- the 8 (row, chunk) pieces land on 8 distinct positions.
+__device__ __forceinline__ int chunk_swizzle(int row) {
+    const int i = row & 15;
+    return ((i & 3) << 1) | ((i & 4) << 1) | ((i >> 3) & 1);
+}
 
 template <int D>
 __device__ __forceinline__ int lds_off(int row, int chunk) {
-    // Element offset of logical 16-byte chunk `chunk` of key row `row` (XOR swizzle so
-    // 16 lanes reading one chunk column of 16 rows hit distinct banks).
-    return row * D + ((chunk ^ (row & PrefillShape<D>::kSwz)) << 3);
+    // Element offset of logical 16-byte chunk `chunk` of key row `row`.
+    constexpr int kMask = PrefillShape<D>::kCPR - 1;
+    return row * D + ((chunk ^ (chunk_swizzle(row) & kMask)) << 3);
 }
 
+// Direct global->LDS staging of one 64-key K/V tile (gfx950 global_load_lds_dwordx4): an
+// instruction moves 16 bytes per lane straight into LDS at base + 16*lane, so the chunk
+// swizzle is applied on the source side: LDS slot p holds row p/CPR, logical chunk
+// (p%CPR) ^ swizzle(row). Rows outside the visible range (past the context, negative block
+// ids, past the table row) are fetched from `zero_row` so the tile never holds garbage that
+// a masked probability of 0 could turn into NaN. Validity flags go to lvalid[row].
 template <int D>
-__device__ __forceinline__ void stage_load(StageRegs<D>& st, const __bf16* __restrict__ k_cache,
-                                           const __bf16* __restrict__ v_cache,
-                                           const int32_t* __restrict__ req_blocks, int key_base,
-                                           int ctx, int mbpr, int kv_head, int hkv) {
+__device__ __forceinline__ void stage_issue(__bf16* lk, __bf16* lv, uint8_t* lvalid,
+                                            const __bf16* __restrict__ k_cache,
+                                            const __bf16* __restrict__ v_cache,
+                                            const __bf16* __restrict__ zero_row,
+                                            const int32_t* lbt, int key_base, int ctx, int nblk,
+                                            int kv_head, int hkv) {
     constexpr int CPR = PrefillShape<D>::kCPR;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
 #pragma unroll
     for (int x = 0; x < PrefillShape<D>::kLoadsPerThread; ++x) {
-        const int linear = threadIdx.x + kThreads * x;
-        const int row = linear / CPR;
-        const int chunk = linear % CPR;
+        const int slot0 = (x * kWaves + wave) * 64;  // first 16-byte LDS slot of this load
+        const int p = slot0 + lane;
+        const int row = p / CPR;
+        const int lchunk = (p % CPR) ^ (chunk_swizzle(row) & (CPR - 1));
         const int key = key_base + row;
-        const int lb = key >> 4;  // 16-token blocks (the fast path's contract)
+        const int lb = key >> 4;
         int pb = -1;
-        if (key < ctx && lb < mbpr) pb = req_blocks[lb];
-        st.valid[x] = pb >= 0;
+        if (key < ctx && lb < nblk) pb = lbt[lb];
+        const __bf16* ks = zero_row;
+        const __bf16* vs = zero_row;
         if (pb >= 0) {
             const int64_t base =
                 ((static_cast<int64_t>(pb) * kBlock + (key & (kBlock - 1))) * hkv + kv_head) * D;
-            st.k[x] = load16(k_cache + base + chunk * 8);
-            st.v[x] = load16(v_cache + base + chunk * 8);
-        } else {
-            st.k[x] = u32x4{0, 0, 0, 0};
-            st.v[x] = u32x4{0, 0, 0, 0};
+            ks = k_cache + base;
+            vs = v_cache + base;
         }
-    }
-}
-
-template <int D>
-__device__ __forceinline__ void stage_store(const StageRegs<D>& st, __bf16* lk, __bf16* lv,
-                                            uint8_t* lvalid) {
-    constexpr int CPR = PrefillShape<D>::kCPR;
-#pragma unroll
-    for (int x = 0; x < PrefillShape<D>::kLoadsPerThread; ++x) {
-        const int linear = threadIdx.x + kThreads * x;
-        const int row = linear / CPR;
-        const int chunk = linear % CPR;
-        const int off = lds_off<D>(row, chunk);
-        *reinterpret_cast<u32x4*>(lk + off) = st.k[x];
-        *reinterpret_cast<u32x4*>(lv + off) = st.v[x];
-        if (chunk == 0) lvalid[row] = static_cast<uint8_t>(st.valid[x]);
+        __builtin_amdgcn_global_load_lds(
+            ks + lchunk * 8, (__attribute__((address_space(3))) void*)(lk + slot0 * 8), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(
+            vs + lchunk * 8, (__attribute__((address_space(3))) void*)(lv + slot0 * 8), 16, 0, 0);
+        if ((p % CPR) == 0) lvalid[row] = static_cast<uint8_t>(pb >= 0);
     }
 }
 
@@ -271,17 +276,25 @@ __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
     const __bf16* __restrict__ v_cache, const int32_t* __restrict__ block_table,
     const int32_t* __restrict__ qsl, const int32_t* __restrict__ context_lens,
     __bf16* __restrict__ out, const int32_t* __restrict__ counts,
-    const TileEntry* __restrict__ tiles, int total_tokens, int mbpr, int hq, int hkv,
-    int block_size, float scale_log2) {
+    const TileEntry* __restrict__ tiles, const __bf16* __restrict__ zero_row, int total_tokens,
+    int mbpr, int hq, int hkv, int block_size, float scale_log2) {
     (void)block_size;  // the fast path is specialised for 16-token blocks
     using Sh = PrefillShape<D>;
     constexpr int QT = Sh::kQT;
     constexpr int QW = Sh::kQW;
     constexpr int S = Sh::kSteps;
     constexpr int NT = D / 16;  // PV dim tiles
-    __shared__ __attribute__((aligned(16))) __bf16 lds_k[2][kKeysPerTile * D];
-    __shared__ __attribute__((aligned(16))) __bf16 lds_v[2][kKeysPerTile * D];
-    __shared__ uint8_t lds_valid[2][kKeysPerTile];
+    // Two K/V buffers as distinct arrays: every access names its buffer statically, so the
+    // compiler can see that the direct-to-LDS loads filling one buffer never alias reads of
+    // the other and does not drain them before the attention math.
+    __shared__ __attribute__((aligned(16))) __bf16 lds_k0[kKeysPerTile * D];
+    __shared__ __attribute__((aligned(16))) __bf16 lds_k1[kKeysPerTile * D];
+    __shared__ __attribute__((aligned(16))) __bf16 lds_v0[kKeysPerTile * D];
+    __shared__ __attribute__((aligned(16))) __bf16 lds_v1[kKeysPerTile * D];
+    __shared__ uint8_t lds_valid0[kKeysPerTile];
+    __shared__ uint8_t lds_valid1[kKeysPerTile];
+    // The request's block-table entries for the visible range (-1 past the table row).
+    __shared__ int32_t lds_bt[kMaxTableLds];
 
     const int G = hq / hkv;
     const int HPW = heads_per_wg(G);
@@ -333,134 +346,189 @@ __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
     }
 
     // O^T accumulators: acc[qt][n] lane (query j, grp g) = O[row][16n + 4g + r].
+    // Row sums of P ride on the MFMA unit: ones(16x32) . P^T gives every lane of query
+    // column j the full sum over the 32 keys (and sums the same bf16-rounded P that the PV
+    // product uses).
     f32x4 acc[QT][NT];
-    float m[QT], l[QT];
+    f32x4 lsum[QT];
+    float m[QT];
+    const bf16x8 ones = __builtin_bit_cast(
+        bf16x8, u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
         m[qt] = kNegInf;  // reference max (log2 units, already scaled)
-        l[qt] = 0.f;
+        lsum[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int n = 0; n < NT; ++n) acc[qt][n] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    StageRegs<D> stg;
-    stage_load<D>(stg, k_cache, v_cache, req_blocks, 0, ctx, mbpr, kvh, hkv);
-    stage_store<D>(stg, lds_k[0], lds_v[0], lds_valid[0]);
+    // Stage the visible block-table slice in LDS (so tile staging never waits on a global
+    // load) and note whether it has holes (negative or missing entries).
+    __shared__ int s_holes;
+    if (threadIdx.x == 0) s_holes = 0;
+    __syncthreads();
+    // Positions past the table row are invalid, so only min(visible, mbpr) entries matter;
+    // the host routes tables longer than kMaxTableLds to the generic kernel.
+    const int nblk_vis = (kv_end + kBlock - 1) / kBlock;
+    const int nblk = min(nblk_vis, mbpr);
+    for (int lb = threadIdx.x; lb < nblk; lb += kThreads) {
+        const int pb = req_blocks[lb];
+        lds_bt[lb] = pb;
+        if (pb < 0) s_holes = 1;
+    }
+    __syncthreads();
+    const bool holes = s_holes != 0 || nblk_vis > mbpr;
+
+    stage_issue<D>(lds_k0, lds_v0, lds_valid0, k_cache, v_cache, zero_row, lds_bt, 0, ctx, nblk,
+                   kvh, hkv);
+    __builtin_amdgcn_s_waitcnt(0);  // this wavefront's direct-to-LDS loads have landed
     __syncthreads();
 
-    for (int t = 0; t < ntiles; ++t) {
-        const int cur = t & 1;
-        const bool more = t + 1 < ntiles;
-        if (more) {
-            stage_load<D>(stg, k_cache, v_cache, req_blocks, (t + 1) * kKeysPerTile, ctx, mbpr,
-                          kvh, hkv);
+    // Attention over one staged 64-key tile, straight-line so the scheduler can overlap the
+    // LDS reads, MFMAs and softmax VALU work of both 32-key halves. kMask selects the variant
+    // with the causal / validity mask (diagonal, ragged-end and hole tiles only).
+    auto attend_tile = [&](const __bf16* lk, const __bf16* lv, const uint64_t vmask, int key0,
+                           auto mask_tag) __attribute__((always_inline)) {
+        constexpr bool kMask = decltype(mask_tag)::value;
+        // S^T: st[kb][qt] lane (query j, g) holds keys key0 + 16kb + 4g + r.
+        f32x4 st[4][QT];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            if (kb == 2) __builtin_amdgcn_sched_barrier(0);  // bound K operands in flight
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) st[kb][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < S; ++kk) {
+                const bf16x8 kop = __builtin_bit_cast(
+                    bf16x8,
+                    *reinterpret_cast<const u32x4*>(lk + lds_off<D>(kb * 16 + j, kk * 4 + g)));
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt)
+                    st[kb][qt] = mfma16x16x32(kop, qop[qt][kk], st[kb][qt]);
+            }
         }
-        const __bf16* lk = lds_k[cur];
-        const __bf16* lv = lds_v[cur];
-        const int key0 = t * kKeysPerTile;
-        if (key0 <= wave_max_key) {
-            const uint64_t vmask = __builtin_amdgcn_ballot_w64(lds_valid[cur][lane] != 0);
+        if constexpr (kMask) {
 #pragma unroll
-            for (int h2 = 0; h2 < 2; ++h2) {
-                const int hkey0 = key0 + 32 * h2;
-                if (hkey0 > wave_max_key) break;  // above the diagonal for every row here
-                // S^T for the 32 keys of this half: st[kb][qt] lane (query j, g) holds keys
-                // hkey0 + 16kb + 4g + r.
-                f32x4 st[2][QT];
+            for (int qt = 0; qt < QT; ++qt) {
+                const int limit = prefix + tw + qt * 16 + j;  // last visible key of the row
 #pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
+                for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
-                    for (int qt = 0; qt < QT; ++qt) st[kb][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int kk = 0; kk < S; ++kk) {
-                        const bf16x8 kop = __builtin_bit_cast(
-                            bf16x8, *reinterpret_cast<const u32x4*>(
-                                        lk + lds_off<D>(32 * h2 + kb * 16 + j, kk * 4 + g)));
-#pragma unroll
-                        for (int qt = 0; qt < QT; ++qt)
-                            st[kb][qt] = mfma16x16x32(kop, qop[qt][kk], st[kb][qt]);
+                    for (int r = 0; r < 4; ++r) {
+                        const int kt = kb * 16 + g * 4 + r;
+                        const bool ok = key0 + kt <= limit && ((vmask >> kt) & 1ull);
+                        st[kb][qt][r] = ok ? st[kb][qt][r] : kNegInf;
                     }
-                }
-                // Causal / validity mask, only where needed (diagonal, ragged end, holes).
-                const uint32_t hmask = static_cast<uint32_t>(vmask >> (32 * h2));
-                const bool need_mask = (hkey0 + 31 > prefix + tw) || hmask != 0xffffffffu;
-                if (need_mask) {
-#pragma unroll
-                    for (int qt = 0; qt < QT; ++qt) {
-                        const int limit = prefix + tw + qt * 16 + j;  // last visible key
-#pragma unroll
-                        for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-                            for (int r = 0; r < 4; ++r) {
-                                const int kt = kb * 16 + g * 4 + r;
-                                const bool ok = hkey0 + kt <= limit && ((hmask >> kt) & 1u);
-                                st[kb][qt][r] = ok ? st[kb][qt][r] : kNegInf;
-                            }
-                        }
-                    }
-                }
-                // Row max; rescale only when some row's max grew past the slack.
-                float mt[QT];
-                bool grow = false;
-#pragma unroll
-                for (int qt = 0; qt < QT; ++qt) {
-                    float x = fmaxf(fmaxf(fmaxf(st[0][qt][0], st[0][qt][1]),
-                                          fmaxf(st[0][qt][2], st[0][qt][3])),
-                                    fmaxf(fmaxf(st[1][qt][0], st[1][qt][1]),
-                                          fmaxf(st[1][qt][2], st[1][qt][3])));
-                    x = wave_max_xor16_32(x) * scale_log2;
-                    mt[qt] = x;
-                    grow |= x > m[qt] + kRescaleSlack;
-                }
-                if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-#pragma unroll
-                    for (int qt = 0; qt < QT; ++qt) {
-                        const float m_new = fmaxf(m[qt], mt[qt]);
-                        const float alpha =
-                            m_new == kNegInf ? 1.f : __builtin_amdgcn_exp2f(m[qt] - m_new);
-                        l[qt] *= alpha;
-#pragma unroll
-                        for (int n = 0; n < NT; ++n) acc[qt][n] = acc[qt][n] * alpha;
-                        m[qt] = m_new;
-                    }
-                }
-                // P = exp2(s * scale - m) as the bf16 P^T operand of each query tile.
-                bf16x8 pop[QT];
-#pragma unroll
-                for (int qt = 0; qt < QT; ++qt) {
-                    const float mneg = m[qt] == kNegInf ? 0.f : -m[qt];
-                    float p[8];
-                    float psum = 0.f;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        p[e] = __builtin_amdgcn_exp2f(
-                            __builtin_fmaf(st[e >> 2][qt][e & 3], scale_log2, mneg));
-                        psum += p[e];
-                    }
-                    l[qt] += psum;
-                    u32x4 pw;
-#pragma unroll
-                    for (int x = 0; x < 4; ++x) pw[x] = pack_bf16x2(p[2 * x], p[2 * x + 1]);
-                    pop[qt] = __builtin_bit_cast(bf16x8, pw);
-                }
-                // O^T += V^T . P^T.
-#pragma unroll
-                for (int n = 0; n < NT; ++n) {
-                    const bf16x8 vop = load_vt<D>(lv, h2, n, lane);
-#pragma unroll
-                    for (int qt = 0; qt < QT; ++qt)
-                        acc[qt][n] = mfma16x16x32(vop, pop[qt], acc[qt][n]);
                 }
             }
         }
-        if (more) stage_store<D>(stg, lds_k[cur ^ 1], lds_v[cur ^ 1], lds_valid[cur ^ 1]);
+        // Row max of the tile; rescale only when some row's max grew past the slack.
+        float mt[QT];
+        bool grow = false;
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+            float x = kNegInf;
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb)
+                x = fmaxf(x, fmaxf(fmaxf(st[kb][qt][0], st[kb][qt][1]),
+                                   fmaxf(st[kb][qt][2], st[kb][qt][3])));
+            x = wave_max_xor16_32(x) * scale_log2;
+            mt[qt] = x;
+            grow |= x > m[qt] + kRescaleSlack;
+        }
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) {
+                const float m_new = fmaxf(m[qt], mt[qt]);
+                const float alpha =
+                    m_new == kNegInf ? 1.f : __builtin_amdgcn_exp2f(m[qt] - m_new);
+                lsum[qt] = lsum[qt] * alpha;
+#pragma unroll
+                for (int n = 0; n < NT; ++n) acc[qt][n] = acc[qt][n] * alpha;
+                m[qt] = m_new;
+            }
+        }
+        // P = exp2(s * scale - m) as bf16 P^T operands; O^T += V^T . P^T; row sums.
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+            // Keep each half's V reads and exp work in its own scheduling window (bounds the
+            // registers in flight at two wavefronts per SIMD).
+            __builtin_amdgcn_sched_barrier(0);
+            bf16x8 pop[QT];
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) {
+                const float mneg = m[qt] == kNegInf ? 0.f : -m[qt];
+                float p[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    p[e] = __builtin_amdgcn_exp2f(
+                        __builtin_fmaf(st[2 * h2 + (e >> 2)][qt][e & 3], scale_log2, mneg));
+                }
+                u32x4 pw;
+#pragma unroll
+                for (int x = 0; x < 4; ++x) pw[x] = pack_bf16x2(p[2 * x], p[2 * x + 1]);
+                pop[qt] = __builtin_bit_cast(bf16x8, pw);
+                lsum[qt] = mfma16x16x32(ones, pop[qt], lsum[qt]);
+            }
+#pragma unroll
+            for (int n = 0; n < NT; ++n) {
+                const bf16x8 vop = load_vt<D>(lv, h2, n, lane);
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt)
+                    acc[qt][n] = mfma16x16x32(vop, pop[qt], acc[qt][n]);
+            }
+        }
+    };
+
+    // One K/V tile from buffer B (0/1, a compile-time constant), with the next tile's loads
+    // in flight into the other buffer. Every wavefront stages every tile and meets one barrier
+    // per tile; the attention work is skipped for tiles entirely above its diagonal.
+    auto process_tile = [&](int t, auto buf_tag, auto mask_tag) __attribute__((always_inline)) {
+        constexpr int B = decltype(buf_tag)::value;
+        __bf16* ck = B == 0 ? lds_k0 : lds_k1;
+        __bf16* cv = B == 0 ? lds_v0 : lds_v1;
+        uint8_t* cvalid = B == 0 ? lds_valid0 : lds_valid1;
+        __bf16* nk = B == 0 ? lds_k1 : lds_k0;
+        __bf16* nv = B == 0 ? lds_v1 : lds_v0;
+        uint8_t* nvalid = B == 0 ? lds_valid1 : lds_valid0;
+        const bool more = t + 1 < ntiles;
+        if (more) {
+            stage_issue<D>(nk, nv, nvalid, k_cache, v_cache, zero_row, lds_bt,
+                           (t + 1) * kKeysPerTile, ctx, nblk, kvh, hkv);
+        }
+        const int key0 = t * kKeysPerTile;
+        if (key0 <= wave_max_key) {
+            const uint64_t vmask = decltype(mask_tag)::value
+                                       ? __builtin_amdgcn_ballot_w64(cvalid[lane] != 0)
+                                       : ~0ull;
+            attend_tile(ck, cv, vmask, key0, mask_tag);
+        }
+        if (more) __builtin_amdgcn_s_waitcnt(0);  // next tile resident before the barrier
         __syncthreads();
+    };
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+
+    // Tiles wholly below this wavefront's diagonal need no mask unless the block table has
+    // holes inside the visible range (then every tile takes the masked path). Tiles go in
+    // pairs (buffer 0 then 1); the mask-free count is rounded down to a pair.
+    int mask_free = 0;
+    if (!holes) mask_free = min(ntiles, (prefix + tw + 1) / kKeysPerTile) & ~1;
+    int t = 0;
+    for (; t < mask_free; t += 2) {
+        process_tile(t, B0{}, std::false_type{});
+        process_tile(t + 1, B1{}, std::false_type{});
     }
+    for (; t + 1 < ntiles; t += 2) {
+        process_tile(t, B0{}, std::true_type{});
+        process_tile(t + 1, B1{}, std::true_type{});
+    }
+    if (t < ntiles) process_tile(t, B0{}, std::true_type{});
 
     // Epilogue: lane (j, g) holds O[row][16n + 4g + r] = acc[qt][n][r].
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-        const float l_tot = wave_sum_xor16_32(l[qt]);
+        const float l_tot = lsum[qt][0];
         const int tq = tw + qt * 16 + j;
         if (tq >= rows) continue;
         const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
@@ -476,7 +544,7 @@ __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
 }
 
 struct PrefillLayout {
-    size_t counts_off, tiles_off, dec_off, decode_ws_off, total;
+    size_t counts_off, zero_off, tiles_off, dec_off, decode_ws_off, total;
     int max_tiles;
     int tile_tokens;
     DecodePlan plan;
@@ -499,6 +567,8 @@ PrefillLayout prefill_layout(int batch_size, int total_query_tokens, int max_blo
     size_t off = 0;
     L.counts_off = off;
     off = align256(off + 2 * sizeof(int32_t));
+    L.zero_off = off;  // one all-zero K/V row (head_dim bf16), rewritten by the planner
+    off = align256(off + static_cast<size_t>(head_dim) * 2);
     L.tiles_off = off;
     off = align256(off + static_cast<size_t>(L.max_tiles) * sizeof(TileEntry));
     L.dec_off = off;
@@ -514,7 +584,8 @@ hipError_t launch_tiles(const void* q, const void* k_cache, const void* v_cache,
                         const int32_t* block_table, const int32_t* qsl,
                         const int32_t* context_lens, void* output, int total_query_tokens,
                         int mbpr, int hq, int hkv, int block_size, const int32_t* counts,
-                        const TileEntry* tiles, int max_tiles, hipStream_t stream) {
+                        const TileEntry* tiles, const void* zero_row, int max_tiles,
+                        hipStream_t stream) {
     const int G = hq / hkv;
     const int U = hkv * (G / heads_per_wg(G));
     const int64_t grid = static_cast<int64_t>(max_tiles) * U;
@@ -522,15 +593,17 @@ hipError_t launch_tiles(const void* q, const void* k_cache, const void* v_cache,
     prefill_tile_kernel<D><<<static_cast<unsigned>(grid), kThreads, 0, stream>>>(
         static_cast<const __bf16*>(q), static_cast<const __bf16*>(k_cache),
         static_cast<const __bf16*>(v_cache), block_table, qsl, context_lens,
-        static_cast<__bf16*>(output), counts, tiles, total_query_tokens, mbpr, hq, hkv,
-        block_size, scale_log2);
+        static_cast<__bf16*>(output), counts, tiles, static_cast<const __bf16*>(zero_row),
+        total_query_tokens, mbpr, hq, hkv, block_size, scale_log2);
     return hipGetLastError();
 }
 
 }  // namespace
 
-bool prefill_fast_supported(int num_q_heads, int num_kv_heads, int head_dim) {
+bool prefill_fast_supported(int num_q_heads, int num_kv_heads, int head_dim,
+                            int max_blocks_per_req) {
     if (num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0) return false;
+    if (max_blocks_per_req > kMaxTableLds) return false;
     const int G = num_q_heads / num_kv_heads;
     return G <= 16 && (head_dim == 64 || head_dim == 128 || head_dim == 256);
 }
@@ -556,9 +629,10 @@ hipError_t prefill_attention(const void* q, const void* k_cache, const void* v_c
     int32_t* counts = reinterpret_cast<int32_t*>(ws + L.counts_off);
     TileEntry* tiles = reinterpret_cast<TileEntry*>(ws + L.tiles_off);
     int32_t* dec = reinterpret_cast<int32_t*>(ws + L.dec_off);
+    uint32_t* zero_row = reinterpret_cast<uint32_t*>(ws + L.zero_off);
     prefill_plan_kernel<<<1, 1024, 0, stream>>>(query_start_loc, context_lens, batch_size,
                                                 total_query_tokens, L.tile_tokens, counts, tiles,
-                                                dec);
+                                                dec, zero_row, head_dim / 2);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     switch (head_dim) {
@@ -566,19 +640,19 @@ hipError_t prefill_attention(const void* q, const void* k_cache, const void* v_c
             err = launch_tiles<64>(q, k_cache, v_cache, block_table, query_start_loc,
                                    context_lens, output, total_query_tokens, max_blocks_per_req,
                                    num_q_heads, num_kv_heads, block_size, counts, tiles,
-                                   L.max_tiles, stream);
+                                   zero_row, L.max_tiles, stream);
             break;
         case 128:
             err = launch_tiles<128>(q, k_cache, v_cache, block_table, query_start_loc,
                                     context_lens, output, total_query_tokens, max_blocks_per_req,
                                     num_q_heads, num_kv_heads, block_size, counts, tiles,
-                                    L.max_tiles, stream);
+                                    zero_row, L.max_tiles, stream);
             break;
         case 256:
             err = launch_tiles<256>(q, k_cache, v_cache, block_table, query_start_loc,
                                     context_lens, output, total_query_tokens, max_blocks_per_req,
                                     num_q_heads, num_kv_heads, block_size, counts, tiles,
-                                    L.max_tiles, stream);
+                                    zero_row, L.max_tiles, stream);
             break;
         default:
             return hipErrorInvalidValue;
