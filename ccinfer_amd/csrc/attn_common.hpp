@@ -61,6 +61,18 @@ __device__ __forceinline__ float wave_max_xor16_32(float v) {
     return v;
 }
 
+// Max over lanes l, l^16, l^32, l^48 with the gfx950 lane-swap instructions (no LDS
+// round trip): permlane32_swap on two copies leaves {x[l%32], x[l%32+32]} in the pair,
+// permlane16_swap then pairs 16-lane rows 0/1 and 2/3.
+__device__ __forceinline__ float wave_max_swap16_32(float v) {
+    const uint32_t u = __float_as_uint(v);
+    const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    const float m32 = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const uint32_t w = __float_as_uint(m32);
+    const auto b = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 __device__ __forceinline__ float wave_sum_xor16_32(float v) {
     v += __shfl_xor(v, 16);
     v += __shfl_xor(v, 32);

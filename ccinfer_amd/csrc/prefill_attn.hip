@@ -184,10 +184,7 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(
 // over any 16 consecutive rows, so the K operand read (16 rows, one logical chunk) hits 16
 // distinct chunk positions, and for any 4 rows 4g..4g+3 and chunk pair {2n, 2n+1} -- one
 // transposing V read -- the 8 (row, chunk) pieces land on 8 distinct positions.
-__device__ __forceinline__ int chunk_swizzle(int row) {
-    const int i = row & 15;
-    return ((i & 3) << 1) | ((i & 4) << 1) | ((i >> 3) & 1);
-}
+__device__ __forceinline__ int chunk_swizzle(int row) { return row & 15; }
 
 template <int D>
 __device__ __forceinline__ int lds_off(int row, int chunk) {
@@ -269,6 +266,7 @@ __device__ __forceinline__ bf16x8 load_vt(const __bf16* lv, int h2, int n, int l
 // stay <= 2^8 and sums of them fit fp32 comfortably; acc and l always share one reference
 // max, so the final acc / l is exact whatever the reference.
 constexpr float kRescaleSlack = 8.0f;
+constexpr float kMaxInit = -1.0e30f;
 
 template <int D>
 __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
@@ -543,6 +541,488 @@ __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// Pipelined tile kernel (head_dim 64 / 128).
+//
+// One workgroup = 8 wavefronts (two per SIMD, <= 256 VGPRs each); each wavefront owns 32
+// query rows of one q-head and the workgroup covers the Hq/Hkv heads that share a KV head,
+// so every K/V tile staged in LDS feeds all of them. Work advances in 32-key halves through
+// a software pipeline so that each wavefront always has independent MFMA and VALU work:
+//     X_i: P_i = exp2(S_i * scale - m)           ||  S_{i+1} = K_{i+1} . Q^T
+//     Y_i: O  += V_i^T . P_i^T                   ||  mask + row max of S_{i+1}
+// with the instruction interleave pinned by sched_group_barrier. K/V tiles are
+// triple-buffered in LDS: at the barrier in the middle of tile t every wavefront has
+// finished tile t-1 and tile t+1 has landed, so tile t+2 streams into the freed buffer
+// while tiles t and t+1 are read.
+// ---------------------------------------------------------------------------
+template <int D, int QT>
+struct PipeShape {
+    static constexpr int kQT = QT;
+    static constexpr int kRows = 16 * QT;                // query rows per wavefront
+    static constexpr int kWaves = 8;
+    static constexpr int kThreads = 64 * kWaves;
+    static constexpr int kSteps = D / 32;                // QK k-steps
+    static constexpr int kNT = D / 16;                   // PV dim tiles
+    static constexpr int kCPR = D / 8;                   // 16-byte chunks per K/V row
+    static constexpr int kLoads = kKeysPerTile * kCPR / kThreads;  // per K or V
+    static_assert(kKeysPerTile * kCPR % kThreads == 0, "staging must split evenly");
+};
+constexpr int kPipeQT = 2;  // 32 rows per wavefront
+
+__host__ __device__ constexpr bool pipe_head_dim(int d) { return d == 64 || d == 128; }
+
+template <int D, int QTT>
+__global__ __launch_bounds__((PipeShape<D, QTT>::kThreads))
+void prefill_pipe_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ k_cache,
+                         const __bf16* __restrict__ v_cache,
+                         const int32_t* __restrict__ block_table,
+                         const int32_t* __restrict__ qsl,
+                         const int32_t* __restrict__ context_lens, __bf16* __restrict__ out,
+                         const int32_t* __restrict__ counts, const TileEntry* __restrict__ tiles,
+                         int total_tokens, int mbpr, int hq, int hkv, float scale_log2) {
+    using Sh = PipeShape<D, QTT>;
+    constexpr int QT = Sh::kQT;
+    constexpr int S = Sh::kSteps;
+    constexpr int NT = Sh::kNT;
+    constexpr int CPR = Sh::kCPR;
+    constexpr int NL = Sh::kLoads;
+    constexpr int kPipeWaves = Sh::kWaves;
+    constexpr int kPipeThreads = Sh::kThreads;
+    constexpr int kPipeRows = Sh::kRows;
+    // Three K/V buffers as distinct arrays (see prefill_tile_kernel: the compiler then knows
+    // the direct-to-LDS loads into one buffer never alias reads of another).
+    __shared__ __attribute__((aligned(16))) __bf16 lds_k0[kKeysPerTile * D];
+    __shared__ __attribute__((aligned(16))) __bf16 lds_k1[kKeysPerTile * D];
+    __shared__ __attribute__((aligned(16))) __bf16 lds_k2[kKeysPerTile * D];
+    __shared__ __attribute__((aligned(16))) __bf16 lds_v0[kKeysPerTile * D];
+    __shared__ __attribute__((aligned(16))) __bf16 lds_v1[kKeysPerTile * D];
+    __shared__ __attribute__((aligned(16))) __bf16 lds_v2[kKeysPerTile * D];
+    __shared__ uint8_t lds_valid0[kKeysPerTile];
+    __shared__ uint8_t lds_valid1[kKeysPerTile];
+    __shared__ uint8_t lds_valid2[kKeysPerTile];
+    __shared__ int32_t lds_bt[kMaxTableLds];
+    __shared__ int s_holes;
+
+    const int G = hq / hkv;
+    const int HPW = heads_per_wg(G);
+    const int WPH = kPipeWaves / HPW;
+    const int U = hkv * (G / HPW);
+    const int tile_idx = blockIdx.x / U;
+    if (tile_idx >= counts[0]) return;
+    const int u = blockIdx.x % U;
+    const int kvh = u / (G / HPW);
+    const int hg = u % (G / HPW);
+    const TileEntry te = tiles[tile_idx];
+    const int req = te.req;
+    const int t0 = te.t0;
+
+    const int qb = qsl[req];
+    const int qlen = qsl[req + 1] - qb;
+    const int ctx = context_lens[req];
+    const int prefix = ctx - qlen;
+    const int qe = min(qb + qlen, total_tokens);
+    const int rows = qe - qb;
+    const int TT = WPH * kPipeRows;
+    const int kv_end = prefix + min(t0 + TT, rows);  // keys past it are masked for every row
+    // Positions past the table row are invalid: no tile needs to reach them.
+    const int kv_lim = min(kv_end, mbpr * kBlock);
+    const int ntiles = (kv_lim + kKeysPerTile - 1) / kKeysPerTile;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int head_local = wave / WPH;
+    const int tw = t0 + (wave % WPH) * kPipeRows;
+    const int q_head = kvh * G + hg * HPW + head_local;
+    const int j = lane & 15;
+    const int g = lane >> 4;
+    const int32_t* req_blocks = block_table + static_cast<int64_t>(req) * mbpr;
+
+    // Block-table slice in LDS: entries for every block the tiles touch, -1 past the
+    // visible range or the table row. Holes (negative ids inside the visible range, or a
+    // visible range longer than the row) force the masked path on every tile.
+    if (threadIdx.x == 0) s_holes = 0;
+    __syncthreads();
+    const int nblk_vis = (kv_end + kBlock - 1) / kBlock;
+    const int nblk = min(nblk_vis, mbpr);
+    for (int lb = threadIdx.x; lb < ntiles * (kKeysPerTile / kBlock); lb += kPipeThreads) {
+        const int pb = lb < nblk ? req_blocks[lb] : -1;
+        lds_bt[lb] = pb;
+        if (lb < nblk && pb < 0) s_holes = 1;
+    }
+
+    // Zero the K/V buffers once: slots that are never loaded must hold finite values.
+    {
+        constexpr int kWords = kKeysPerTile * D / 8;  // 16-byte words per buffer
+        __bf16* bufs[6] = {lds_k0, lds_k1, lds_k2, lds_v0, lds_v1, lds_v2};
+#pragma unroll
+        for (int bi = 0; bi < 6; ++bi)
+            for (int i = threadIdx.x; i < kWords; i += kPipeThreads)
+                reinterpret_cast<u32x4*>(bufs[bi])[i] = u32x4{0, 0, 0, 0};
+    }
+
+    // Staging constants. Load x of a wavefront fills the 64 16-byte LDS slots starting at
+    // slot0 = (x * waves + wave) * 64: rows slot0/CPR .. +64/CPR-1, which lie in one 16-row
+    // cache block, so the block id is wave-uniform and each address is a scalar block base
+    // plus this lane's 32-bit byte offset inside the block (row-in-block, kv head, chunk,
+    // with the LDS chunk swizzle applied on the source side).
+    int st_row[NL];
+    uint32_t st_off[NL];
+#pragma unroll
+    for (int x = 0; x < NL; ++x) {
+        const int p = (x * kPipeWaves + wave) * 64 + lane;
+        const int row = p / CPR;
+        const int lch = (p % CPR) ^ (chunk_swizzle(row) & (CPR - 1));
+        st_row[x] = row;
+        st_off[x] = static_cast<uint32_t>((((row & (kBlock - 1)) * hkv + kvh) * D + lch * 8) * 2);
+    }
+    const int64_t blk_bytes = static_cast<int64_t>(kBlock) * hkv * D * 2;
+
+    // Per-lane LDS read offsets (elements). Rows 16 apart share a swizzle, so one offset per
+    // k-step (K reads: row j, chunk 4kk+g) and per dim tile (transposing V reads: rows
+    // 4g + s/4, chunk 2n + (s/2)%2) serves every half, 16-row block and buffer; the rest is
+    // a constant the compiler folds into the instruction.
+    int koff[S];
+#pragma unroll
+    for (int kk = 0; kk < S; ++kk) koff[kk] = lds_off<D>(j, kk * 4 + g);
+    int voff[NT];
+    {
+        const int s16 = lane & 15;
+        const int row0 = 4 * g + (s16 >> 2);
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+            const int dim = 16 * n + 4 * (s16 & 3);
+            voff[n] = lds_off<D>(row0, dim >> 3) + (dim & 7);
+        }
+    }
+
+    // Rows past kv_end or in unmapped blocks are not loaded: their LDS slots keep earlier,
+    // finite contents (the buffers are zeroed first) and the mask gives them probability 0.
+    auto stage = [&](int t, __bf16* lk, __bf16* lv, uint8_t* lvalid)
+                     __attribute__((always_inline)) {
+        const int key_base = t * kKeysPerTile;
+#pragma unroll
+        for (int x = 0; x < NL; ++x) {
+            const int slot0 = (x * kPipeWaves + wave) * 64;
+            const int row = st_row[x];
+            const int pb = __builtin_amdgcn_readfirstlane(
+                lds_bt[t * (kKeysPerTile / kBlock) + ((slot0 / CPR) >> 4)]);
+            const bool in_range = key_base + row < kv_end;
+            if (pb >= 0) {
+                const int64_t boff = static_cast<int64_t>(pb) * blk_bytes;
+                const char* kb = reinterpret_cast<const char*>(k_cache) + boff;
+                const char* vb = reinterpret_cast<const char*>(v_cache) + boff;
+                if (in_range) {
+                    __builtin_amdgcn_global_load_lds(
+                        (void*)(kb + st_off[x]),  // a char* argument makes clang drop the
+                                                  // kernel's host launch stub silently
+                        (__attribute__((address_space(3))) void*)(lk + slot0 * 8), 16, 0, 0);
+                    __builtin_amdgcn_global_load_lds(
+                        (void*)(vb + st_off[x]),
+                        (__attribute__((address_space(3))) void*)(lv + slot0 * 8), 16, 0, 0);
+                }
+            }
+            if (((slot0 + lane) % CPR) == 0)
+                lvalid[row] = static_cast<uint8_t>(pb >= 0 && in_range);
+        }
+    };
+
+    // Q^T operands: lane (query j, grp g) holds dims (kk*4+g)*8.. of row tw + qt*16 + j.
+    bf16x8 qop[QT][S];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        const int tq = tw + qt * 16 + j;
+        const bool live = tq < rows;
+        const __bf16* qv = q + (static_cast<int64_t>(qb + (live ? tq : 0)) * hq + q_head) * D;
+#pragma unroll
+        for (int kk = 0; kk < S; ++kk) {
+            u32x4 w = load16(qv + (kk * 4 + g) * 8);
+            if (!live) w = u32x4{0, 0, 0, 0};
+            qop[qt][kk] = __builtin_bit_cast(bf16x8, w);
+        }
+    }
+    __syncthreads();  // block table staged
+    const bool holes = s_holes != 0 || nblk_vis > mbpr;
+
+    f32x4 acc[QT][NT];
+    f32x4 lsum[QT];
+    float m[QT];
+    int limit[QT];  // last key visible to query row tw + 16 qt + j
+    const bf16x8 ones = __builtin_bit_cast(
+        bf16x8, u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        // A finite "no key yet" reference: exp2(s - m) needs no -inf guard, the first half
+        // with a visible key always outgrows it (rescale with alpha = 0), and fully masked
+        // scores (-inf) still give probability 0.
+        m[qt] = kMaxInit;
+        lsum[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        limit[qt] = prefix + tw + qt * 16 + j;
+#pragma unroll
+        for (int n = 0; n < NT; ++n) acc[qt][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    // ---- pipeline pieces (h = 32-key half of a 64-key tile) ----
+    // S^T of one half: st[kbl][qt] lane (j, g) holds keys 32h + 16 kbl + 4g + r.
+    auto qk_half = [&](const __bf16* lk, int h, f32x4 (&st)[2][QT])
+                       __attribute__((always_inline)) {
+#pragma unroll
+        for (int kbl = 0; kbl < 2; ++kbl) {
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) st[kbl][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < S; ++kk) {
+                const bf16x8 kop = __builtin_bit_cast(
+                    bf16x8, *reinterpret_cast<const u32x4*>(lk + (h * 32 + kbl * 16) * D +
+                                                            koff[kk]));
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt)
+                    st[kbl][qt] = mfma16x16x32(kop, qop[qt][kk], st[kbl][qt]);
+            }
+        }
+    };
+    // Causal / validity mask of one half; key0 = first key of the half, vbits = validity
+    // of its 32 keys.
+    auto mask_half = [&](f32x4 (&st)[2][QT], int key0, uint32_t vbits)
+                         __attribute__((always_inline)) {
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+#pragma unroll
+            for (int kbl = 0; kbl < 2; ++kbl) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int kt = kbl * 16 + g * 4 + r;
+                    const bool ok = key0 + kt <= limit[qt] && ((vbits >> kt) & 1u);
+                    st[kbl][qt][r] = ok ? st[kbl][qt][r] : kNegInf;
+                }
+            }
+        }
+    };
+    // Row max of one half (scaled, log2 units); returns whether any row outgrew the slack.
+    auto max_half = [&](const f32x4 (&st)[2][QT], float (&mt)[QT])
+                        __attribute__((always_inline)) {
+        bool grow = false;
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+            float x = fmaxf(fmaxf(fmaxf(st[0][qt][0], st[0][qt][1]),
+                                  fmaxf(st[0][qt][2], st[0][qt][3])),
+                            fmaxf(fmaxf(st[1][qt][0], st[1][qt][1]),
+                                  fmaxf(st[1][qt][2], st[1][qt][3])));
+            x = wave_max_swap16_32(x) * scale_log2;
+            mt[qt] = x;
+            grow |= x > m[qt] + kRescaleSlack;
+        }
+        return grow;
+    };
+    auto rescale = [&](bool grow, const float (&mt)[QT]) __attribute__((always_inline)) {
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) {
+                const float m_new = fmaxf(m[qt], mt[qt]);
+                const float alpha = __builtin_amdgcn_exp2f(m[qt] - m_new);
+                lsum[qt] = lsum[qt] * alpha;
+#pragma unroll
+                for (int n = 0; n < NT; ++n) acc[qt][n] = acc[qt][n] * alpha;
+                m[qt] = m_new;
+            }
+        }
+    };
+    // P^T operands of one half (keys T(g, e) = 16(e/4) + 4g + e%4) and their row sums.
+    auto exp_half = [&](const f32x4 (&st)[2][QT], bf16x8 (&pop)[QT])
+                        __attribute__((always_inline)) {
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+            const float mneg = -m[qt];
+            u32x4 pw;
+#pragma unroll
+            for (int x = 0; x < 4; ++x) {
+                const int e = 2 * x;
+                const float p0 = __builtin_amdgcn_exp2f(
+                    __builtin_fmaf(st[e >> 2][qt][e & 3], scale_log2, mneg));
+                const float p1 = __builtin_amdgcn_exp2f(
+                    __builtin_fmaf(st[(e + 1) >> 2][qt][(e + 1) & 3], scale_log2, mneg));
+                pw[x] = pack_bf16x2(p0, p1);
+            }
+            pop[qt] = __builtin_bit_cast(bf16x8, pw);
+        }
+    };
+    auto sum_half = [&](const bf16x8 (&pop)[QT]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) lsum[qt] = mfma16x16x32(ones, pop[qt], lsum[qt]);
+    };
+    auto pv_half = [&](const __bf16* lv, int h, const bf16x8 (&pop)[QT])
+                       __attribute__((always_inline)) {
+        using v4s = short __attribute__((ext_vector_type(4)));
+        using v8s = short __attribute__((ext_vector_type(8)));
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+            const __bf16* p0 = lv + h * 32 * D + voff[n];
+            const v4s a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) v4s*)(p0));
+            const v4s b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) v4s*)(p0 + 16 * D));
+            const v8s ab = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+            const bf16x8 vop = __builtin_bit_cast(bf16x8, ab);
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) acc[qt][n] = mfma16x16x32(vop, pop[qt], acc[qt][n]);
+        }
+    };
+    auto vbits_of = [&](const uint8_t* lvalid, int h) __attribute__((always_inline)) {
+        const uint64_t v = __builtin_amdgcn_ballot_w64(lvalid[lane] != 0);
+        return static_cast<uint32_t>(v >> (32 * h));
+    };
+
+    // Interleave patterns for the two pipeline phases (igrouplp masks: 0x8 MFMA, 0x100 DS
+    // read, 0x402 VALU incl. transcendental). X: 2 MFMAs of the next half's QK per K read,
+    // with the exp work of the current half spread between them. Y: one V^T operand (two
+    // transposing reads) per QT MFMAs, with the next half's mask / max work in between.
+    constexpr int kXGroups = 2 * S;            // K operand reads in a QK half
+    constexpr int kXValu = (QT * 20 + kXGroups - 1) / kXGroups;
+    constexpr int kYValu = (QT * 16 + NT - 1) / NT;
+    constexpr int kXPre = 2;  // K operand reads issued ahead of the MFMAs using them
+    constexpr int kYPre = 2;  // V^T operands read ahead
+    auto interleave_x = [&]() __attribute__((always_inline)) {
+        __builtin_amdgcn_sched_group_barrier(0x100, kXPre, 0);
+#pragma unroll
+        for (int i = 0; i < kXGroups; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x402, kXValu, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, QT, 0);
+            if (i + kXPre < kXGroups) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+    };
+    auto interleave_y = [&]() __attribute__((always_inline)) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * kYPre, 0);
+#pragma unroll
+        for (int i = 0; i < NT; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x402, kYValu, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, QT, 0);
+            if (i + kYPre < NT) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
+    };
+
+    f32x4 sc[2][QT];  // S of the half being exponentiated
+    f32x4 sn[2][QT];  // S of the next half
+    bf16x8 pop[QT];
+    float mt[QT];
+
+    // Prologue: tiles 0 and 1 in flight, S of tile 0 / half 0 formed, masked and maxed.
+    stage(0, lds_k0, lds_v0, lds_valid0);
+    if (ntiles > 1) {
+        stage(1, lds_k1, lds_v1, lds_valid1);
+        __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * NL));  // tile 0 landed (vmcnt <= tile 1's)
+    } else {
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+    }
+    __syncthreads();
+    qk_half(lds_k0, 0, sc);
+    mask_half(sc, 0, vbits_of(lds_valid0, 0));
+    rescale(max_half(sc, mt), mt);
+
+    // One tile step. Entering: sc = S of (tile t, half 0), already masked and rescaled for.
+    // kLast: tile t is the last one (no next tile to start).
+    auto step = [&](int t, auto cur, auto nxt, auto ld, auto mask_tag, auto last_tag)
+                    __attribute__((always_inline)) {
+        constexpr int BC = decltype(cur)::value;
+        constexpr int BN = decltype(nxt)::value;
+        constexpr int BL = decltype(ld)::value;
+        constexpr bool kMask = decltype(mask_tag)::value;
+        constexpr bool kLast = decltype(last_tag)::value;
+        const __bf16* kc = BC == 0 ? lds_k0 : (BC == 1 ? lds_k1 : lds_k2);
+        const __bf16* vc = BC == 0 ? lds_v0 : (BC == 1 ? lds_v1 : lds_v2);
+        const uint8_t* valc = BC == 0 ? lds_valid0 : (BC == 1 ? lds_valid1 : lds_valid2);
+        const __bf16* kn = BN == 0 ? lds_k0 : (BN == 1 ? lds_k1 : lds_k2);
+        const uint8_t* valn = BN == 0 ? lds_valid0 : (BN == 1 ? lds_valid1 : lds_valid2);
+        __bf16* kl = BL == 0 ? lds_k0 : (BL == 1 ? lds_k1 : lds_k2);
+        __bf16* vl = BL == 0 ? lds_v0 : (BL == 1 ? lds_v1 : lds_v2);
+        uint8_t* vall = BL == 0 ? lds_valid0 : (BL == 1 ? lds_valid1 : lds_valid2);
+        const int key0 = t * kKeysPerTile;
+
+        // X: exp of (t, 0) || QK of (t, 1)
+        __builtin_amdgcn_sched_barrier(0);
+        exp_half(sc, pop);
+        qk_half(kc, 1, sn);
+        sum_half(pop);
+        interleave_x();
+        // Y: PV of (t, 0) || mask + max of (t, 1)
+        __builtin_amdgcn_sched_barrier(0);
+        pv_half(vc, 0, pop);
+        if constexpr (kMask) mask_half(sn, key0 + 32, vbits_of(valc, 1));
+        const bool grow1 = max_half(sn, mt);
+        interleave_y();
+        __builtin_amdgcn_sched_barrier(0);
+        rescale(grow1, mt);
+        if constexpr (!kLast) {
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // this wavefront's loads of tile t+1 landed
+            __syncthreads();                     // ... and everyone's; tile t-1 is free
+            if (t + 2 < ntiles) stage(t + 2, kl, vl, vall);
+        }
+        // X: exp of (t, 1) || QK of (t+1, 0)
+        __builtin_amdgcn_sched_barrier(0);
+        exp_half(sn, pop);
+        if constexpr (!kLast) qk_half(kn, 0, sc);
+        sum_half(pop);
+        if constexpr (!kLast) interleave_x();
+        // Y: PV of (t, 1) || mask + max of (t+1, 0)
+        __builtin_amdgcn_sched_barrier(0);
+        pv_half(vc, 1, pop);
+        if constexpr (!kLast) {
+            if constexpr (kMask) mask_half(sc, key0 + kKeysPerTile, vbits_of(valn, 0));
+            const bool grow0 = max_half(sc, mt);
+            interleave_y();
+            __builtin_amdgcn_sched_barrier(0);
+            rescale(grow0, mt);
+        }
+    };
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    using B2 = std::integral_constant<int, 2>;
+    using F = std::false_type;
+    using T = std::true_type;
+
+    // Steps whose tiles t and t+1 lie wholly below the workgroup's first query row need no
+    // mask (unless the table has holes); they run in triples so buffer roles stay static.
+    const int mask_free_tiles = holes ? 0 : (prefix + t0 + 1) / kKeysPerTile;
+    const int mf_steps = max(0, min(ntiles - 1, mask_free_tiles - 1));
+    int t = 0;
+    for (; t + 3 <= mf_steps; t += 3) {
+        step(t, B0{}, B1{}, B2{}, F{}, F{});
+        step(t + 1, B1{}, B2{}, B0{}, F{}, F{});
+        step(t + 2, B2{}, B0{}, B1{}, F{}, F{});
+    }
+    for (;;) {
+        if (t >= ntiles - 1) break;
+        step(t, B0{}, B1{}, B2{}, T{}, F{});
+        ++t;
+        if (t >= ntiles - 1) break;
+        step(t, B1{}, B2{}, B0{}, T{}, F{});
+        ++t;
+        if (t >= ntiles - 1) break;
+        step(t, B2{}, B0{}, B1{}, T{}, F{});
+        ++t;
+    }
+    switch (t % 3) {
+        case 0: step(t, B0{}, B1{}, B2{}, T{}, T{}); break;
+        case 1: step(t, B1{}, B2{}, B0{}, T{}, T{}); break;
+        default: step(t, B2{}, B0{}, B1{}, T{}, T{}); break;
+    }
+
+    // Epilogue: lane (j, g) holds O[row][16n + 4g + r] = acc[qt][n][r].
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        const float l_tot = lsum[qt][0];
+        const int tq = tw + qt * 16 + j;
+        if (tq >= rows) continue;
+        const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+        __bf16* o = out + (static_cast<int64_t>(qb + tq) * hq + q_head) * D;
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+            u32x2 w;
+            w[0] = pack_bf16x2(acc[qt][n][0] * inv, acc[qt][n][1] * inv);
+            w[1] = pack_bf16x2(acc[qt][n][2] * inv, acc[qt][n][3] * inv);
+            *reinterpret_cast<u32x2*>(o + 16 * n + 4 * g) = w;
+        }
+    }
+}
+
 struct PrefillLayout {
     size_t counts_off, zero_off, tiles_off, dec_off, decode_ws_off, total;
     int max_tiles;
@@ -553,8 +1033,9 @@ struct PrefillLayout {
 size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
 int tile_tokens_for(int head_dim, int G) {
-    const int qw = head_dim <= 128 ? 32 : 16;
-    return (kWaves / heads_per_wg(G)) * qw;
+    if (pipe_head_dim(head_dim))
+        return (PipeShape<64, kPipeQT>::kWaves / heads_per_wg(G)) * PipeShape<64, kPipeQT>::kRows;
+    return (kWaves / heads_per_wg(G)) * PrefillShape<256>::kQW;
 }
 
 PrefillLayout prefill_layout(int batch_size, int total_query_tokens, int max_blocks_per_req,
@@ -590,12 +1071,22 @@ hipError_t launch_tiles(const void* q, const void* k_cache, const void* v_cache,
     const int U = hkv * (G / heads_per_wg(G));
     const int64_t grid = static_cast<int64_t>(max_tiles) * U;
     const float scale_log2 = kLog2e / sqrtf(static_cast<float>(D));
-    prefill_tile_kernel<D><<<static_cast<unsigned>(grid), kThreads, 0, stream>>>(
-        static_cast<const __bf16*>(q), static_cast<const __bf16*>(k_cache),
-        static_cast<const __bf16*>(v_cache), block_table, qsl, context_lens,
-        static_cast<__bf16*>(output), counts, tiles, static_cast<const __bf16*>(zero_row),
-        total_query_tokens, mbpr, hq, hkv, block_size, scale_log2);
-    return hipGetLastError();
+    if constexpr (pipe_head_dim(D)) {
+        prefill_pipe_kernel<D, kPipeQT>
+            <<<static_cast<unsigned>(grid), PipeShape<D, kPipeQT>::kThreads, 0, stream>>>(
+            static_cast<const __bf16*>(q), static_cast<const __bf16*>(k_cache),
+            static_cast<const __bf16*>(v_cache), block_table, qsl, context_lens,
+            static_cast<__bf16*>(output), counts, tiles, total_query_tokens, mbpr, hq, hkv,
+            scale_log2);
+        return hipGetLastError();
+    } else {
+        prefill_tile_kernel<D><<<static_cast<unsigned>(grid), kThreads, 0, stream>>>(
+            static_cast<const __bf16*>(q), static_cast<const __bf16*>(k_cache),
+            static_cast<const __bf16*>(v_cache), block_table, qsl, context_lens,
+            static_cast<__bf16*>(output), counts, tiles, static_cast<const __bf16*>(zero_row),
+            total_query_tokens, mbpr, hq, hkv, block_size, scale_log2);
+        return hipGetLastError();
+    }
 }
 
 }  // namespace
