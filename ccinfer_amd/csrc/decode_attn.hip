@@ -10,6 +10,12 @@
 //   positions (a multiple of 32, at most 2048). All Hq/Hkv query heads of the GQA group are
 //   handled by the same wavefront, so every K/V byte of a (request, kv_head) is read from
 //   HBM exactly once.
+//   Split length: plain decode batches of 4..256 requests use the balanced plan -- every
+//   wavefront reads the batch's context lengths, derives the split length from the actual
+//   total (so ragged batches get equal-length splits instead of splits sized for the longest
+//   possible context) and finds its (request, split) with a wave-wide prefix scan; the merge
+//   kernel repeats the same computation. Other batches use a fixed split length chosen on
+//   the host from the longest possible context.
 //
 // Per 32-token chunk (two 16-token cache blocks) the wavefront computes
 //   S^T[token][head] = K[token][:] . Q^T           (v_mfma_f32_16x16x32_bf16, D/32 steps/block)
@@ -35,6 +41,8 @@
 // would need agent-scope release/acquire fences, which on gfx950 write back and invalidate
 // the whole L2 and cost far more than the extra launch). A row whose context fits one split
 // is written directly by the first kernel and skipped by the merge.
+#include <algorithm>
+
 #include "attn_common.hpp"
 #include "kernels.hpp"
 
@@ -47,6 +55,7 @@ constexpr int kWavesPerGroup = 4;
 constexpr int kMaxSplitTokens = 2048;  // 128 blocks: two table entries per lane
 // Wavefronts the split plan aims for: two resident per SIMD on 1024 SIMDs, two rounds.
 constexpr int64_t kTargetWaves = 4096;
+constexpr int kBalancedMinItems = 4;
 
 struct ItemArgs {
     int num_items;
@@ -85,6 +94,90 @@ __device__ __forceinline__ int effective_ctx(int ctx, int mbpr, int zero_invalid
     }
     // Prefill semantics: positions past the table row are invalid, not an error.
     return ctx < cap ? ctx : cap;
+}
+
+// ---- balanced split plan (evaluated identically by every wavefront) ----
+// C = total 32-token chunks of the batch's valid contexts; every split covers
+// T = clamp(ceil(C / W), 1, kMaxSplitTokens / kChunk) chunks, so all wavefronts stream about
+// the same number of tokens whatever the spread of context lengths. Request r gets
+// ceil(c_r / T) splits (one zero-writing split if its context is invalid), laid out
+// request-major in split slots 0, 1, ... of each kv_head.
+struct BalancedSplit {
+    int req;          // request of the split
+    int split;        // split index within the request
+    int nsplit;       // splits of the request
+    int first_slot;   // slot of the request's first split
+    int split_tokens; // T * kChunk
+    int ctx;          // effective context of the request (-1: invalid)
+};
+
+__device__ __forceinline__ int wave_inclusive_scan(int v, int lane) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int u = __shfl_up(v, off);
+        if (lane >= off) v += u;
+    }
+    return v;
+}
+
+__device__ __forceinline__ int wave_sum_i32(int v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+// Finds the split of slot `slot` (by_request == false) or the splits of request `slot`
+// (by_request == true). Returns false when the slot is past the last split.
+__device__ bool balanced_lookup(const int32_t* __restrict__ context_lens, int B, int mbpr,
+                                int zero_invalid, int W, int slot, bool by_request, int lane,
+                                BalancedSplit* out) {
+    const int rounds = (B + 63) / 64;  // B <= kBalancedMaxItems
+    int cr[kBalancedMaxItems / 64];
+    int ectx[kBalancedMaxItems / 64];
+    bool valid[kBalancedMaxItems / 64];
+    int total = 0;
+#pragma unroll
+    for (int k = 0; k < kBalancedMaxItems / 64; ++k) {
+        cr[k] = 0;
+        ectx[k] = -1;
+        valid[k] = false;
+        if (k < rounds) {
+            const int r = k * 64 + lane;
+            if (r < B) {
+                const int ctx = effective_ctx(context_lens[r], mbpr, zero_invalid);
+                ectx[k] = ctx;
+                valid[k] = ctx >= 0;
+                cr[k] = ctx > 0 ? (ctx + kChunk - 1) / kChunk : 0;
+            }
+            total += cr[k];
+        }
+    }
+    const int C = wave_sum_i32(total);
+    int T = (C + W - 1) / W;
+    T = T < 1 ? 1 : (T > kMaxSplitTokens / kChunk ? kMaxSplitTokens / kChunk : T);
+    int carry = 0;
+#pragma unroll
+    for (int k = 0; k < kBalancedMaxItems / 64; ++k) {
+        if (k >= rounds) break;
+        const int r = k * 64 + lane;
+        const int sr = r < B ? (valid[k] && cr[k] > 0 ? (cr[k] + T - 1) / T : 1) : 0;
+        const int incl = wave_inclusive_scan(sr, lane) + carry;
+        const int excl = incl - sr;
+        const bool hit = by_request ? (r == slot) : (slot >= excl && slot < incl);
+        const uint64_t m = __builtin_amdgcn_ballot_w64(hit);
+        if (m != 0) {
+            const int src = __builtin_ffsll(static_cast<long long>(m)) - 1;
+            out->req = k * 64 + src;
+            out->first_slot = __builtin_amdgcn_readlane(excl, src);
+            out->nsplit = __builtin_amdgcn_readlane(sr, src);
+            out->split = slot - out->first_slot;
+            out->split_tokens = T * kChunk;
+            out->ctx = __builtin_amdgcn_readlane(ectx[k], src);
+            return true;
+        }
+        carry = __builtin_amdgcn_readlane(incl, 63);
+    }
+    return false;
 }
 
 template <int D>
@@ -208,12 +301,14 @@ __device__ __forceinline__ void consume_chunk(SoftmaxState<D>& st, ChunkRegs<D>&
 }
 
 // Log-sum-exp merge of the ns splits of one (item, head) row by one wavefront; writes bf16.
-// Split weights are computed 64 at a time, one split per lane, and broadcast with readlane;
-// every lane then accumulates its D/64 dims over the splits (independent loads).
+// Split weights are computed one split per lane and broadcast with readlane; every lane then
+// accumulates its D/64 dims over the splits, 8 splits' partial rows loaded before any is
+// used so a row costs a couple of memory latencies, not one per split.
 template <int D>
 __device__ void merge_row(const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
                           int64_t base, int ns, float eps, __bf16* __restrict__ o, int lane) {
     constexpr int kPer = D / 64;
+    constexpr int kBatch = 8;
     float mmax = kNegInf;
     for (int s = lane; s < ns; s += 64) mmax = fmaxf(mmax, ws_ml[(base + s) * 2]);
 #pragma unroll
@@ -232,10 +327,23 @@ __device__ void merge_row(const float* __restrict__ ws_o, const float* __restric
             }
             const int nt = min(64, ns - sb);
             const float* po = ws_o + (base + sb) * D + lane * kPer;
-            for (int t = 0; t < nt; ++t) {
-                const float wt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), t));
+            for (int t0 = 0; t0 < nt; t0 += kBatch) {
+                float v[kBatch][kPer];
 #pragma unroll
-                for (int x = 0; x < kPer; ++x) acc[x] += po[t * D + x] * wt;
+                for (int u = 0; u < kBatch; ++u) {
+                    const int t = min(t0 + u, nt - 1);  // clamped: the weight of a repeat is 0
+#pragma unroll
+                    for (int x = 0; x < kPer; ++x) v[u][x] = po[t * D + x];
+                }
+#pragma unroll
+                for (int u = 0; u < kBatch; ++u) {
+                    const int t = t0 + u;
+                    const float wt = t < nt ? __int_as_float(__builtin_amdgcn_readlane(
+                                                  __float_as_int(w), t & 63))
+                                            : 0.f;
+#pragma unroll
+                    for (int x = 0; x < kPer; ++x) acc[x] += v[u][x] * wt;
+                }
             }
         }
     }
@@ -252,7 +360,7 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     const __bf16* __restrict__ v_cache, const int32_t* __restrict__ block_table,
     const int32_t* __restrict__ context_lens, __bf16* __restrict__ out, float* __restrict__ ws_o,
     float* __restrict__ ws_ml, ItemArgs items, int mbpr, int hq, int hkv, int splits,
-    int split_tokens, float scale_log2) {
+    int split_tokens, int balanced_w, int slots, float scale_log2) {
     constexpr int S = DecodeShape<D>::kSteps;
     constexpr int NV = DecodeShape<D>::kNV;
     const int lane = threadIdx.x & 63;
@@ -263,12 +371,28 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     // slot next to each other), which measured 10-20% faster than split-fastest ordering.
     const int h = wi % hkv;
     const int rest = wi / hkv;
-    const int s = rest % splits;
-    const int item = rest / splits;
+    int s, item, ns_bal = 0, first_slot = 0, ctx_bal = 0;
+    if (balanced_w > 0) {
+        BalancedSplit bs;
+        if (rest >= slots ||
+            !balanced_lookup(context_lens, items.num_items, mbpr, items.zero_invalid,
+                             balanced_w, rest, false, lane, &bs))
+            return;
+        item = bs.req;
+        s = bs.split;
+        ns_bal = bs.nsplit;
+        first_slot = bs.first_slot;
+        split_tokens = bs.split_tokens;
+        ctx_bal = bs.ctx;
+    } else {
+        s = rest % splits;
+        item = rest / splits;
+    }
 
     int req, qrow;
     if (!resolve_item(items, item, &req, &qrow)) return;
-    const int ctx = effective_ctx(context_lens[req], mbpr, items.zero_invalid);
+    const int ctx =
+        balanced_w > 0 ? ctx_bal : effective_ctx(context_lens[req], mbpr, items.zero_invalid);
     const int G = hq / hkv;
     const int j = lane & 15;
     const int g = lane >> 4;
@@ -285,7 +409,7 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     const int begin = s * split_tokens;
     if (begin >= ctx) return;
     const int end = min(ctx, begin + split_tokens);
-    const int ns = (ctx + split_tokens - 1) / split_tokens;  // splits with work for this row
+    const int ns = balanced_w > 0 ? ns_bal : (ctx + split_tokens - 1) / split_tokens;
     const int32_t* req_blocks = block_table + static_cast<int64_t>(req) * mbpr;
 
     // Block ids of this split, one per lane (two registers cover 128 blocks).
@@ -359,7 +483,10 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
 
     // Partial of this split; decode_merge_kernel combines the splits.
     if (!live) return;
-    const int64_t slot = (static_cast<int64_t>(item) * hq + head) * splits + s;
+    // Partials of one row are contiguous over its splits.
+    const int64_t slot = balanced_w > 0
+                             ? static_cast<int64_t>(head) * slots + first_slot + s
+                             : (static_cast<int64_t>(item) * hq + head) * splits + s;
     float* po = ws_o + slot * D;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -387,7 +514,7 @@ template <int D>
 __global__ __launch_bounds__(256) void decode_merge_kernel(
     const int32_t* __restrict__ context_lens, __bf16* __restrict__ out,
     const float* __restrict__ ws_o, const float* __restrict__ ws_ml, ItemArgs items, int mbpr,
-    int hq, int splits, int split_tokens) {
+    int hq, int splits, int split_tokens, int balanced_w, int slots) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wi = blockIdx.x * kWavesPerGroup + wave;
@@ -397,9 +524,21 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(
     if (!resolve_item(items, item, &req, &qrow)) return;
     const int ctx = effective_ctx(context_lens[req], mbpr, items.zero_invalid);
     if (ctx < 0) return;  // zeros already written (decode) / row untouched (prefill)
-    const int ns = (ctx + split_tokens - 1) / split_tokens;
+    int ns;
+    int64_t base;
+    if (balanced_w > 0) {
+        BalancedSplit bs;
+        if (!balanced_lookup(context_lens, items.num_items, mbpr, items.zero_invalid, balanced_w,
+                             item, true, lane, &bs))
+            return;
+        ns = bs.nsplit;
+        base = static_cast<int64_t>(head) * slots + bs.first_slot;
+    } else {
+        ns = (ctx + split_tokens - 1) / split_tokens;
+        base = (static_cast<int64_t>(item) * hq + head) * splits;
+    }
     if (ns <= 1) return;  // written directly by the split kernel
-    merge_row<D>(ws_o, ws_ml, (static_cast<int64_t>(item) * hq + head) * splits, ns, items.eps,
+    merge_row<D>(ws_o, ws_ml, base, ns, items.eps,
                  out + (static_cast<int64_t>(qrow) * hq + head) * D, lane);
 }
 
@@ -408,15 +547,17 @@ struct DecodeWs {
     float* ml;
 };
 
-DecodeWs carve(void* workspace, int num_items, int hq, int hkv, int d, int splits) {
+// Partial rows of the plan: (item, q_head, split) in fixed mode, (q_head, slot) balanced.
+size_t partial_rows(int num_items, int hq, const DecodePlan& plan) {
+    return plan.balanced ? static_cast<size_t>(hq) * plan.slots
+                         : static_cast<size_t>(num_items) * hq * plan.splits;
+}
+
+DecodeWs carve(void* workspace, size_t rows, int d) {
     DecodeWs w{};
     char* p = static_cast<char*>(workspace);
-    const size_t o_bytes = static_cast<size_t>(num_items) * hq * splits * d * sizeof(float);
-    const size_t ml_bytes = static_cast<size_t>(num_items) * hq * splits * 2 * sizeof(float);
     w.o = reinterpret_cast<float*>(p);
-    w.ml = reinterpret_cast<float*>(p + o_bytes);
-    (void)ml_bytes;
-    (void)hkv;
+    w.ml = reinterpret_cast<float*>(p + rows * d * sizeof(float));
     return w;
 }
 
@@ -426,35 +567,56 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
                          const ItemArgs& it, int mbpr, int hq, int hkv, const DecodePlan& plan,
                          void* workspace, hipStream_t stream) {
     const float scale_log2 = kLog2e / sqrtf(static_cast<float>(D));
-    const int64_t waves = static_cast<int64_t>(it.num_items) * hkv * plan.splits;
+    const int64_t waves = plan.balanced
+                              ? static_cast<int64_t>(plan.slots) * hkv
+                              : static_cast<int64_t>(it.num_items) * hkv * plan.splits;
     const int grid = static_cast<int>((waves + kWavesPerGroup - 1) / kWavesPerGroup);
+    const bool merge = plan.balanced || plan.splits > 1;
     DecodeWs w{};
-    if (plan.splits > 1) w = carve(workspace, it.num_items, hq, hkv, D, plan.splits);
+    if (merge) w = carve(workspace, partial_rows(it.num_items, hq, plan), D);
+    const int bw = plan.balanced ? plan.wave_target : 0;
     decode_split_kernel<D><<<grid, 256, 0, stream>>>(
         static_cast<const __bf16*>(q), static_cast<const __bf16*>(k_cache),
         static_cast<const __bf16*>(v_cache), block_table, context_lens,
         static_cast<__bf16*>(output), w.o, w.ml, it, mbpr, hq, hkv, plan.splits,
-        plan.split_tokens, scale_log2);
+        plan.split_tokens, bw, plan.slots, scale_log2);
     hipError_t err = hipGetLastError();
-    if (err != hipSuccess || plan.splits == 1) return err;
+    if (err != hipSuccess || !merge) return err;
     const int64_t rows = static_cast<int64_t>(it.num_items) * hq;
     const int mgrid = static_cast<int>((rows + kWavesPerGroup - 1) / kWavesPerGroup);
     decode_merge_kernel<D><<<mgrid, 256, 0, stream>>>(context_lens, static_cast<__bf16*>(output),
                                                       w.o, w.ml, it, mbpr, hq, plan.splits,
-                                                      plan.split_tokens);
+                                                      plan.split_tokens, bw, plan.slots);
     return hipGetLastError();
 }
 
 }  // namespace
 
-DecodePlan plan_decode(int num_items, int num_kv_heads, int max_ctx) {
+DecodePlan plan_decode(int num_items, int num_kv_heads, int max_ctx, bool allow_balanced) {
     DecodePlan p;
     const int chunks = max_ctx > 0 ? (max_ctx + kChunk - 1) / kChunk : 1;
+    constexpr int kMaxChunksPerSplit = kMaxSplitTokens / kChunk;
+    // Small batches keep the fixed plan: their splits are already even and the on-device
+    // plan would only add its lookup to a latency-bound launch.
+    if (allow_balanced && num_items >= kBalancedMinItems &&
+        num_items <= kBalancedMaxItems && chunks > 1) {
+        p.balanced = true;
+        p.wave_target = static_cast<int>(std::max<int64_t>(1, kTargetWaves / num_kv_heads));
+        // Splits per kv_head: at most C/T + B with T >= C/W (or, with T at its cap,
+        // B * chunks / cap + B), and never more than one per chunk.
+        const int64_t capped =
+            static_cast<int64_t>(num_items) * ((chunks + kMaxChunksPerSplit - 1) / kMaxChunksPerSplit);
+        const int64_t bound = std::max<int64_t>(p.wave_target, capped) + num_items;
+        p.slots = static_cast<int>(std::min<int64_t>(bound, static_cast<int64_t>(num_items) * chunks));
+        p.splits = 0;
+        p.split_tokens = 0;
+        return p;
+    }
     const int64_t target_waves = kTargetWaves;
     const int64_t total = static_cast<int64_t>(num_items) * num_kv_heads * chunks;
     int64_t cpw = (total + target_waves - 1) / target_waves;
     if (cpw < 1) cpw = 1;
-    if (cpw > kMaxSplitTokens / kChunk) cpw = kMaxSplitTokens / kChunk;
+    if (cpw > kMaxChunksPerSplit) cpw = kMaxChunksPerSplit;
     if (cpw > chunks) cpw = chunks;
     p.split_tokens = static_cast<int>(cpw) * kChunk;
     p.splits = (chunks + static_cast<int>(cpw) - 1) / static_cast<int>(cpw);
@@ -463,9 +625,9 @@ DecodePlan plan_decode(int num_items, int num_kv_heads, int max_ctx) {
 
 size_t decode_workspace_bytes(int num_items, int num_q_heads, int head_dim,
                               const DecodePlan& plan) {
-    if (plan.splits <= 1) return 0;
-    const size_t rows = static_cast<size_t>(num_items) * num_q_heads * plan.splits;
-    return rows * (head_dim + 2) * sizeof(float);  // partial O + (m, l) per row and split
+    if (!plan.balanced && plan.splits <= 1) return 0;
+    // partial O + (m, l) per partial row
+    return partial_rows(num_items, num_q_heads, plan) * (head_dim + 2) * sizeof(float);
 }
 
 bool decode_fast_supported(int num_q_heads, int num_kv_heads, int head_dim, int block_size) {

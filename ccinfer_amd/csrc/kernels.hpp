@@ -16,13 +16,25 @@ hipError_t write_kv_cache(const void* k_new, const void* v_new, void* k_cache, v
 
 // ---- decode ---------------------------------------------------------------
 // Split-KV plan: `splits` partitions of `split_tokens` tokens per (request, kv_head).
+// Split-KV plan. Fixed mode: `splits` partitions of `split_tokens` tokens per (request,
+// kv_head), sized from the longest possible context. Balanced mode (plain decode batches of
+// up to kBalancedMaxItems requests): the split length is chosen on the device from the
+// batch's actual total context so that every wavefront streams about the same number of
+// tokens; `slots` bounds the number of splits per kv_head and `wave_target` is the number
+// of wavefronts per kv_head the split length aims for.
 struct DecodePlan {
     int splits = 1;
     int split_tokens = 0;  // multiple of 32
+    bool balanced = false;
+    int slots = 0;
+    int wave_target = 0;
 };
 
-// Returns the plan for a batch whose longest context is max_ctx tokens.
-DecodePlan plan_decode(int num_items, int num_kv_heads, int max_ctx);
+constexpr int kBalancedMaxItems = 256;
+
+// Returns the plan for a batch whose longest context is max_ctx tokens. allow_balanced:
+// the items are plain decode requests (item i = request i), so the balanced mode may be used.
+DecodePlan plan_decode(int num_items, int num_kv_heads, int max_ctx, bool allow_balanced);
 
 // Scratch bytes the split-KV decode needs for `num_items` query rows.
 size_t decode_workspace_bytes(int num_items, int num_q_heads, int head_dim,
