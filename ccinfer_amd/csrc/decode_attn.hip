@@ -10,12 +10,13 @@
 //   positions (a multiple of 32, at most 2048). All Hq/Hkv query heads of the GQA group are
 //   handled by the same wavefront, so every K/V byte of a (request, kv_head) is read from
 //   HBM exactly once.
-//   Split length: plain decode batches of 4..256 requests use the balanced plan -- every
-//   wavefront reads the batch's context lengths, derives the split length from the actual
-//   total (so ragged batches get equal-length splits instead of splits sized for the longest
-//   possible context) and finds its (request, split) with a wave-wide prefix scan; the merge
-//   kernel repeats the same computation. Other batches use a fixed split length chosen on
-//   the host from the longest possible context.
+//   Split length: batches of 4..256 items use the balanced plan -- every wavefront reads the
+//   items' context lengths, derives the split length from the actual total (so ragged
+//   batches get equal-length splits instead of splits sized for the longest possible
+//   context) and finds its (item, split) with a wave-wide prefix scan; the merge kernel
+//   repeats the same computation. This also covers the decode items of a mixed prefill
+//   batch, whose list and count the prefill planner writes on the device. Other batches use
+//   a fixed split length chosen on the host from the longest possible context.
 //
 // Per 32-token chunk (two 16-token cache blocks) the wavefront computes
 //   S^T[token][head] = K[token][:] . Q^T           (v_mfma_f32_16x16x32_bf16, D/32 steps/block)
@@ -128,9 +129,14 @@ __device__ __forceinline__ int wave_sum_i32(int v) {
 
 // Finds the split of slot `slot` (by_request == false) or the splits of request `slot`
 // (by_request == true). Returns false when the slot is past the last split.
-__device__ bool balanced_lookup(const int32_t* __restrict__ context_lens, int B, int mbpr,
-                                int zero_invalid, int W, int slot, bool by_request, int lane,
+__device__ bool balanced_lookup(const int32_t* __restrict__ context_lens, const ItemArgs& items,
+                                int mbpr, int W, int slot, bool by_request, int lane,
                                 BalancedSplit* out) {
+    // Items (query rows) in order; item i is request item_req[i] when a list is given, and
+    // items past the device-side count have no splits.
+    int B = items.num_items;
+    if (items.item_count != nullptr) B = min(B, *items.item_count);
+    const int zero_invalid = items.zero_invalid;
     const int rounds = (B + 63) / 64;  // B <= kBalancedMaxItems
     int cr[kBalancedMaxItems / 64];
     int ectx[kBalancedMaxItems / 64];
@@ -144,7 +150,8 @@ __device__ bool balanced_lookup(const int32_t* __restrict__ context_lens, int B,
         if (k < rounds) {
             const int r = k * 64 + lane;
             if (r < B) {
-                const int ctx = effective_ctx(context_lens[r], mbpr, zero_invalid);
+                const int req = items.item_req != nullptr ? items.item_req[r] : r;
+                const int ctx = effective_ctx(context_lens[req], mbpr, zero_invalid);
                 ectx[k] = ctx;
                 valid[k] = ctx >= 0;
                 cr[k] = ctx > 0 ? (ctx + kChunk - 1) / kChunk : 0;
@@ -375,8 +382,7 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     if (balanced_w > 0) {
         BalancedSplit bs;
         if (rest >= slots ||
-            !balanced_lookup(context_lens, items.num_items, mbpr, items.zero_invalid,
-                             balanced_w, rest, false, lane, &bs))
+            !balanced_lookup(context_lens, items, mbpr, balanced_w, rest, false, lane, &bs))
             return;
         item = bs.req;
         s = bs.split;
@@ -528,8 +534,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(
     int64_t base;
     if (balanced_w > 0) {
         BalancedSplit bs;
-        if (!balanced_lookup(context_lens, items.num_items, mbpr, items.zero_invalid, balanced_w,
-                             item, true, lane, &bs))
+        if (!balanced_lookup(context_lens, items, mbpr, balanced_w, item, true, lane, &bs))
             return;
         ns = bs.nsplit;
         base = static_cast<int64_t>(head) * slots + bs.first_slot;

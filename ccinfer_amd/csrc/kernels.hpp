@@ -32,8 +32,8 @@ struct DecodePlan {
 
 constexpr int kBalancedMaxItems = 256;
 
-// Returns the plan for a batch whose longest context is max_ctx tokens. allow_balanced:
-// the items are plain decode requests (item i = request i), so the balanced mode may be used.
+// Returns the plan for a batch whose longest context is max_ctx tokens. allow_balanced: the
+// balanced mode may be used (it resolves items through DecodeItems like the kernel does).
 DecodePlan plan_decode(int num_items, int num_kv_heads, int max_ctx, bool allow_balanced);
 
 // Scratch bytes the split-KV decode needs for `num_items` query rows.

@@ -1044,7 +1044,7 @@ PrefillLayout prefill_layout(int batch_size, int total_query_tokens, int max_blo
     const int G = num_q_heads / num_kv_heads;
     L.tile_tokens = tile_tokens_for(head_dim, G);
     L.max_tiles = total_query_tokens / L.tile_tokens + batch_size;
-    L.plan = plan_decode(batch_size, num_kv_heads, max_blocks_per_req * block_size, false);
+    L.plan = plan_decode(batch_size, num_kv_heads, max_blocks_per_req * block_size, true);
     size_t off = 0;
     L.counts_off = off;
     off = align256(off + 2 * sizeof(int32_t));
