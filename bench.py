@@ -1,13 +1,14 @@
 """Benchmark of the paged-attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5,6] [--no-cpu]
 
 One "step" is one pass of the hot path over one batch of synthetic input already resident in
 HBM. The headline (the JSON `value`) is BASELINE.json's decode metric on configs[1]: batched
 paged decode, batch 64, Qwen3-0.6B heads (16 q / 8 kv, d=128), contexts U[128, 4096], one
 step = KV-cache write of the 64 new tokens + decode attention; value = algorithmic KV bytes
 read per step (K+V of every context position, once per (sequence, kv_head)) / step time.
-The other configurations are reported under "configs". rank 0 prints ONE JSON line.
+The other configurations are reported under "configs"; "6" is the fused decode prologue
+(split QKV + q/k RMSNorm + RoPE + KV write in one launch), in algorithmic bytes per second. rank 0 prints ONE JSON line.
 
 Timing: W untimed warm-up steps, then exactly K steps bracketed by device synchronisation;
 per-op kernel time is measured with HIP events recorded on the stream the kernels run on.
@@ -156,6 +157,35 @@ def cpu_prefill_baseline(w: W.PagedWorkload, pairs, budget_s: float):
     return (time.perf_counter() - t0) / reps, reps
 
 
+def prologue_call(w: W.PrologueWorkload, stream: torch.cuda.Stream):
+    lib = _lib.load()
+    args = (w.qkv.data_ptr(), w.q_norm_w.data_ptr(), w.k_norm_w.data_ptr(),
+            w.positions.data_ptr(), w.rope_cache.data_ptr(), w.slot_mapping.data_ptr(),
+            w.q_out.data_ptr(), w.k_cache.data_ptr(), w.v_cache.data_ptr(), w.tokens, w.hq,
+            w.hkv, w.d, w.rope_cache.shape[0], w.k_cache.shape[0], 1e-6, stream.cuda_stream)
+
+    def fn():
+        rc = lib.ccinfer_qkv_prologue(*args)
+        assert rc == 0, rc
+    return fn
+
+
+def cpu_prologue_baseline(w: W.PrologueWorkload, budget_s: float):
+    """Times the oracle prologue (the reference's five steps in sequence) on one host core."""
+    import oracle
+    qkv, qn, kn = u16(w.qkv), u16(w.q_norm_w), u16(w.k_norm_w)
+    pos, sm = w.positions.cpu().numpy(), w.slot_mapping.cpu().numpy()
+    rc = w.rope_cache.cpu().numpy()
+    kc, vc = u16(w.k_cache), u16(w.v_cache)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.qkv_prologue(qkv, qn, kn, pos, rc, sm, kc, vc, w.hq, w.hkv, w.d, 1e-6)
+        reps += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    return (time.perf_counter() - t0) / reps, reps
+
+
 def prefill_pair_flops(w: W.PagedWorkload, pairs) -> int:
     """FLOPs of the (query row, head) pairs: 4*D per visible key."""
     qsl = w.query_start_loc
@@ -254,6 +284,23 @@ def run(args):
         out["5_decode_b32_ctx32768_gqa4"] = r
         del w
 
+    if 6 in configs:
+        # fused decode prologue: a decode batch of 64 tokens (configs[1]'s batch) and the
+        # 12288 query tokens of configs[2] (the HBM-bound size)
+        for tokens, key in ((64, "6_prologue_t64"), (12288, "6_prologue_t12288")):
+            w = W.prologue(device=dev, tokens=tokens)
+            ms, host_ms = time_loop(prologue_call(w, stream), max(args.steps, 50),
+                                    args.warmup, stream)
+            r = {"ms_per_step": ms, "host_ms_per_step": host_ms, "bytes": w.bytes(),
+                 "GBps": w.bytes() / (ms * 1e-3) / 1e9}
+            r["hbm_frac"] = r["GBps"] * 1e9 / HBM_PEAK
+            if not args.no_cpu and tokens == 64:
+                s, reps = cpu_prologue_baseline(w, 1.0)
+                r["cpu_GBps"] = w.bytes() / s / 1e9
+                r["cpu_sample"] = "the same 64 tokens, 1 thread"
+            out[key] = r
+            del w
+
     torch.cuda.synchronize()
     return head, out, nt
 
@@ -269,6 +316,8 @@ def profile(op: str, iters: int) -> None:
         src = torch.ones(COPY_BYTES // 2, dtype=torch.bfloat16, device=dev)
         dst = torch.empty_like(src)
         fn = lambda: dst.copy_(src)  # noqa: E731
+    elif op == "prologue":
+        fn = prologue_call(W.prologue(device=dev, tokens=12288), stream)
     else:
         w = {"decode": W.decode_batched, "write": W.decode_batched, "prefill": W.prefill_prefix,
              "mixed": W.mixed_step, "long": W.decode_long}[op](device=dev)
@@ -287,11 +336,11 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--configs", default="1,2,3,4,5")
+    ap.add_argument("--configs", default="1,2,3,4,5,6")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=5.0)
     ap.add_argument("--profile-op", choices=["decode", "write", "prefill", "mixed", "long",
-                                             "copy"], default=None)
+                                             "prologue", "copy"], default=None)
     ap.add_argument("--profile-iters", type=int, default=5)
     args = ap.parse_args()
     if args.gpus != 1:

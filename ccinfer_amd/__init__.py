@@ -10,6 +10,7 @@ from .ops import (  # noqa: F401
     decode_workspace_size,
     prefill_attention,
     prefill_workspace_size,
+    qkv_prologue,
     write_kv_cache,
 )
 
@@ -19,5 +20,6 @@ __all__ = [
     "decode_workspace_size",
     "prefill_attention",
     "prefill_workspace_size",
+    "qkv_prologue",
     "write_kv_cache",
 ]

@@ -16,6 +16,10 @@ _vp = ctypes.c_void_p
 # name -> (restype, argtypes); must match include/ccinfer_attn.h.
 SIGNATURES = {
     "ccinfer_write_kv_cache": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp]),
+    "ccinfer_qkv_prologue": (
+        _c_int,
+        [_vp] * 9 + [_c_int] * 6 + [ctypes.c_float, _vp],
+    ),
     "ccinfer_decode_workspace_size": (_c_size, [_c_int] * 6),
     "ccinfer_decode_attention": (
         _c_int,

@@ -43,6 +43,7 @@ SOURCES = [
     CSRC / "decode_attn.hip",
     CSRC / "prefill_attn.hip",
     CSRC / "generic_attn.hip",
+    CSRC / "qkv_prologue.hip",
     CSRC / "capi.cpp",
     CSRC / "dropin" / "launchers.cpp",
     CSRC / "dropin" / "hip_backend.cpp",

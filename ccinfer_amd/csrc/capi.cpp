@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 
 #include <climits>
+#include <cstring>
 #include <cstdint>
 
 #include "ccinfer_attn.h"
@@ -98,6 +99,35 @@ int ccinfer_write_kv_cache(const void* k_new, const void* v_new, void* k_cache, 
     return map_hip_error(write_kv_cache(k_new, v_new, k_cache, v_cache, slot_mapping,
                                         total_tokens, n_kv_heads, head_dim, max_slots,
                                         as_stream(stream)));
+}
+
+int ccinfer_qkv_prologue(const void* qkv, const void* q_norm_weight, const void* k_norm_weight,
+                         const int32_t* positions, const void* rope_cache,
+                         const int32_t* slot_mapping, void* q_out, void* k_cache, void* v_cache,
+                         int num_tokens, int num_q_heads, int num_kv_heads, int head_dim,
+                         int rope_cache_max_position, int max_slots, float eps, void* stream) {
+    if (!qkv || !positions || !rope_cache || !slot_mapping || !q_out || !k_cache || !v_cache)
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    if (num_tokens <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || max_slots <= 0 ||
+        rope_cache_max_position <= 0)
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    if (head_dim <= 0 || head_dim % 2 != 0 || head_dim > 1024) return CCINFER_ERR_INVALID_ARGUMENT;
+    // eps > 0 (backend.h:84); NaN and inf are tested on the bits, which stays correct when
+    // the compiler is told that NaNs do not occur.
+    uint32_t eps_bits;
+    std::memcpy(&eps_bits, &eps, sizeof eps_bits);
+    if ((eps_bits & 0x7f800000u) == 0x7f800000u || !(eps > 0.0f))
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    const int64_t rows = static_cast<int64_t>(num_tokens) * (num_q_heads + num_kv_heads);
+    if (!fits_int(rows) ||
+        !fits_int(static_cast<int64_t>(num_q_heads + 2 * static_cast<int64_t>(num_kv_heads)) *
+                  head_dim))
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    return map_hip_error(qkv_prologue(qkv, q_norm_weight, k_norm_weight, positions, rope_cache,
+                                      slot_mapping, q_out, k_cache, v_cache, num_tokens,
+                                      num_q_heads, num_kv_heads, head_dim,
+                                      rope_cache_max_position, max_slots, eps,
+                                      as_stream(stream)));
 }
 
 size_t ccinfer_decode_workspace_size(int batch_size, int max_blocks_per_req, int num_q_heads,

@@ -75,6 +75,16 @@ hipError_t prefill_attention(const void* q, const void* k_cache, const void* v_c
                              int num_kv_heads, int head_dim, int block_size, void* workspace,
                              hipStream_t stream);
 
+// ---- fused decode-side prologue: split QKV, q/k RMSNorm, RoPE, KV write -----
+bool qkv_prologue_fast_supported(int head_dim);
+
+hipError_t qkv_prologue(const void* qkv, const void* q_norm_w, const void* k_norm_w,
+                        const int32_t* positions, const void* rope_cache,
+                        const int32_t* slot_mapping, void* q_out, void* k_cache, void* v_cache,
+                        int num_tokens, int num_q_heads, int num_kv_heads, int head_dim,
+                        int rope_cache_max_position, int max_slots, float eps,
+                        hipStream_t stream);
+
 // ---- generic (any head_dim / GQA ratio / block size) ----------------------
 hipError_t generic_decode_attention(const void* q, const void* k_cache, const void* v_cache,
                                     const int32_t* block_table, const int32_t* context_lens,

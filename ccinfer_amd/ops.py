@@ -1,6 +1,7 @@
 """Torch-facing operators over the C ABI, mirroring the reference's backend ops.
 
 Reference interface: DeviceBackend::{write_kv_cache, decode_attention, prefill_attention}
+(plus qkv_prologue, one launch for split_qkv + rms_norm + rope + write_kv_cache)
 (src/backend/backend.h:172-223) with the parameter structs of src/backend/params.h:148-211.
 Argument names, meaning and error behaviour follow it: invalid arguments raise
 CcinferError with code ErrorCode::InvalidArgument (6), the same value the reference returns.
@@ -84,6 +85,53 @@ def write_kv_cache(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tens
     _check(lib.ccinfer_write_kv_cache(_ptr(k_new), _ptr(v_new), _ptr(k_cache), _ptr(v_cache),
                                       _ptr(slot_mapping), total, hkv, d,
                                       slots if max_slots is None else max_slots, _stream()), op)
+
+
+def qkv_prologue(qkv: torch.Tensor, q_norm_weight: Optional[torch.Tensor],
+                 k_norm_weight: Optional[torch.Tensor], positions: torch.Tensor,
+                 rope_cache: torch.Tensor, slot_mapping: torch.Tensor, k_cache: torch.Tensor,
+                 v_cache: torch.Tensor, num_q_heads: int, eps: float = 1e-6,
+                 q_out: Optional[torch.Tensor] = None,
+                 max_slots: Optional[int] = None) -> torch.Tensor:
+    """One launch for the per-layer attention prologue of src/model/qwen3/qwen3_model.cpp:
+    174-244: split_qkv, rms_norm of q and k (skipped for a None weight), rope with
+    rotary_dim = head_dim, write_kv_cache. Returns q [num_tokens, num_q_heads, head_dim].
+
+    qkv [num_tokens, (num_q_heads + 2 num_kv_heads) * head_dim] bf16; rope_cache
+    [max_position, head_dim / 2, 2] float32 (cos, sin); num_kv_heads and head_dim come from
+    k_cache."""
+    op = "qkv_prologue"
+    for t in (qkv, k_cache, v_cache):
+        _dev_tensor(t, torch.bfloat16, op)
+    for t in (q_norm_weight, k_norm_weight):
+        if t is not None:
+            _dev_tensor(t, torch.bfloat16, op)
+    _dev_tensor(positions, torch.int32, op)
+    _dev_tensor(slot_mapping, torch.int32, op)
+    _dev_tensor(rope_cache, torch.float32, op)
+    slots, hkv, d = _kv_shape(k_cache)
+    _require(v_cache.numel() == k_cache.numel() and num_q_heads > 0, op)
+    width = (num_q_heads + 2 * hkv) * d
+    _require(qkv.numel() % width == 0 and qkv.shape[-1] == width, op)
+    tokens = qkv.numel() // width
+    _require(positions.numel() == tokens and slot_mapping.numel() == tokens, op)
+    for w in (q_norm_weight, k_norm_weight):
+        _require(w is None or w.numel() == d, op)
+    _require(rope_cache.dim() >= 2 and rope_cache.numel() % d == 0, op)
+    max_pos = rope_cache.numel() // d
+    if q_out is None:
+        q_out = torch.empty(tokens, num_q_heads, d, dtype=torch.bfloat16, device=qkv.device)
+    else:
+        _dev_tensor(q_out, torch.bfloat16, op)
+        _require(q_out.numel() == tokens * num_q_heads * d, op)
+    lib = _lib.load()
+    _check(lib.ccinfer_qkv_prologue(_ptr(qkv), _ptr(q_norm_weight), _ptr(k_norm_weight),
+                                    _ptr(positions), _ptr(rope_cache), _ptr(slot_mapping),
+                                    _ptr(q_out), _ptr(k_cache), _ptr(v_cache), tokens,
+                                    num_q_heads, hkv, d, max_pos,
+                                    slots if max_slots is None else max_slots, float(eps),
+                                    _stream()), op)
+    return q_out
 
 
 def decode_workspace_size(batch_size: int, max_blocks_per_req: int, num_q_heads: int,

@@ -249,3 +249,63 @@ def decode_items_kv_bytes(w: PagedWorkload) -> int:
     qsl = w.query_start_loc
     ql = qsl[1:] - qsl[:-1]
     return int(np.sum(w.context_lens[ql == 1].astype(np.int64))) * w.hkv * w.d * 4
+
+
+@dataclass
+class PrologueWorkload:
+    """One layer's attention prologue input: the packed QKV projection of `tokens` tokens,
+    q/k RMSNorm weights, positions, a (cos, sin) table and the slots of a paged KV cache."""
+    name: str
+    hq: int
+    hkv: int
+    d: int
+    qkv: torch.Tensor            # [tokens, (hq + 2 hkv) d] bf16
+    q_norm_w: torch.Tensor       # [d] bf16
+    k_norm_w: torch.Tensor       # [d] bf16
+    positions: torch.Tensor      # [tokens] int32
+    rope_cache: torch.Tensor     # [max_position, d / 2, 2] float32
+    slot_mapping: torch.Tensor   # [tokens] int32
+    k_cache: torch.Tensor        # [slots, hkv, d] bf16
+    v_cache: torch.Tensor
+    q_out: torch.Tensor          # [tokens, hq, d] bf16
+
+    @property
+    def tokens(self) -> int:
+        return self.qkv.shape[0]
+
+    def bytes(self) -> int:
+        """Algorithmic HBM bytes: the QKV rows read once, q written, K and V written to the
+        cache, one (cos, sin) row, position and slot per token, and the two weight rows."""
+        per_token = ((self.hq + 2 * self.hkv) * self.d * 2 + self.hq * self.d * 2
+                     + 2 * self.hkv * self.d * 2 + (self.d // 2) * 8 + 8)
+        return self.tokens * per_token + 2 * self.d * 2
+
+
+def rope_cache_table(max_position: int, rotary_dim: int, theta: float, device) -> torch.Tensor:
+    """(cos, sin) of pos * theta^(-2p / rotary_dim) in float32, [max_position, rotary_dim/2, 2]
+    (the table src/model/rope/rope_cache.cpp builds on the host)."""
+    half = rotary_dim // 2
+    p = torch.arange(half, dtype=torch.float32)
+    inv = 1.0 / torch.pow(torch.tensor(theta, dtype=torch.float32), p * 2.0 / rotary_dim)
+    ang = torch.arange(max_position, dtype=torch.float32)[:, None] * inv[None, :]
+    return torch.stack([torch.cos(ang), torch.sin(ang)], -1).contiguous().to(device)
+
+
+def prologue(device="cpu", seed: int = 6, tokens: int = 64, hq: int = 16, hkv: int = 8,
+             d: int = 128, max_position: int = 40960, theta: float = 1e6,
+             cache_slots: Optional[int] = None) -> PrologueWorkload:
+    """Decode-side prologue of one layer: `tokens` new tokens (one per sequence for a decode
+    batch) at random positions, written to distinct random slots of the cache."""
+    rng = np.random.default_rng(seed)
+    slots = cache_slots or max(4 * tokens, 1024)
+    g = _gen(seed, device)
+    qkv = randn_bf16((tokens, (hq + 2 * hkv) * d), g, device)
+    qn = randn_bf16((d,), g, device)
+    kn = randn_bf16((d,), g, device)
+    pos = torch.from_numpy(rng.integers(0, max_position, tokens).astype(np.int32)).to(device)
+    sm = torch.from_numpy(rng.permutation(slots)[:tokens].astype(np.int32)).to(device)
+    kc = torch.zeros((slots, hkv, d), dtype=torch.bfloat16, device=device)
+    return PrologueWorkload(f"prologue_t{tokens}", hq, hkv, d, qkv, qn, kn, pos,
+                            rope_cache_table(max_position, d, theta, device), sm, kc,
+                            torch.zeros_like(kc),
+                            torch.empty((tokens, hq, d), dtype=torch.bfloat16, device=device))

@@ -53,6 +53,24 @@ int ccinfer_write_kv_cache(const void* k_new, const void* v_new, void* k_cache, 
                            const int32_t* slot_mapping, int total_tokens, int n_kv_heads,
                            int head_dim, int max_slots, void* stream);
 
+/* Fused attention prologue for one layer: replaces the five launches
+ * launch_split_qkv, launch_rms_norm (q), launch_rms_norm (k), launch_rope and
+ * launch_write_kv_cache (src/kernel/cuda_kernels.h, called in sequence by
+ * src/model/qwen3/qwen3_model.cpp:174-244).
+ * qkv: [num_tokens][(num_q_heads + 2 num_kv_heads) head_dim] bf16, the packed projection;
+ * q_norm_weight, k_norm_weight: [head_dim] bf16 or NULL (no norm for that side);
+ * positions: [num_tokens] int32; rope_cache: [rope_cache_max_position][head_dim/2] float
+ * (cos, sin) pairs (src/model/rope_cache.cpp); q_out: [num_tokens][num_q_heads][head_dim]
+ * bf16; k_cache/v_cache as in ccinfer_write_kv_cache. Rotation is skipped for positions
+ * outside [0, rope_cache_max_position); tokens whose slot is outside [0, max_slots) write no
+ * K/V. head_dim must be even and at most 1024; eps > 0 (backend.h:84). Results match the five reference kernels
+ * in sequence (bf16 rounding between steps, the same reduction order). */
+int ccinfer_qkv_prologue(const void* qkv, const void* q_norm_weight, const void* k_norm_weight,
+                         const int32_t* positions, const void* rope_cache,
+                         const int32_t* slot_mapping, void* q_out, void* k_cache, void* v_cache,
+                         int num_tokens, int num_q_heads, int num_kv_heads, int head_dim,
+                         int rope_cache_max_position, int max_slots, float eps, void* stream);
+
 /* Workspace bytes ccinfer_decode_attention needs for this batch shape (may be 0). */
 size_t ccinfer_decode_workspace_size(int batch_size, int max_blocks_per_req, int num_q_heads,
                                      int num_kv_heads, int head_dim, int cache_block_size);

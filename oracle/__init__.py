@@ -44,6 +44,10 @@ def load() -> ctypes.CDLL:
         lib.orc_prefill_attention_pairs.argtypes = [_P] * 7 + [_I] * 7 + [_P, _I, _I]
         lib.orc_naive_attention.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I]
         lib.orc_lcg_fill.argtypes = [_P, _I, ctypes.c_uint]
+        lib.orc_split_qkv.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I]
+        lib.orc_rms_norm.argtypes = [_P, _P, _P, _I, _I, ctypes.c_float]
+        lib.orc_rope.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I]
+        lib.orc_qkv_prologue.argtypes = [_P] * 11 + [_I] * 6 + [ctypes.c_float]
         _lib = lib
     return _lib
 
@@ -146,3 +150,70 @@ def lcg_fill(n: int, seed: int) -> np.ndarray:
     out = np.empty(n, np.uint16)
     load().orc_lcg_fill(_p(out), n, seed)
     return out
+
+
+# ---- decode-side prologue (split QKV, q/k RMSNorm, RoPE, KV write) ----
+
+def split_qkv(qkv, nq: int, nkv: int, hd: int):
+    """qkv uint16 [T, (nq + 2 nkv) * hd] -> (q [T, nq, hd], k [T, nkv, hd], v [T, nkv, hd])."""
+    x = _c(qkv, np.uint16)
+    t = x.shape[0]
+    q = np.empty((t, nq, hd), np.uint16)
+    k = np.empty((t, nkv, hd), np.uint16)
+    v = np.empty((t, nkv, hd), np.uint16)
+    load().orc_split_qkv(_p(x), _p(q), _p(k), _p(v), t, nq, nkv, hd)
+    return q, k, v
+
+
+def rms_norm(x, weight, eps: float):
+    """Rows of x (uint16 [..., dim]) normalised as the reference kernel does; uint16 out."""
+    x = _c(x, np.uint16)
+    w = _c(weight, np.uint16)
+    dim = x.shape[-1]
+    out = np.empty_like(x)
+    load().orc_rms_norm(_p(x), _p(w), _p(out), x.size // dim, dim, eps)
+    return out
+
+
+def rope(q, k, positions, rope_cache, rotary_dim=None):
+    """Returns rotated copies of q [T, nq, hd] and k [T, nkv, hd] (uint16); rope_cache is
+    float32 [max_pos, rotary_dim / 2, 2] of (cos, sin)."""
+    q, k = _c(q, np.uint16).copy(), _c(k, np.uint16).copy()
+    pos = _c(positions, np.int32)
+    rc = _c(rope_cache, np.float32)
+    t, nq, hd = q.shape
+    rd = hd if rotary_dim is None else rotary_dim
+    load().orc_rope(_p(q), _p(k), _p(pos), _p(rc), t, nq, k.shape[1], hd, rd, rc.shape[0])
+    return q, k
+
+
+def qkv_prologue(qkv, q_norm_w, k_norm_w, positions, rope_cache, slot_mapping, k_cache,
+                 v_cache, nq: int, nkv: int, hd: int, eps: float, max_slots=None):
+    """The fused prologue; returns q_out [T, nq, hd] and updates k_cache / v_cache in place."""
+    x = _c(qkv, np.uint16)
+    t = x.shape[0]
+    qw = None if q_norm_w is None else _c(q_norm_w, np.uint16)
+    kw = None if k_norm_w is None else _c(k_norm_w, np.uint16)
+    pos = _c(positions, np.int32)
+    rc = _c(rope_cache, np.float32)
+    sm = _c(slot_mapping, np.int32)
+    assert k_cache.flags.c_contiguous and v_cache.flags.c_contiguous
+    q_out = np.empty((t, nq, hd), np.uint16)
+    kt = np.empty((t, nkv, hd), np.uint16)
+    vt = np.empty((t, nkv, hd), np.uint16)
+    load().orc_qkv_prologue(_p(x), None if qw is None else _p(qw), None if kw is None else _p(kw),
+                            _p(pos), _p(rc), _p(sm), _p(q_out), _p(kt), _p(vt), _p(k_cache),
+                            _p(v_cache), t, nq, nkv, hd, rc.shape[0],
+                            k_cache.shape[0] if max_slots is None else max_slots, eps)
+    return q_out
+
+
+def rope_cache_table(max_position: int, rotary_dim: int, theta: float) -> np.ndarray:
+    """(cos, sin) table [max_position, rotary_dim / 2, 2] float32, computed in float32 as the
+    reference builds it (src/model/rope/rope_cache.cpp:29-44)."""
+    half = rotary_dim // 2
+    pairs = np.arange(half, dtype=np.float32)
+    inv = (np.float32(1.0) / np.power(np.float32(theta),
+                                      pairs * np.float32(2) / np.float32(rotary_dim))).astype(np.float32)
+    ang = (np.arange(max_position, dtype=np.float32)[:, None] * inv[None, :]).astype(np.float32)
+    return np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float32)

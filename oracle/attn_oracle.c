@@ -345,3 +345,115 @@ void orc_lcg_fill(uint16_t* data, int n, unsigned int seed) {
         data[i] = orc_f32_to_bf16(v * 0.5f);
     }
 }
+
+/* ---------------------------------------------------------------------------------------
+ * Decode-side prologue of one attention layer (the sequence of qwen3_model.cpp:174-244):
+ * split the fused QKV projection, RMS-normalise q and k per head, apply split-half RoPE,
+ * write the new K/V into the cache.
+ * ------------------------------------------------------------------------------------- */
+
+/* src/kernel/elementwise/elementwise.cu:34-64: qkv[t] = [q heads | k heads | v heads]. */
+void orc_split_qkv(const uint16_t* qkv, uint16_t* q, uint16_t* k, uint16_t* v, int T, int nq,
+                   int nkv, int hd) {
+    const int64_t qd = (int64_t)nq * hd, kd = (int64_t)nkv * hd, row = qd + 2 * kd;
+    for (int64_t t = 0; t < T; ++t) {
+        memcpy(q + t * qd, qkv + t * row, (size_t)qd * 2);
+        memcpy(k + t * kd, qkv + t * row + qd, (size_t)kd * 2);
+        memcpy(v + t * kd, qkv + t * row + qd + kd, (size_t)kd * 2);
+    }
+}
+
+static float orc_bf16_round(float x) { return orc_bf16_to_f32(orc_f32_to_bf16(x)); }
+
+/* Warp sum of cuda_common.cuh:14-20 over 32 lanes: shfl_down by 16, 8, 4, 2, 1; lanes past
+ * the top read their own value back (shfl_down keeps it), so only lane 0's result is
+ * meaningful and it sums pairs in that tree order. */
+static float orc_warp_tree_sum(float v[32]) {
+    for (int off = 16; off > 0; off >>= 1) {
+        for (int l = 0; l + off < 32; ++l) v[l] = v[l] + v[l + off];
+    }
+    return v[0];
+}
+
+/* src/kernel/norm/rms_norm.cu:22-58 (dim even, the bf16x2 path) and :60-88 (dim odd, the
+ * scalar path), with kBlockSize = 256 (:93) and block_reduce_sum of cuda_common.cuh:30-62:
+ * per-thread partial sums of squares rounded to bf16 after every addition, a 32-lane tree
+ * per warp, the 8 warp sums reduced by warp 0 with the same tree, the total rounded to bf16,
+ * inv_rms = 1 / sqrt(total / dim + eps), out = bf16(x * inv_rms * w). In place is allowed. */
+void orc_rms_norm(const uint16_t* input, const uint16_t* weight, uint16_t* output, int rows,
+                  int dim, float eps) {
+    enum { kBlock = 256, kWarp = 32 };
+    float part[kBlock];
+    for (int r = 0; r < rows; ++r) {
+        const uint16_t* x = input + (int64_t)r * dim;
+        uint16_t* o = output + (int64_t)r * dim;
+        const int even = (dim % 2) == 0;
+        for (int tid = 0; tid < kBlock; ++tid) {
+            float s = 0.0f;
+            if (even) {
+                for (int i = tid; i < dim / 2; i += kBlock) {
+                    const float a = orc_bf16_to_f32(x[2 * i]), b = orc_bf16_to_f32(x[2 * i + 1]);
+                    const float term = a * a + b * b;
+                    s = orc_bf16_round(s + term);
+                }
+            } else {
+                for (int i = tid; i < dim; i += kBlock) {
+                    const float a = orc_bf16_to_f32(x[i]);
+                    s = orc_bf16_round(s + a * a);
+                }
+            }
+            part[tid] = s;
+        }
+        float warp_sums[kWarp];
+        for (int w = 0; w < kWarp; ++w) warp_sums[w] = 0.0f;
+        for (int w = 0; w < kBlock / kWarp; ++w) warp_sums[w] = orc_warp_tree_sum(part + w * kWarp);
+        const float total = orc_bf16_round(orc_warp_tree_sum(warp_sums));
+        const float inv_rms = 1.0f / sqrtf(total / (float)dim + eps);
+        /* read all of x before writing (the kernel's first loop completes before the second) */
+        for (int i = 0; i < dim; ++i) {
+            const float a = orc_bf16_to_f32(x[i]);
+            const float w = orc_bf16_to_f32(weight[i]);
+            o[i] = orc_f32_to_bf16(a * inv_rms * w);
+        }
+    }
+}
+
+/* src/kernel/pos/rope.cu:14-43 (split-half pairs (i, i + rotary_dim/2); the bf16x2 path at
+ * :46-88 computes the same per-element formula): rows of q [T][nq][hd] and k [T][nkv][hd] in
+ * place, rope_cache [max_pos][rotary_dim/2] of (cos, sin); tokens with pos < 0 or
+ * pos >= rope_cache_max_position are left unchanged. */
+void orc_rope(uint16_t* q, uint16_t* k, const int32_t* positions, const float* rope_cache,
+              int T, int nq, int nkv, int hd, int rotary_dim, int rope_cache_max_position) {
+    const int half = rotary_dim / 2;
+    for (int t = 0; t < T; ++t) {
+        const int pos = positions[t];
+        if (pos < 0 || pos >= rope_cache_max_position) continue;
+        for (int lh = 0; lh < nq + nkv; ++lh) {
+            const int is_q = lh < nq;
+            uint16_t* x = is_q ? q + ((int64_t)t * nq + lh) * hd
+                               : k + ((int64_t)t * nkv + (lh - nq)) * hd;
+            for (int p = 0; p < half; ++p) {
+                const float c = rope_cache[((int64_t)pos * half + p) * 2];
+                const float s = rope_cache[((int64_t)pos * half + p) * 2 + 1];
+                const float x0 = orc_bf16_to_f32(x[p]), x1 = orc_bf16_to_f32(x[p + half]);
+                x[p] = orc_f32_to_bf16(x0 * c - x1 * s);
+                x[p + half] = orc_f32_to_bf16(x1 * c + x0 * s);
+            }
+        }
+    }
+}
+
+/* The whole prologue: split, q/k RMSNorm (skipped when the weight is NULL), RoPE over the
+ * full head_dim, KV-cache write. q_out [T][nq][hd]; k_tmp, v_tmp [T][nkv][hd] receive the
+ * K/V rows that are written. */
+void orc_qkv_prologue(const uint16_t* qkv, const uint16_t* q_norm_w, const uint16_t* k_norm_w,
+                      const int32_t* positions, const float* rope_cache,
+                      const int32_t* slot_mapping, uint16_t* q_out, uint16_t* k_tmp,
+                      uint16_t* v_tmp, uint16_t* k_cache, uint16_t* v_cache, int T, int nq,
+                      int nkv, int hd, int rope_cache_max_position, int max_slots, float eps) {
+    orc_split_qkv(qkv, q_out, k_tmp, v_tmp, T, nq, nkv, hd);
+    if (q_norm_w) orc_rms_norm(q_out, q_norm_w, q_out, T * nq, hd, eps);
+    if (k_norm_w) orc_rms_norm(k_tmp, k_norm_w, k_tmp, T * nkv, hd, eps);
+    orc_rope(q_out, k_tmp, positions, rope_cache, T, nq, nkv, hd, hd, rope_cache_max_position);
+    orc_write_kv_cache(k_tmp, v_tmp, k_cache, v_cache, slot_mapping, T, nkv, hd, max_slots);
+}

@@ -17,6 +17,11 @@
  *                               causal contract of src/backend/params.h:140-146
  *   - orc_naive_attention     : tests/kernel/test_naive_attn.cu:16-65 (dense causal)
  *   - orc_lcg_fill            : tests/kernel/test_naive_attn.cu:67-74
+ *   - orc_split_qkv           : src/kernel/elementwise/elementwise.cu:34-64
+ *   - orc_rms_norm            : src/kernel/norm/rms_norm.cu:22-88 with the reduction order
+ *                               of src/kernel/cuda_common.cuh:14-62
+ *   - orc_rope                : src/kernel/pos/rope.cu:14-43
+ *   - orc_qkv_prologue        : the sequence of src/model/qwen3/qwen3_model.cpp:174-244
  *
  * Every function is pinned by tests/test_oracle.py (known-answer vectors from the
  * reference tests, closed forms, torch's float64 scaled_dot_product_attention as an
@@ -86,6 +91,19 @@ void orc_naive_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v
 
 /* The reference tests' LCG fill: values in [-0.5, 0.5) rounded to bf16. */
 void orc_lcg_fill(uint16_t* data, int n, unsigned int seed);
+
+/* Decode-side prologue (qwen3_model.cpp:174-244). */
+void orc_split_qkv(const uint16_t* qkv, uint16_t* q, uint16_t* k, uint16_t* v, int T, int nq,
+                   int nkv, int hd);
+void orc_rms_norm(const uint16_t* input, const uint16_t* weight, uint16_t* output, int rows,
+                  int dim, float eps);
+void orc_rope(uint16_t* q, uint16_t* k, const int32_t* positions, const float* rope_cache,
+              int T, int nq, int nkv, int hd, int rotary_dim, int rope_cache_max_position);
+void orc_qkv_prologue(const uint16_t* qkv, const uint16_t* q_norm_w, const uint16_t* k_norm_w,
+                      const int32_t* positions, const float* rope_cache,
+                      const int32_t* slot_mapping, uint16_t* q_out, uint16_t* k_tmp,
+                      uint16_t* v_tmp, uint16_t* k_cache, uint16_t* v_cache, int T, int nq,
+                      int nkv, int hd, int rope_cache_max_position, int max_slots, float eps);
 
 #ifdef __cplusplus
 }

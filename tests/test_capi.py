@@ -130,3 +130,23 @@ def test_error_code_values_match_reference_enum():
         val = int(re.search(rf"{code}\s*=\s*(\d+)", hdr).group(1))
         assert names.index(ename) == val, (code, ename)
     assert ctypes.sizeof(ctypes.c_size_t) == 8
+
+
+def _prologue(lib, **kw):
+    a = dict(qkv=FAKE, qw=FAKE, kw=FAKE, pos=FAKE, rc=FAKE, sm=FAKE, qo=FAKE, kc=FAKE, vc=FAKE,
+             t=4, nq=8, nkv=2, d=128, mp=64, slots=64, eps=1e-6)
+    a.update(kw)
+    return lib.ccinfer_qkv_prologue(a["qkv"], a["qw"], a["kw"], a["pos"], a["rc"], a["sm"],
+                                    a["qo"], a["kc"], a["vc"], a["t"], a["nq"], a["nkv"],
+                                    a["d"], a["mp"], a["slots"], a["eps"], None)
+
+
+def test_qkv_prologue_validation(lib):
+    for ptr in ["qkv", "pos", "rc", "sm", "qo", "kc", "vc"]:
+        assert _prologue(lib, **{ptr: None}) == INVALID, ptr
+    for field in ["t", "nq", "nkv", "d", "mp", "slots"]:
+        assert _prologue(lib, **{field: 0}) == INVALID, field
+    assert _prologue(lib, d=127) == INVALID           # RoPE pairs need an even head_dim
+    assert _prologue(lib, d=1026) == INVALID
+    assert _prologue(lib, eps=0.0) == INVALID         # backend.h:84
+    assert _prologue(lib, eps=float("nan")) == INVALID
