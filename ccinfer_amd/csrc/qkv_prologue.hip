@@ -17,16 +17,16 @@
 // to bf16 before RoPE (as the reference stores them between its kernels); RoPE uses the
 // caller's (cos, sin) table.
 //
-// head_dim 128 (the fast path): a wavefront holds one (token, head) row at a time (R rows per
-// wavefront, their loads issued together). Lane l holds elements
-// 2l and 2l+1 -- exactly the pair thread l of the reference kernel sums, so lanes 0..31 and
-// 32..63 are the reference's two warps and the same trees apply. The RoPE partner of element
-// j is j + 64, held by lane l ^ 32, and is fetched with v_permlane32_swap. A wavefront that
-// handles a K row also copies the matching V row into the cache.
+// head_dim 128 (the fast path): a wavefront takes up to eight consecutive (token, head) rows
+// of one section of the packed QKV row and holds each as lane pairs: lane l holds elements 2l and 2l+1 -- exactly
+// the pair thread l of the reference kernel sums, so lanes 0..31 and 32..63 are the
+// reference's two warps and the same trees apply. The RoPE partner of element j is j + 64,
+// held by lane l ^ 32, and is fetched with v_permlane32_swap. V rows are copied through.
 // Other head dims: one workgroup of 256 threads per row, laid out as the reference kernel.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "attn_common.hpp"
 #include "kernels.hpp"
@@ -79,89 +79,109 @@ __device__ __forceinline__ float dpp_f(float v) {
 // v_permlane32_swap brings lane 32's sum to lane 0. Lane 0 ends with the total (unrounded),
 // added in exactly the reference's order.
 __device__ __forceinline__ float row_sum_squares(float x0, float x1) {
-    float v = bf16_round(x0 * x0 + x1 * x1);
+    // A swap leaves the receiving lanes' own values in the other returned register (VDST
+    // keeps its even rows / low half), so each step adds the two results and the input
+    // register is not needed afterwards.
+    const float v = bf16_round(x0 * x0 + x1 * x1);
     const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
                                                       false, false);
-    v += __uint_as_float(s16[1]);  // lanes 0..15: v[l] + v[l + 16]
-    v += dpp_f<0x108>(v);          // row_shl:8
-    v += dpp_f<0x104>(v);          // row_shl:4
-    v += dpp_f<0x102>(v);          // row_shl:2
-    v += dpp_f<0x101>(v);          // row_shl:1 -> lane 0: warp 0's sum, lane 32: warp 1's
-    const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+    float u = __uint_as_float(s16[0]) + __uint_as_float(s16[1]);  // lanes 0..15: v[l] + v[l+16]
+    u += dpp_f<0x108>(u);  // row_shl:8
+    u += dpp_f<0x104>(u);  // row_shl:4
+    u += dpp_f<0x102>(u);  // row_shl:2
+    u += dpp_f<0x101>(u);  // row_shl:1 -> lane 0: warp 0's sum, lane 32: warp 1's
+    const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(u), __float_as_uint(u),
                                                       false, false);
-    return v + __uint_as_float(s32[1]);
+    return __uint_as_float(s32[0]) + __uint_as_float(s32[1]);  // lane 0: warp 0 + warp 1
 }
 
-// R rows per wavefront, interleaved across the workgroup's waves so that each step of the
-// four waves covers four consecutive rows. kNorm: both norm weights given (else neither).
-//
-// Phases: (1) positions and slots (scalar loads); (2) every vector load of the R rows (QKV
-// row, V row, (cos, sin) pairs), unconditional -- a q row "loads V" from its own row, an
-// out-of-table position reads row 0 -- and fenced from the math; (3) sums of squares, the
-// totals of the R rows gathered into lanes 0..R-1 of one register so that the correctly
-// rounded sqrt and division run once for all rows; (4) normalise and rotate; (5) stores.
-template <int R, bool kNorm>
+// Raw buffer descriptor over `base` (dword 3: 32-bit data format, the gfx9-family raw-buffer
+// setting). Loads past `num_records` bytes (lane offset + immediate) return 0. Descriptors
+// are built once per wavefront on the scalar unit; a lane's address is then its 32-bit byte
+// offset plus an immediate, with no per-row address arithmetic.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base,
+                                                            uint32_t num_records) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0,
+                                             static_cast<int>(num_records), 0x00020000);
+}
+
+// One wavefront = up to kRowsPerWave (8, or 2 for small launches) consecutive rows of one section (q heads, k heads or v heads)
+// of one token's packed QKV row; each section is split into groups of that size. kNorm: both
+// norm weights given (else neither). A v wavefront copies its rows into the cache. A q or
+// k wavefront: (1) issues every load (rows past the section's end read as 0), the token's
+// (cos, sin) pairs and the weight row, fenced from the math; (2) sums of squares, the eight
+// totals gathered into lanes 0..kRowsPerWave-1 of one register so that the correctly rounded sqrt and
+// division run once; (3) normalise and rotate; (4) stores the section's rows.
+template <int kRowsPerWave, bool kNorm>
 __global__ __launch_bounds__(256) void qkv_prologue_d128_kernel(PrologueArgs a) {
     constexpr int D = 128;
+    constexpr int kRowBytes = D * 2;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int heads = a.nq + a.nkv;
-    const int total = a.T * heads;  // fits in int (checked by the caller)
-    const int64_t qkv_row = static_cast<int64_t>(a.nq + 2 * a.nkv) * D;
-    const int p0 = 2 * (lane & 31);  // pair index of element 2*lane (mod D/2)
+    const int gq = (a.nq + kRowsPerWave - 1) / kRowsPerWave;
+    const int gkv = (a.nkv + kRowsPerWave - 1) / kRowsPerWave;
+    const int groups = gq + 2 * gkv;
+    const int wave_id = blockIdx.x * kWavesPerGroup + wave;
+    if (wave_id >= a.T * groups) return;  // whole wavefronts only; no barriers below
+    const int t = wave_id / groups;
+    const int g = wave_id - t * groups;
+    // section 0: q heads, 1: k heads, 2: v heads
+    const int section = g < gq ? 0 : (g < gq + gkv ? 1 : 2);
+    const int h0 = (section == 0 ? g : (section == 1 ? g - gq : g - gq - gkv)) * kRowsPerWave;
+    const int sec_rows = section == 0 ? a.nq : a.nkv;
+    const int sec_start = section == 0 ? 0 : (section == 1 ? a.nq : a.nq + a.nkv);
+    const int n = min(kRowsPerWave, sec_rows - h0);  // rows of this wavefront
+    const int lane_off = lane * 4;                   // byte offset of the lane's pair in a row
+    const int row_all = a.nq + 2 * a.nkv;
+
+    const auto src = make_rsrc(a.qkv + (static_cast<int64_t>(t) * row_all + sec_start + h0) * D,
+                               static_cast<uint32_t>(n) * kRowBytes);
+    uint32_t w[kRowsPerWave];
+#pragma unroll
+    for (int r = 0; r < kRowsPerWave; ++r)
+        w[r] = __builtin_amdgcn_raw_buffer_load_b32(src, lane_off + r * kRowBytes, 0, 0);
+
+    const int slot = a.slot_mapping[t];
+    const bool slot_ok = slot >= 0 && slot < a.max_slots;
+    const int64_t kv_row = (static_cast<int64_t>(slot) * a.nkv + h0) * D;
+
+    if (section == 2) {  // v rows: copy into the cache
+        if (!slot_ok) return;
+        const auto dst = make_rsrc(a.v_cache + kv_row, static_cast<uint32_t>(n) * kRowBytes);
+#pragma unroll
+        for (int r = 0; r < kRowsPerWave; ++r)  // rows past n fall outside the descriptor
+            __builtin_amdgcn_raw_buffer_store_b32(w[r], dst, lane_off + r * kRowBytes, 0, 0);
+        return;
+    }
+
     const bool lo_half = lane < 32;
-    const uint32_t sin_sign = lo_half ? 0x80000000u : 0u;  // lo element: x0 c - x1 s
-
-    float qw0 = 0.f, qw1 = 0.f, kw0 = 0.f, kw1 = 0.f;
-    if constexpr (kNorm) {
-        const uint32_t qnw = reinterpret_cast<const uint32_t*>(a.q_norm_w)[lane];
-        const uint32_t knw = reinterpret_cast<const uint32_t*>(a.k_norm_w)[lane];
-        qw0 = lo_f(qnw), qw1 = hi_f(qnw), kw0 = lo_f(knw), kw1 = hi_f(knw);
-    }
-
-    // Row of step r: (blockIdx.x * R + r) * waves + wave. The (token, head) pair of the first
-    // row takes one division; later rows advance by `waves` heads. Rows past the end are
-    // clamped to the last row for loading and skipped when storing.
-    const int row0 = (blockIdx.x * R) * kWavesPerGroup + wave;
-    const int last_t = a.T - 1;
-    int t = row0 / heads;
-    int h = row0 - t * heads;
-    int tok[R], tl[R], lh[R], pos_r[R], slot_r[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        if (r > 0) {
-            h += kWavesPerGroup;
-            while (h >= heads) { h -= heads; ++t; }
-        }
-        const bool valid = row0 + r * kWavesPerGroup < total;
-        tl[r] = valid ? t : last_t;
-        lh[r] = valid ? h : heads - 1;
-        tok[r] = valid ? t : -1;
-        slot_r[r] = a.slot_mapping[tl[r]];
-        pos_r[r] = a.positions[tl[r]];
-    }
-
-    uint32_t w[R], v[R];
-    float4 cs[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int hl = lh[r];
-        const __bf16* src = a.qkv + tl[r] * qkv_row + static_cast<int64_t>(hl) * D;
-        const __bf16* vsrc = hl >= a.nq ? src + static_cast<int64_t>(a.nkv) * D : src;
-        w[r] = reinterpret_cast<const uint32_t*>(src)[lane];
-        v[r] = reinterpret_cast<const uint32_t*>(vsrc)[lane];
-        const int pos = pos_r[r];
-        const int pos_c = (pos >= 0 && pos < a.rope_max) ? pos : 0;
-        cs[r] = *reinterpret_cast<const float4*>(a.rope_cache +
-                                                 static_cast<int64_t>(pos_c) * (D / 2) + p0);
-    }
+    // lo element of a pair: x0 c - x1 s, so lanes 0..31 negate the partner (both halves)
+    const uint32_t partner_sign = lo_half ? 0x80008000u : 0u;
+    const int pos = a.positions[t];
+    const bool rotate = pos >= 0 && pos < a.rope_max;
+    const float4 cs = __builtin_bit_cast(
+        float4, __builtin_amdgcn_raw_buffer_load_b128(
+                    make_rsrc(a.rope_cache + static_cast<int64_t>(rotate ? pos : 0) * (D / 2),
+                              D * 4),
+                    (lane & 31) * 16, 0, 0));  // pairs 2 * (lane & 31) and +1
+    uint32_t nw = 0;
+    if constexpr (kNorm)
+        nw = __builtin_amdgcn_raw_buffer_load_b32(
+            make_rsrc(section == 0 ? a.q_norm_w : a.k_norm_w, kRowBytes), lane_off, 0, 0);
     __builtin_amdgcn_sched_barrier(0);  // every load above is issued before any math below
+    const float nw0 = lo_f(nw), nw1 = hi_f(nw);
+    // Rows keep x where the position is outside the table. The select runs as a bit select
+    // on a mask the compiler cannot see is uniform (a vector copy it does not look
+    // through); a select on a uniform condition would become a branch, with the (cos, sin)
+    // load moved into it and waited for late.
+    uint32_t rot_mask;
+    asm("v_mov_b32 %0, %1" : "=v"(rot_mask) : "s"(rotate ? ~0u : 0u));
 
-    float inv_rms_lanes = 0.f;  // lane r: 1 / rms of row r
+    float inv_rms_lanes = 0.f;  // lane r: 1 / rms of row h0 + r
     if constexpr (kNorm) {
         float totals = 0.f;
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
+        for (int r = 0; r < kRowsPerWave; ++r) {
             const float sum = row_sum_squares(lo_f(w[r]), hi_f(w[r]));
             const float sum0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sum), 0));
             totals = lane == r ? sum0 : totals;
@@ -169,47 +189,40 @@ __global__ __launch_bounds__(256) void qkv_prologue_d128_kernel(PrologueArgs a) 
         inv_rms_lanes = 1.0f / sqrtf(bf16_round(totals) / static_cast<float>(D) + a.eps);
     }
 
-    uint32_t out[R];
+    uint32_t out[kRowsPerWave];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const bool is_q = lh[r] < a.nq;
+    for (int r = 0; r < kRowsPerWave; ++r) {
         uint32_t x = w[r];
         if constexpr (kNorm) {
             const float inv = __int_as_float(
                 __builtin_amdgcn_readlane(__float_as_int(inv_rms_lanes), r));
-            x = pack_bf16x2((lo_f(x) * inv) * (is_q ? qw0 : kw0),
-                            (hi_f(x) * inv) * (is_q ? qw1 : kw1));
+            x = pack_bf16x2((lo_f(x) * inv) * nw0, (hi_f(x) * inv) * nw1);
         }
         // Partner elements 2l+64, 2l+65 (lane l < 32) or 2l-64, 2l-63 (lane l >= 32).
         // v_permlane32_swap moves VSRC's lanes 0..31 into VDST's lanes 32..63 and VDST's
         // lanes 32..63 into VSRC's lanes 0..31; with both operands x, the returned VSRC
-        // (element 1) holds x[l + 32] in lanes 0..31 and the returned VDST (element 0) holds
-        // x[l - 32] in lanes 32..63.
+        // (element 1) holds x[l + 32] in lanes 0..31 and the returned VDST (element 0)
+        // holds x[l - 32] in lanes 32..63, while the lane's own x survives in the other
+        // register (VDST keeps lanes 0..31, VSRC keeps lanes 32..63).
         const auto sw = __builtin_amdgcn_permlane32_swap(x, x, false, false);
-        const uint32_t partner = lo_half ? sw[1] : sw[0];
-        const float s0 = __uint_as_float(__float_as_uint(cs[r].y) ^ sin_sign);
-        const float s1 = __uint_as_float(__float_as_uint(cs[r].w) ^ sin_sign);
-        const uint32_t rotated = pack_bf16x2(lo_f(x) * cs[r].x + lo_f(partner) * s0,
-                                             hi_f(x) * cs[r].z + hi_f(partner) * s1);
-        const int pos = pos_r[r];
-        out[r] = (pos >= 0 && pos < a.rope_max) ? rotated : x;
+        const uint32_t partner = (lo_half ? sw[1] : sw[0]) ^ partner_sign;
+        x = lo_half ? sw[0] : sw[1];
+        const uint32_t rotated = pack_bf16x2(lo_f(x) * cs.x + lo_f(partner) * cs.y,
+                                             hi_f(x) * cs.z + hi_f(partner) * cs.w);
+        out[r] = x ^ ((x ^ rotated) & rot_mask);
     }
 
+    // A skipped slot gets an empty descriptor (its stores are dropped) rather than an early
+    // return, which would let the compiler move the math and the (cos, sin) load behind it.
+    const uint32_t dst_bytes = section == 1 && !slot_ok ? 0u : static_cast<uint32_t>(n) * kRowBytes;
+    // both candidate addresses are computed and one selected: no branch between the loads
+    // and the stores, which would again invite the compiler to sink the loads
+    __bf16* const q_row = a.q_out + (static_cast<int64_t>(t) * a.nq + h0) * D;
+    __bf16* const k_row = a.k_cache + kv_row;
+    const auto dst = make_rsrc(section == 0 ? q_row : k_row, dst_bytes);
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int tt = tok[r];
-        if (tt < 0) break;
-        if (lh[r] < a.nq) {
-            reinterpret_cast<uint32_t*>(a.q_out + (static_cast<int64_t>(tt) * a.nq + lh[r]) * D)
-                [lane] = out[r];
-            continue;
-        }
-        const int slot = slot_r[r];
-        if (slot < 0 || slot >= a.max_slots) continue;
-        const int64_t dst = (static_cast<int64_t>(slot) * a.nkv + (lh[r] - a.nq)) * D;
-        reinterpret_cast<uint32_t*>(a.k_cache + dst)[lane] = out[r];
-        reinterpret_cast<uint32_t*>(a.v_cache + dst)[lane] = v[r];
-    }
+    for (int r = 0; r < kRowsPerWave; ++r)  // rows past n fall outside the descriptor
+        __builtin_amdgcn_raw_buffer_store_b32(out[r], dst, lane_off + r * kRowBytes, 0, 0);
 }
 
 // Any head_dim: one 256-thread workgroup per (token, head) row, the reference's layout.
@@ -325,26 +338,25 @@ hipError_t qkv_prologue(const void* qkv, const void* q_norm_w, const void* k_nor
     // The fast path takes both norm weights or neither (one alone goes to the generic kernel).
     const bool norm_pair = (q_norm_w == nullptr) == (k_norm_w == nullptr);
     if (qkv_prologue_fast_supported(head_dim) && aligned && norm_pair) {
-        // Eight rows per wave once the grid still has a few thousand workgroups; small
-        // (decode-batch) launches keep one row per wave for the shortest latency.
-        constexpr int kBig = 8;
-        const int64_t big_groups = (rows + kBig * kWavesPerGroup - 1) / (kBig * kWavesPerGroup);
-        const int64_t small_groups = (rows + kWavesPerGroup - 1) / kWavesPerGroup;
-        const bool norm = q_norm_w != nullptr;
-        if (big_groups >= 2048) {
-            if (norm)
-                qkv_prologue_d128_kernel<kBig, true>
-                    <<<static_cast<unsigned>(big_groups), 256, 0, stream>>>(a);
+        auto launch = [&](auto rows_tag) {
+            constexpr int kRows = decltype(rows_tag)::value;
+            const int64_t groups = (num_q_heads + kRows - 1) / kRows +
+                                   2 * ((num_kv_heads + kRows - 1) / kRows);
+            const int64_t waves = static_cast<int64_t>(num_tokens) * groups;
+            const unsigned grid =
+                static_cast<unsigned>((waves + kWavesPerGroup - 1) / kWavesPerGroup);
+            if (q_norm_w != nullptr)
+                qkv_prologue_d128_kernel<kRows, true><<<grid, 256, 0, stream>>>(a);
             else
-                qkv_prologue_d128_kernel<kBig, false>
-                    <<<static_cast<unsigned>(big_groups), 256, 0, stream>>>(a);
-        } else if (norm) {
-            qkv_prologue_d128_kernel<1, true>
-                <<<static_cast<unsigned>(small_groups), 256, 0, stream>>>(a);
-        } else {
-            qkv_prologue_d128_kernel<1, false>
-                <<<static_cast<unsigned>(small_groups), 256, 0, stream>>>(a);
-        }
+                qkv_prologue_d128_kernel<kRows, false><<<grid, 256, 0, stream>>>(a);
+        };
+        // Eight rows per wavefront keep enough loads in flight to stream HBM once there are
+        // thousands of wavefronts; decode-size launches take two rows per wavefront, which
+        // spreads them over more CUs and shortens each wavefront's dependent chain.
+        if (static_cast<int64_t>(num_tokens) * (num_q_heads + 2 * num_kv_heads) >= 16384 * 8)
+            launch(std::integral_constant<int, 8>{});
+        else
+            launch(std::integral_constant<int, 2>{});
     } else {
         qkv_prologue_generic_kernel<<<static_cast<unsigned>(rows), 256,
                                       static_cast<size_t>(head_dim) * sizeof(float), stream>>>(a);

@@ -78,6 +78,13 @@ def test_head_dim_128_fast_path(gpu, t, nq, nkv):
     assert dq < 0.01 and dk < 0.01
 
 
+@pytest.mark.parametrize("t,nq,nkv", [(3000, 32, 8), (8000, 14, 2)])
+def test_large_launch_eight_row_path(gpu, t, nq, nkv):
+    # at least 131072 (token, head) rows selects eight rows per wavefront; 14 and 2 heads
+    # leave partial groups in every section
+    _run(gpu, 600 + nq, t, nq, nkv, 128, slots=2 * t)
+
+
 @pytest.mark.parametrize("hd", [64, 96, 256, 2, 130])
 def test_other_head_dims(gpu, hd):
     _run(gpu, 200 + hd, 9, 8, 2, hd, slots=32)
