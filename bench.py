@@ -1,6 +1,6 @@
 """Benchmark of the paged-attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5,6] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5,6,7] [--no-cpu]
 
 One "step" is one pass of the hot path over one batch of synthetic input already resident in
 HBM. The headline (the JSON `value`) is BASELINE.json's decode metric on configs[1]: batched
@@ -8,7 +8,8 @@ paged decode, batch 64, Qwen3-0.6B heads (16 q / 8 kv, d=128), contexts U[128, 4
 step = KV-cache write of the 64 new tokens + decode attention; value = algorithmic KV bytes
 read per step (K+V of every context position, once per (sequence, kv_head)) / step time.
 The other configurations are reported under "configs"; "6" is the fused decode prologue
-(split QKV + q/k RMSNorm + RoPE + KV write in one launch), in algorithmic bytes per second. rank 0 prints ONE JSON line.
+(split QKV + q/k RMSNorm + RoPE + KV write in one launch), in algorithmic bytes per second;
+"7" is the per-step batch metadata built on the device, beside the reference's host path. rank 0 prints ONE JSON line.
 
 Timing: W untimed warm-up steps, then exactly K steps bracketed by device synchronisation;
 per-op kernel time is measured with HIP events recorded on the stream the kernels run on.
@@ -186,6 +187,46 @@ def cpu_prologue_baseline(w: W.PrologueWorkload, budget_s: float):
     return (time.perf_counter() - t0) / reps, reps
 
 
+def batch_items(rng, batch: int, ctx_lo: int, ctx_hi: int, new_tokens: int, decode: bool):
+    """Compact per-item records of one step (tokens in the cache, new tokens, flags, block
+    lists as CSR) with distinct random blocks."""
+    ctx = rng.integers(ctx_lo, ctx_hi + 1, batch).astype(np.int64) + new_tokens
+    kvw = (ctx - new_tokens).astype(np.int32)
+    new = np.full(batch, new_tokens, np.int32)
+    flags = np.full(batch, 1 if decode else 2, np.int32)
+    counts = -(-ctx // 16)
+    start = np.zeros(batch + 1, np.int32)
+    start[1:] = np.cumsum(counts)
+    blocks = rng.permutation(int(start[-1]) * 2)[:start[-1]].astype(np.int32)
+    return kvw, new, flags, start, blocks, int(counts.max()), int(start[-1]) * 2
+
+
+def host_metadata_path(items, T, mbpr, ncb, dev, reps: int):
+    """The reference's host path for one step, timed: build the arrays on the host (the
+    oracle restates BatchTranslator's loops), upload them with seven synchronous copies
+    (batch_translator.cpp:387-420), copy four back and check them (model_runner.h:102-171).
+    Returns ms per step."""
+    import oracle
+    kvw, new, flags, start, blocks = items
+    b = len(kvw)
+    bufs = {k: torch.empty(n, dtype=torch.int32, device=dev)
+            for k, n in (("tok", T), ("pos", T), ("sm", T), ("bt", b * mbpr), ("qsl", b + 1),
+                         ("ctx", b), ("li", b))}
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        st, o = oracle.build_batch_metadata(kvw, new, flags, start, blocks, T, mbpr, 16, ncb)
+        host = {"tok": o["positions"], "pos": o["positions"], "sm": o["slot_mapping"],
+                "bt": o["block_table"].ravel(), "qsl": o["query_start_loc"],
+                "ctx": o["context_lens"], "li": o["logits_indices"]}
+        for k, v in host.items():
+            bufs[k].copy_(torch.from_numpy(v))
+        torch.cuda.synchronize()
+        for k in ("qsl", "pos", "ctx", "li"):
+            v = bufs[k].cpu().numpy()
+            assert v.size > 0
+    return (time.perf_counter() - t0) * 1e3 / reps
+
+
 def prefill_pair_flops(w: W.PagedWorkload, pairs) -> int:
     """FLOPs of the (query row, head) pairs: 4*D per visible key."""
     qsl = w.query_start_loc
@@ -301,6 +342,36 @@ def run(args):
             out[key] = r
             del w
 
+    if 7 in configs:
+        # per-step metadata built on the device (BatchTranslator's arrays + checks) for the
+        # configs[1] decode batch and the configs[2] prefill batch
+        lib = _lib.load()
+        rng = np.random.default_rng(7)
+        for key, shape in (("7_batch_meta_decode_b64", (64, 128, 4096, 1, True)),
+                           ("7_batch_meta_prefill_8x1536", (8, 512, 512, 1536, False))):
+            kvw, new, flags, start, blocks, mbpr, ncb = batch_items(rng, *shape)
+            T = int(new.sum())
+            d = [torch.from_numpy(a).to(dev) for a in (kvw, new, flags, start, blocks)]
+            outs = [torch.empty(n, dtype=torch.int32, device=dev)
+                    for n in (T, T, len(kvw) * mbpr, len(kvw) + 1, len(kvw), len(kvw), 1)]
+
+            def build():
+                rc = lib.ccinfer_build_batch_metadata(
+                    *[t.data_ptr() for t in d], len(kvw), T, len(blocks), mbpr, 16, ncb,
+                    *[t.data_ptr() for t in outs], stream.cuda_stream)
+                assert rc == 0, rc
+            ms, host_ms = time_loop(build, max(args.steps, 50), args.warmup, stream)
+            assert int(outs[-1].item()) == 0
+            r = {"ms_per_step": ms, "host_ms_per_step": host_ms, "batch": len(kvw),
+                 "tokens": T, "max_blocks_per_req": mbpr}
+            if not args.no_cpu:
+                r["reference_host_path_ms"] = host_metadata_path(
+                    (kvw, new, flags, start, blocks), T, mbpr, ncb, dev, 20)
+                r["reference_host_path_note"] = ("host build (oracle restatement of the "
+                                                 "translator loops) + 7 uploads + sync + "
+                                                 "4 validation copy-backs")
+            out[key] = r
+
     torch.cuda.synchronize()
     return head, out, nt
 
@@ -336,7 +407,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--configs", default="1,2,3,4,5,6")
+    ap.add_argument("--configs", default="1,2,3,4,5,6,7")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=5.0)
     ap.add_argument("--profile-op", choices=["decode", "write", "prefill", "mixed", "long",

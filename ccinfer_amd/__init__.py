@@ -5,7 +5,10 @@ Python host side: a ctypes binding of the C ABI (`_lib`), torch-facing operators
 the reference's backend ops (`ops`), and seeded synthetic workloads (`workloads`).
 """
 from .ops import (  # noqa: F401
+    ITEM_DECODE,
+    ITEM_SAMPLE,
     CcinferError,
+    build_batch_metadata,
     decode_attention,
     decode_workspace_size,
     prefill_attention,
@@ -15,7 +18,10 @@ from .ops import (  # noqa: F401
 )
 
 __all__ = [
+    "ITEM_DECODE",
+    "ITEM_SAMPLE",
     "CcinferError",
+    "build_batch_metadata",
     "decode_attention",
     "decode_workspace_size",
     "prefill_attention",

@@ -20,6 +20,7 @@ SIGNATURES = {
         _c_int,
         [_vp] * 9 + [_c_int] * 6 + [ctypes.c_float, _vp],
     ),
+    "ccinfer_build_batch_metadata": (_c_int, [_vp] * 5 + [_c_int] * 6 + [_vp] * 8),
     "ccinfer_decode_workspace_size": (_c_size, [_c_int] * 6),
     "ccinfer_decode_attention": (
         _c_int,

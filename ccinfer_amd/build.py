@@ -44,6 +44,7 @@ SOURCES = [
     CSRC / "prefill_attn.hip",
     CSRC / "generic_attn.hip",
     CSRC / "qkv_prologue.hip",
+    CSRC / "batch_meta.hip",
     CSRC / "capi.cpp",
     CSRC / "dropin" / "launchers.cpp",
     CSRC / "dropin" / "hip_backend.cpp",

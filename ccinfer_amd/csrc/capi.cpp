@@ -130,6 +130,32 @@ int ccinfer_qkv_prologue(const void* qkv, const void* q_norm_weight, const void*
                                       as_stream(stream)));
 }
 
+int ccinfer_build_batch_metadata(const int32_t* item_kv_written, const int32_t* item_new_tokens,
+                                 const int32_t* item_flags, const int32_t* item_block_start,
+                                 const int32_t* blocks, int batch_size, int num_tokens,
+                                 int total_blocks, int max_blocks_per_req, int block_size,
+                                 int num_cache_blocks, int32_t* positions, int32_t* slot_mapping,
+                                 int32_t* block_table, int32_t* query_start_loc,
+                                 int32_t* context_lens, int32_t* logits_indices, int32_t* status,
+                                 void* stream) {
+    if (!item_kv_written || !item_new_tokens || !item_flags || !item_block_start || !positions ||
+        !slot_mapping || !block_table || !query_start_loc || !context_lens || !logits_indices ||
+        !status)
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    if (total_blocks > 0 && !blocks) return CCINFER_ERR_INVALID_ARGUMENT;
+    if (batch_size <= 0 || num_tokens <= 0 || total_blocks < 0 || max_blocks_per_req <= 0 ||
+        block_size <= 0 || num_cache_blocks <= 0)
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    if (!fits_int(static_cast<int64_t>(batch_size) * max_blocks_per_req) ||
+        !fits_int(static_cast<int64_t>(num_cache_blocks) * block_size))
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    return map_hip_error(build_batch_metadata(
+        item_kv_written, item_new_tokens, item_flags, item_block_start, blocks, batch_size,
+        num_tokens, total_blocks, max_blocks_per_req, block_size, num_cache_blocks, positions,
+        slot_mapping, block_table, query_start_loc, context_lens, logits_indices, status,
+        as_stream(stream)));
+}
+
 size_t ccinfer_decode_workspace_size(int batch_size, int max_blocks_per_req, int num_q_heads,
                                      int num_kv_heads, int head_dim, int cache_block_size) {
     if (!decode_shape_ok(batch_size, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,

@@ -75,6 +75,19 @@ hipError_t prefill_attention(const void* q, const void* k_cache, const void* v_c
                              int num_kv_heads, int head_dim, int block_size, void* workspace,
                              hipStream_t stream);
 
+// ---- per-step batch metadata built on the device ------------------------------
+constexpr int kItemDecode = 1;  // item flag: decode item (exactly one new token)
+constexpr int kItemSample = 2;  // item flag: sample the item's last token
+
+hipError_t build_batch_metadata(const int32_t* item_kv_written, const int32_t* item_new_tokens,
+                                const int32_t* item_flags, const int32_t* item_block_start,
+                                const int32_t* blocks, int batch_size, int num_tokens,
+                                int total_blocks, int max_blocks_per_req, int block_size,
+                                int num_cache_blocks, int32_t* positions, int32_t* slot_mapping,
+                                int32_t* block_table, int32_t* query_start_loc,
+                                int32_t* context_lens, int32_t* logits_indices, int32_t* status,
+                                hipStream_t stream);
+
 // ---- fused decode-side prologue: split QKV, q/k RMSNorm, RoPE, KV write -----
 bool qkv_prologue_fast_supported(int head_dim);
 

@@ -1,7 +1,8 @@
 """Torch-facing operators over the C ABI, mirroring the reference's backend ops.
 
 Reference interface: DeviceBackend::{write_kv_cache, decode_attention, prefill_attention}
-(plus qkv_prologue, one launch for split_qkv + rms_norm + rope + write_kv_cache)
+(plus qkv_prologue, one launch for split_qkv + rms_norm + rope + write_kv_cache, and
+build_batch_metadata, BatchTranslator's per-step arrays built on the device)
 (src/backend/backend.h:172-223) with the parameter structs of src/backend/params.h:148-211.
 Argument names, meaning and error behaviour follow it: invalid arguments raise
 CcinferError with code ErrorCode::InvalidArgument (6), the same value the reference returns.
@@ -132,6 +133,47 @@ def qkv_prologue(qkv: torch.Tensor, q_norm_weight: Optional[torch.Tensor],
                                     slots if max_slots is None else max_slots, float(eps),
                                     _stream()), op)
     return q_out
+
+
+ITEM_DECODE = 1  # decode item: one new token, always sampled
+ITEM_SAMPLE = 2  # prefill chunk whose last token needs logits
+
+
+def build_batch_metadata(item_kv_written: torch.Tensor, item_new_tokens: torch.Tensor,
+                         item_flags: torch.Tensor, item_block_start: torch.Tensor,
+                         blocks: torch.Tensor, num_tokens: int, max_blocks_per_req: int,
+                         num_cache_blocks: int, block_size: int = 16,
+                         out: Optional[dict] = None) -> dict:
+    """One step's attention metadata built on the device (the arrays of
+    src/worker/batch_translator.cpp:213-302 and the checks of src/model/model_runner.h:
+    102-171). Returns int32 device tensors positions, slot_mapping, block_table,
+    query_start_loc, context_lens, logits_indices and status ([1]: 0 or 6). Nothing is
+    synchronised: read `status` when the result is needed. `out` reuses tensors of an
+    earlier call with the same shapes."""
+    op = "build_batch_metadata"
+    for t in (item_kv_written, item_new_tokens, item_flags, item_block_start, blocks):
+        _dev_tensor(t, torch.int32, op)
+    b = item_kv_written.numel()
+    _require(b > 0 and item_new_tokens.numel() == b and item_flags.numel() == b, op)
+    _require(item_block_start.numel() == b + 1, op)
+    dev = item_kv_written.device
+    shapes = {"positions": (num_tokens,), "slot_mapping": (num_tokens,),
+              "block_table": (b, max_blocks_per_req), "query_start_loc": (b + 1,),
+              "context_lens": (b,), "logits_indices": (b,), "status": (1,)}
+    if out is None:
+        out = {k: torch.empty(v, dtype=torch.int32, device=dev) for k, v in shapes.items()}
+    for k, v in shapes.items():
+        _dev_tensor(out[k], torch.int32, op)
+        _require(tuple(out[k].shape) == v, op)
+    lib = _lib.load()
+    _check(lib.ccinfer_build_batch_metadata(
+        _ptr(item_kv_written), _ptr(item_new_tokens), _ptr(item_flags), _ptr(item_block_start),
+        _ptr(blocks) if blocks.numel() else None, b, num_tokens, blocks.numel(),
+        max_blocks_per_req, block_size, num_cache_blocks, _ptr(out["positions"]),
+        _ptr(out["slot_mapping"]), _ptr(out["block_table"]), _ptr(out["query_start_loc"]),
+        _ptr(out["context_lens"]), _ptr(out["logits_indices"]), _ptr(out["status"]),
+        _stream()), op)
+    return out
 
 
 def decode_workspace_size(batch_size: int, max_blocks_per_req: int, num_q_heads: int,

@@ -71,6 +71,33 @@ int ccinfer_qkv_prologue(const void* qkv, const void* q_norm_weight, const void*
                          int num_tokens, int num_q_heads, int num_kv_heads, int head_dim,
                          int rope_cache_max_position, int max_slots, float eps, void* stream);
 
+/* Item flags of ccinfer_build_batch_metadata. */
+#define CCINFER_ITEM_DECODE 1 /* decode item: exactly one new token, always sampled */
+#define CCINFER_ITEM_SAMPLE 2 /* prefill chunk whose last token needs logits */
+
+/* Builds one step's attention metadata on the device, replacing the host array building
+ * and uploads of BatchTranslator::translate (src/worker/batch_translator.cpp:213-302,
+ * 305-420) and ModelRunner's blocking copy-back validation (src/model/model_runner.h:
+ * 102-171). Inputs (device, int32): per item i < batch_size the tokens already in the
+ * cache (item_kv_written), the new tokens (item_new_tokens), flags (CCINFER_ITEM_*), and
+ * its block list after this step's allocation, as blocks[item_block_start[i] ..
+ * item_block_start[i + 1]) (total_blocks entries in all; blocks may be NULL when 0).
+ * Outputs (device, int32): positions[num_tokens], slot_mapping[num_tokens],
+ * block_table[batch_size][max_blocks_per_req] (-1 padded), query_start_loc[batch_size + 1],
+ * context_lens[batch_size], logits_indices[batch_size] (-1 = no sample), exactly as the
+ * reference's host loops write them; and status[0] = 0, or CCINFER_ERR_INVALID_ARGUMENT
+ * when a check of model_runner.h fails (entries that fail are written as -1). The status
+ * word is written by every call (no clearing needed) and is read by the caller when it
+ * chooses -- the call itself never synchronises. */
+int ccinfer_build_batch_metadata(const int32_t* item_kv_written, const int32_t* item_new_tokens,
+                                 const int32_t* item_flags, const int32_t* item_block_start,
+                                 const int32_t* blocks, int batch_size, int num_tokens,
+                                 int total_blocks, int max_blocks_per_req, int block_size,
+                                 int num_cache_blocks, int32_t* positions, int32_t* slot_mapping,
+                                 int32_t* block_table, int32_t* query_start_loc,
+                                 int32_t* context_lens, int32_t* logits_indices, int32_t* status,
+                                 void* stream);
+
 /* Workspace bytes ccinfer_decode_attention needs for this batch shape (may be 0). */
 size_t ccinfer_decode_workspace_size(int batch_size, int max_blocks_per_req, int num_q_heads,
                                      int num_kv_heads, int head_dim, int cache_block_size);

@@ -48,6 +48,8 @@ def load() -> ctypes.CDLL:
         lib.orc_rms_norm.argtypes = [_P, _P, _P, _I, _I, ctypes.c_float]
         lib.orc_rope.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I]
         lib.orc_qkv_prologue.argtypes = [_P] * 11 + [_I] * 6 + [ctypes.c_float]
+        lib.orc_build_batch_metadata.argtypes = [_P] * 5 + [_I] * 6 + [_P] * 6
+        lib.orc_build_batch_metadata.restype = _I
         _lib = lib
     return _lib
 
@@ -217,3 +219,36 @@ def rope_cache_table(max_position: int, rotary_dim: int, theta: float) -> np.nda
                                       pairs * np.float32(2) / np.float32(rotary_dim))).astype(np.float32)
     ang = (np.arange(max_position, dtype=np.float32)[:, None] * inv[None, :]).astype(np.float32)
     return np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float32)
+
+
+# ---- per-step batch metadata (block table, slot mapping, positions, ...) ----
+
+ITEM_DECODE = 1
+ITEM_SAMPLE = 2
+
+
+def build_batch_metadata(kv_written, new_tokens, flags, block_start, blocks, num_tokens: int,
+                         max_blocks_per_req: int, block_size: int, num_cache_blocks: int):
+    """Returns (status, dict of int32 arrays) -- the arrays BatchTranslator builds on the host."""
+    kvw = _c(kv_written, np.int32)
+    nt = _c(new_tokens, np.int32)
+    fl = _c(flags, np.int32)
+    bst = _c(block_start, np.int32)
+    blk = _c(blocks, np.int32) if len(blocks) else np.zeros(1, np.int32)
+    b = kvw.shape[0]
+    out = {
+        "positions": np.full(max(num_tokens, 1), -7, np.int32),
+        "slot_mapping": np.full(max(num_tokens, 1), -7, np.int32),
+        "block_table": np.full((b, max_blocks_per_req), -7, np.int32),
+        "query_start_loc": np.full(b + 1, -7, np.int32),
+        "context_lens": np.full(b, -7, np.int32),
+        "logits_indices": np.full(b, -7, np.int32),
+    }
+    st = load().orc_build_batch_metadata(
+        _p(kvw), _p(nt), _p(fl), _p(bst), _p(blk), b, num_tokens, len(blocks), max_blocks_per_req,
+        block_size, num_cache_blocks, _p(out["positions"]), _p(out["slot_mapping"]),
+        _p(out["block_table"]), _p(out["query_start_loc"]), _p(out["context_lens"]),
+        _p(out["logits_indices"]))
+    out["positions"] = out["positions"][:num_tokens]
+    out["slot_mapping"] = out["slot_mapping"][:num_tokens]
+    return int(st), out

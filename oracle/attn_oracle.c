@@ -457,3 +457,88 @@ void orc_qkv_prologue(const uint16_t* qkv, const uint16_t* q_norm_w, const uint1
     orc_rope(q_out, k_tmp, positions, rope_cache, T, nq, nkv, hd, hd, rope_cache_max_position);
     orc_write_kv_cache(k_tmp, v_tmp, k_cache, v_cache, slot_mapping, T, nkv, hd, max_slots);
 }
+
+/* ------------------------------------------------------------------------- */
+/* Batch metadata: the host loops of src/worker/batch_translator.cpp:213-302    */
+/* (slot = table[pos / bs] * bs + pos % bs; positions kv_written + t; table     */
+/* rows -1 padded; query_start_loc prefix sums; context_lens kv_written + new;  */
+/* logits index = the item's last token, or -1 for a prefill chunk that does    */
+/* not sample) with the validation of src/model/model_runner.h:102-171 (query   */
+/* lengths > 0 and 1 for decode items, qsl[B] == T, positions >= 0,             */
+/* 0 < ctx <= max_blocks_per_req * bs, max_blocks_per_req * bs <= max_slots)    */
+/* and the translator's own bound (an item needs ceil(ctx / bs) blocks,         */
+/* batch_translator.cpp:196-211); block ids must lie in [0, num_cache_blocks).  */
+/* ------------------------------------------------------------------------- */
+static int32_t clamp_i32(int64_t v) { return (int32_t)(v < 0x7fffffff ? v : 0x7fffffff); }
+
+int orc_build_batch_metadata(const int32_t* item_kv_written, const int32_t* item_new_tokens,
+                             const int32_t* item_flags, const int32_t* item_block_start,
+                             const int32_t* blocks, int batch_size, int num_tokens,
+                             int total_blocks, int max_blocks_per_req, int block_size,
+                             int num_cache_blocks,
+                             int32_t* positions, int32_t* slot_mapping, int32_t* block_table,
+                             int32_t* query_start_loc, int32_t* context_lens,
+                             int32_t* logits_indices) {
+    const int B = batch_size, T = num_tokens, mbpr = max_blocks_per_req, bs = block_size;
+    int status = 0;
+    if (mbpr > num_cache_blocks) status = 6;
+    int64_t offset = 0;
+    for (int i = 0; i < B; ++i) {
+        const int len = item_new_tokens[i];
+        const int kvw = item_kv_written[i];
+        const int flags = item_flags[i];
+        const int64_t ctx = (int64_t)kvw + len;
+        const int b0 = item_block_start[i];
+        const int b1 = item_block_start[i + 1];
+        int nblk = b1 - b0;
+        if (b0 < 0 || b1 < b0 || b1 > total_blocks) {
+            status = 6;
+            nblk = 0;
+        }
+        if (len <= 0) status = 6;
+        if ((flags & ORC_ITEM_DECODE) && len != 1) status = 6;
+        if (kvw < 0) status = 6;
+        if (ctx <= 0 || ctx > (int64_t)mbpr * bs) status = 6;
+        if (nblk > mbpr || (ctx > 0 && nblk < (ctx + bs - 1) / bs)) status = 6;
+
+        const int n = len > 0 ? len : 0;
+        /* offsets and lengths past INT_MAX (only in a failing batch) are stored as INT_MAX */
+        query_start_loc[i] = clamp_i32(offset);
+        context_lens[i] = clamp_i32(ctx);
+        logits_indices[i] =
+            (flags & (ORC_ITEM_DECODE | ORC_ITEM_SAMPLE)) ? clamp_i32(offset + n - 1) : -1;
+        for (int t = 0; t < n; ++t) {
+            const int64_t tok = offset + t;
+            if (tok >= T) break;
+            const int64_t pos = (int64_t)kvw + t;
+            positions[tok] = (int32_t)pos;
+            int32_t slot = -1;
+            if (pos >= 0) {
+                const int64_t bidx = pos / bs;
+                if (bidx < nblk) {
+                    const int blk = blocks[b0 + bidx];
+                    if (blk >= 0 && blk < num_cache_blocks)
+                        slot = (int32_t)((int64_t)blk * bs + pos % bs);
+                    else
+                        status = 6;
+                }
+            }
+            slot_mapping[tok] = slot;
+        }
+        for (int b = 0; b < mbpr; ++b) {
+            int32_t v = -1;
+            if (b < nblk) {
+                const int blk = blocks[b0 + b];
+                if (blk >= 0 && blk < num_cache_blocks)
+                    v = blk;
+                else
+                    status = 6;
+            }
+            block_table[(int64_t)i * mbpr + b] = v;
+        }
+        offset += n;
+    }
+    query_start_loc[B] = clamp_i32(offset);
+    if (offset != T) status = 6;
+    return status;
+}

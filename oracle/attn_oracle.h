@@ -22,6 +22,8 @@
  *                               of src/kernel/cuda_common.cuh:14-62
  *   - orc_rope                : src/kernel/pos/rope.cu:14-43
  *   - orc_qkv_prologue        : the sequence of src/model/qwen3/qwen3_model.cpp:174-244
+ *   - orc_build_batch_metadata: the arrays of src/worker/batch_translator.cpp:213-302 and
+ *                               the checks of src/model/model_runner.h:102-171
  *
  * Every function is pinned by tests/test_oracle.py (known-answer vectors from the
  * reference tests, closed forms, torch's float64 scaled_dot_product_attention as an
@@ -104,6 +106,24 @@ void orc_qkv_prologue(const uint16_t* qkv, const uint16_t* q_norm_w, const uint1
                       const int32_t* slot_mapping, uint16_t* q_out, uint16_t* k_tmp,
                       uint16_t* v_tmp, uint16_t* k_cache, uint16_t* v_cache, int T, int nq,
                       int nkv, int hd, int rope_cache_max_position, int max_slots, float eps);
+
+/* Per-step attention metadata from compact per-item records (one item = one sequence of
+ * the batch). item_flags: bit 0 = decode item (exactly one new token), bit 1 = sample the
+ * item's last token (a prefill chunk that needs logits); decode items are always sampled.
+ * item_block_start [B + 1] indexes `blocks`, the concatenated block tables (after this
+ * step's allocation) of the items; `blocks` holds total_blocks entries, and an item whose
+ * range does not lie inside it is treated as having no blocks. Returns 0, or 6 (InvalidArgument) when a check fails;
+ * failing entries are written sanitised (slot -1, table entry -1). */
+#define ORC_ITEM_DECODE 1
+#define ORC_ITEM_SAMPLE 2
+int orc_build_batch_metadata(const int32_t* item_kv_written, const int32_t* item_new_tokens,
+                             const int32_t* item_flags, const int32_t* item_block_start,
+                             const int32_t* blocks, int batch_size, int num_tokens,
+                             int total_blocks, int max_blocks_per_req, int block_size,
+                             int num_cache_blocks,
+                             int32_t* positions, int32_t* slot_mapping, int32_t* block_table,
+                             int32_t* query_start_loc, int32_t* context_lens,
+                             int32_t* logits_indices);
 
 #ifdef __cplusplus
 }

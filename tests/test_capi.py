@@ -150,3 +150,22 @@ def test_qkv_prologue_validation(lib):
     assert _prologue(lib, d=1026) == INVALID
     assert _prologue(lib, eps=0.0) == INVALID         # backend.h:84
     assert _prologue(lib, eps=float("nan")) == INVALID
+
+
+def _meta(lib, **kw):
+    a = dict(kvw=FAKE, nt=FAKE, fl=FAKE, bst=FAKE, blk=FAKE, b=4, t=8, nb=6, mbpr=4, bs=16,
+             ncb=64, pos=FAKE, sm=FAKE, bt=FAKE, qsl=FAKE, ctx=FAKE, li=FAKE, st=FAKE)
+    a.update(kw)
+    return lib.ccinfer_build_batch_metadata(
+        a["kvw"], a["nt"], a["fl"], a["bst"], a["blk"], a["b"], a["t"], a["nb"], a["mbpr"],
+        a["bs"], a["ncb"], a["pos"], a["sm"], a["bt"], a["qsl"], a["ctx"], a["li"], a["st"], None)
+
+
+def test_build_batch_metadata_validation(lib):
+    for ptr in ["kvw", "nt", "fl", "bst", "blk", "pos", "sm", "bt", "qsl", "ctx", "li", "st"]:
+        assert _meta(lib, **{ptr: None}) == INVALID, ptr
+    for field in ["b", "t", "mbpr", "bs", "ncb"]:
+        assert _meta(lib, **{field: 0}) == INVALID, field
+    assert _meta(lib, nb=-1) == INVALID
+    assert _meta(lib, b=1 << 16, mbpr=1 << 16) == INVALID      # table entries overflow int
+    assert _meta(lib, ncb=1 << 28, bs=16) == INVALID           # cache slots overflow int
