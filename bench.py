@@ -1,6 +1,6 @@
 """Benchmark of the paged-attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5,6,7] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5,6,7,8] [--no-cpu]
 
 One "step" is one pass of the hot path over one batch of synthetic input already resident in
 HBM. The headline (the JSON `value`) is BASELINE.json's decode metric on configs[1]: batched
@@ -9,7 +9,9 @@ step = KV-cache write of the 64 new tokens + decode attention; value = algorithm
 read per step (K+V of every context position, once per (sequence, kv_head)) / step time.
 The other configurations are reported under "configs"; "6" is the fused decode prologue
 (split QKV + q/k RMSNorm + RoPE + KV write in one launch), in algorithmic bytes per second;
-"7" is the per-step batch metadata built on the device, beside the reference's host path. rank 0 prints ONE JSON line.
+"7" is the per-step batch metadata built on the device, beside the reference's host path;
+"8" is decode over an fp8 (E4M3, per-row scale) cache, in bytes actually read and in the
+bf16 bytes the same attention covers. rank 0 prints ONE JSON line.
 
 Timing: W untimed warm-up steps, then exactly K steps bracketed by device synchronisation;
 per-op kernel time is measured with HIP events recorded on the stream the kernels run on.
@@ -372,6 +374,47 @@ def run(args):
                                                  "4 validation copy-backs")
             out[key] = r
 
+    if 8 in configs:
+        # fp8 KV cache: the configs[1] and configs[4] batches with their caches quantised by
+        # the fp8 write kernel; bytes = K+V bytes plus the row scales actually read
+        lib = _lib.load()
+        for key, make in (("8_fp8_decode_b64_ctx128-4096", W.decode_batched),
+                          ("8_fp8_decode_b32_ctx32768_gqa4", W.decode_long)):
+            w = make(device=dev)
+            slots = w.k_cache.shape[0]
+            kc = torch.empty((slots, w.hkv, w.d), dtype=torch.uint8, device=dev)
+            vc = torch.empty_like(kc)
+            nsc = -(-slots // 16) * 16 * w.hkv
+            ks = torch.empty(nsc, dtype=torch.float32, device=dev)
+            vs = torch.empty_like(ks)
+            ident = torch.arange(slots, dtype=torch.int32, device=dev)
+            rc = lib.ccinfer_write_kv_cache_fp8(
+                w.k_cache.data_ptr(), w.v_cache.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                ks.data_ptr(), vs.data_ptr(), ident.data_ptr(), slots, w.hkv, w.d, slots,
+                stream.cuda_stream)
+            assert rc == 0, rc
+            meta = w.device_meta(dev)
+            outp = torch.empty_like(w.q)
+            n = lib.ccinfer_decode_workspace_size(w.batch, w.mbpr, w.hq, w.hkv, w.d, 16)
+            ws = torch.zeros(max(1, n), dtype=torch.uint8, device=dev)
+
+            def dec():
+                rc = lib.ccinfer_decode_attention_fp8(
+                    w.q.data_ptr(), kc.data_ptr(), vc.data_ptr(), ks.data_ptr(), vs.data_ptr(),
+                    meta["block_table"].data_ptr(), meta["context_lens"].data_ptr(),
+                    outp.data_ptr(), w.batch, w.mbpr, w.hq, w.hkv, w.d, 16, ws.data_ptr(), n,
+                    stream.cuda_stream)
+                assert rc == 0, rc
+            ms, host_ms = time_loop(dec, args.steps, args.warmup, stream)
+            sum_ctx = int(w.context_lens.astype(np.int64).sum())
+            nbytes = sum_ctx * w.hkv * (w.d + 4) * 2
+            r = {"ms_per_step": ms, "host_ms_per_step": host_ms, "bytes": nbytes,
+                 "GBps": nbytes / (ms * 1e-3) / 1e9,
+                 "bf16_equivalent_GBps": w.kv_bytes() / (ms * 1e-3) / 1e9}
+            r["hbm_frac"] = r["GBps"] * 1e9 / HBM_PEAK
+            out[key] = r
+            del w, kc, vc, ks, vs
+
     torch.cuda.synchronize()
     return head, out, nt
 
@@ -407,7 +450,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--configs", default="1,2,3,4,5,6,7")
+    ap.add_argument("--configs", default="1,2,3,4,5,6,7,8")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=5.0)
     ap.add_argument("--profile-op", choices=["decode", "write", "prefill", "mixed", "long",

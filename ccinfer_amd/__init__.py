@@ -10,11 +10,14 @@ from .ops import (  # noqa: F401
     CcinferError,
     build_batch_metadata,
     decode_attention,
+    decode_attention_fp8,
     decode_workspace_size,
     prefill_attention,
     prefill_workspace_size,
     qkv_prologue,
     write_kv_cache,
+    write_kv_cache_fp8,
+    fp8_scale_numel,
 )
 
 __all__ = [
@@ -23,9 +26,12 @@ __all__ = [
     "CcinferError",
     "build_batch_metadata",
     "decode_attention",
+    "decode_attention_fp8",
     "decode_workspace_size",
     "prefill_attention",
     "prefill_workspace_size",
     "qkv_prologue",
     "write_kv_cache",
+    "write_kv_cache_fp8",
+    "fp8_scale_numel",
 ]

@@ -45,6 +45,7 @@ SOURCES = [
     CSRC / "generic_attn.hip",
     CSRC / "qkv_prologue.hip",
     CSRC / "batch_meta.hip",
+    CSRC / "kv_fp8.hip",
     CSRC / "capi.cpp",
     CSRC / "dropin" / "launchers.cpp",
     CSRC / "dropin" / "hip_backend.cpp",

@@ -197,6 +197,49 @@ int ccinfer_decode_attention(const void* q, const void* k_cache, const void* v_c
                                           as_stream(stream)));
 }
 
+int ccinfer_write_kv_cache_fp8(const void* k_new, const void* v_new, void* k_cache,
+                               void* v_cache, float* k_scale, float* v_scale,
+                               const int32_t* slot_mapping, int total_tokens, int n_kv_heads,
+                               int head_dim, int max_slots, void* stream) {
+    if (!k_new || !v_new || !k_cache || !v_cache || !k_scale || !v_scale || !slot_mapping)
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    if (total_tokens <= 0 || n_kv_heads <= 0 || max_slots <= 0) return CCINFER_ERR_INVALID_ARGUMENT;
+    if (head_dim <= 0 || head_dim % 2 != 0 || head_dim > 512) return CCINFER_ERR_INVALID_ARGUMENT;
+    if (!fits_int(static_cast<int64_t>(total_tokens) * n_kv_heads * 2))
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    return map_hip_error(write_kv_cache_fp8(k_new, v_new, k_cache, v_cache, k_scale, v_scale,
+                                            slot_mapping, total_tokens, n_kv_heads, head_dim,
+                                            max_slots, as_stream(stream)));
+}
+
+int ccinfer_decode_attention_fp8(const void* q, const void* k_cache, const void* v_cache,
+                                 const float* k_scale, const float* v_scale,
+                                 const int32_t* block_table, const int32_t* context_lens,
+                                 void* output, int batch_size, int max_blocks_per_req,
+                                 int num_q_heads, int num_kv_heads, int head_dim,
+                                 int cache_block_size, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+    if (!q || !k_cache || !v_cache || !k_scale || !v_scale || !block_table || !context_lens ||
+        !output)
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    if (!decode_shape_ok(batch_size, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
+                         cache_block_size))
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    if (!decode_fast_supported(num_q_heads, num_kv_heads, head_dim, cache_block_size))
+        return CCINFER_ERR_UNSUPPORTED;  // fp8 has the MFMA path only
+    const DecodePlan plan =
+        plan_decode(batch_size, num_kv_heads, max_blocks_per_req * cache_block_size, true);
+    const size_t need = decode_workspace_bytes(batch_size, num_q_heads, head_dim, plan);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    DecodeItems items;
+    items.num_items = batch_size;
+    return map_hip_error(decode_attention_fp8(q, k_cache, v_cache, k_scale, v_scale, block_table,
+                                              context_lens, output, items, max_blocks_per_req,
+                                              num_q_heads, num_kv_heads, head_dim, plan,
+                                              workspace, as_stream(stream)));
+}
+
 size_t ccinfer_prefill_workspace_size(int batch_size, int total_query_tokens,
                                       int max_blocks_per_req, int num_q_heads,
                                       int num_kv_heads, int head_dim, int cache_block_size) {

@@ -43,6 +43,7 @@
 // the whole L2 and cost far more than the extra launch). A row whose context fits one split
 // is written directly by the first kernel and skipped by the merge.
 #include <algorithm>
+#include <type_traits>
 
 #include "attn_common.hpp"
 #include "kernels.hpp"
@@ -236,6 +237,69 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<D>& c, const __bf16* __rest
     }
 }
 
+// fp8 cache: the same lane layout with one byte per element (K: 8 bytes per k-step, V: NV
+// bytes per token piece) plus the row scales of the chunk's tokens T(g, e) =
+// 16 * (e / 4) + 4 * g + e % 4: tokens 4g..4g+3 of each block, 16 contiguous bytes of the
+// block's scale line.
+template <int D>
+struct ChunkRegsF8 {
+    u32x2 k[2][DecodeShape<D>::kSteps];
+    uint32_t v[8][(DecodeShape<D>::kNV + 3) / 4];
+    u32x4 ks[2];
+    u32x4 vs[2];
+};
+
+template <int D>
+__device__ __forceinline__ void load_chunk(ChunkRegsF8<D>& c, const uint8_t* __restrict__ k_cache,
+                                           const uint8_t* __restrict__ v_cache,
+                                           const float* __restrict__ k_scale,
+                                           const float* __restrict__ v_scale, int pb0, int pb1,
+                                           int kv_head, int hkv, int lane) {
+    constexpr int S = DecodeShape<D>::kSteps;
+    constexpr int NV = DecodeShape<D>::kNV;
+    const int i = lane & 15;
+    const int g = lane >> 4;
+    const int pbs[2] = {pb0 < 0 ? 0 : pb0, pb1 < 0 ? 0 : pb1};
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+        const uint8_t* row =
+            k_cache + ((static_cast<int64_t>(pbs[kb]) * kBlock + i) * hkv + kv_head) * D;
+#pragma unroll
+        for (int kk = 0; kk < S; ++kk)
+            c.k[kb][kk] = *reinterpret_cast<const u32x2*>(row + (kk * 4 + g) * 8);
+        const int64_t sl = (static_cast<int64_t>(pbs[kb]) * hkv + kv_head) * kBlock + 4 * g;
+        c.ks[kb] = *reinterpret_cast<const u32x4*>(k_scale + sl);
+        c.vs[kb] = *reinterpret_cast<const u32x4*>(v_scale + sl);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int kb = e >> 2;
+        const int off = g * 4 + (e & 3);
+        const uint8_t* row =
+            v_cache + ((static_cast<int64_t>(pbs[kb]) * kBlock + off) * hkv + kv_head) * D +
+            i * NV;
+        if constexpr (NV == 4) {
+            c.v[e][0] = *reinterpret_cast<const uint32_t*>(row);
+        } else if constexpr (NV == 8) {
+            const u32x2 w = *reinterpret_cast<const u32x2*>(row);
+            c.v[e][0] = w[0];
+            c.v[e][1] = w[1];
+        } else {
+            const u32x4 w = *reinterpret_cast<const u32x4*>(row);
+#pragma unroll
+            for (int x = 0; x < 4; ++x) c.v[e][x] = w[x];
+        }
+    }
+}
+
+// Two E4M3 bytes (the low or high half of `w`) -> a bf16 pair; exact (every E4M3 value is a
+// bf16 value).
+template <bool kHi>
+__device__ __forceinline__ uint32_t e4m3x2_to_bf16x2(uint32_t w) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(
+                                            static_cast<int>(w), 1.0f, kHi));
+}
+
 // Online-softmax state of one wavefront: lane (head j, grp g) holds O[j][NV*(4g+r)+n] in
 // acc[n][r], the running max m (base-2 domain, per head, replicated over the 4 grp lanes)
 // and a per-lane partial sum l.
@@ -246,11 +310,15 @@ struct SoftmaxState {
     float l;
 };
 
-template <int D>
+// kScaled: K/V came from the fp8 cache; ks[e] / vs[e] are the row scales of token T(g, e),
+// applied to its score (K) and to its probability in the PV product (V).
+template <int D, bool kScaled = false>
 __device__ __forceinline__ void consume_chunk(SoftmaxState<D>& st, ChunkRegs<D>& c,
                                               const bf16x8 (&qop)[DecodeShape<D>::kSteps],
                                               int cb, int end, int pb0, int pb1,
-                                              float scale_log2, int g) {
+                                              float scale_log2, int g,
+                                              const float* ks = nullptr,
+                                              const float* vs = nullptr) {
     constexpr int S = DecodeShape<D>::kSteps;
     constexpr int NV = DecodeShape<D>::kNV;
     float sc[8];
@@ -261,7 +329,12 @@ __device__ __forceinline__ void consume_chunk(SoftmaxState<D>& st, ChunkRegs<D>&
         for (int kk = 0; kk < S; ++kk)
             s4 = mfma16x16x32(__builtin_bit_cast(bf16x8, c.k[kb][kk]), qop[kk], s4);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sc[kb * 4 + r] = s4[r] * scale_log2;
+        for (int r = 0; r < 4; ++r) {
+            if constexpr (kScaled)
+                sc[kb * 4 + r] = s4[r] * (scale_log2 * ks[kb * 4 + r]);
+            else
+                sc[kb * 4 + r] = s4[r] * scale_log2;
+        }
     }
     // Masking (context end, negative block ids) is branch-free: the selects are cheap in
     // this memory-bound loop, and a wave-uniform branch around them would merge every V
@@ -294,7 +367,12 @@ __device__ __forceinline__ void consume_chunk(SoftmaxState<D>& st, ChunkRegs<D>&
     st.m = m_new;
     u32x4 pw;
 #pragma unroll
-    for (int x = 0; x < 4; ++x) pw[x] = pack_bf16x2(p[2 * x], p[2 * x + 1]);
+    for (int x = 0; x < 4; ++x) {
+        if constexpr (kScaled)
+            pw[x] = pack_bf16x2(p[2 * x] * vs[2 * x], p[2 * x + 1] * vs[2 * x + 1]);
+        else
+            pw[x] = pack_bf16x2(p[2 * x], p[2 * x + 1]);
+    }
     const bf16x8 pop = __builtin_bit_cast(bf16x8, pw);
 #pragma unroll
     for (int n = 0; n < NV; ++n) {
@@ -305,6 +383,38 @@ __device__ __forceinline__ void consume_chunk(SoftmaxState<D>& st, ChunkRegs<D>&
         st.acc[n] = st.acc[n] * alpha;
         st.acc[n] = mfma16x16x32(__builtin_bit_cast(bf16x8, vw), pop, st.acc[n]);
     }
+}
+
+template <int D>
+__device__ __forceinline__ void consume_chunk(SoftmaxState<D>& st, ChunkRegsF8<D>& r,
+                                              const bf16x8 (&qop)[DecodeShape<D>::kSteps],
+                                              int cb, int end, int pb0, int pb1,
+                                              float scale_log2, int g) {
+    constexpr int S = DecodeShape<D>::kSteps;
+    ChunkRegs<D> c;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int kk = 0; kk < S; ++kk)
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {
+                c.k[kb][kk][2 * w] = e4m3x2_to_bf16x2<false>(r.k[kb][kk][w]);
+                c.k[kb][kk][2 * w + 1] = e4m3x2_to_bf16x2<true>(r.k[kb][kk][w]);
+            }
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int x = 0; x < DecodeShape<D>::kVWords; x += 2) {
+            c.v[e][x] = e4m3x2_to_bf16x2<false>(r.v[e][x >> 1]);
+            c.v[e][x + 1] = e4m3x2_to_bf16x2<true>(r.v[e][x >> 1]);
+        }
+    float ks[8], vs[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        ks[e] = __uint_as_float(r.ks[e >> 2][e & 3]);
+        vs[e] = __uint_as_float(r.vs[e >> 2][e & 3]);
+    }
+    consume_chunk<D, true>(st, c, qop, cb, end, pb0, pb1, scale_log2, g, ks, vs);
 }
 
 // Log-sum-exp merge of the ns splits of one (item, head) row by one wavefront; writes bf16.
@@ -361,15 +471,21 @@ __device__ void merge_row(const float* __restrict__ ws_o, const float* __restric
     for (int x = 0; x < kPer; ++x) o[lane * kPer + x] = static_cast<__bf16>(acc[x] * inv);
 }
 
-template <int D>
+// F8: the cache holds E4M3 bytes with row scales (k_scale / v_scale); else bf16.
+template <int D, bool F8>
 __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
-    const __bf16* __restrict__ q, const __bf16* __restrict__ k_cache,
-    const __bf16* __restrict__ v_cache, const int32_t* __restrict__ block_table,
+    const __bf16* __restrict__ q, const void* __restrict__ k_cache_v,
+    const void* __restrict__ v_cache_v, const float* __restrict__ k_scale,
+    const float* __restrict__ v_scale, const int32_t* __restrict__ block_table,
     const int32_t* __restrict__ context_lens, __bf16* __restrict__ out, float* __restrict__ ws_o,
     float* __restrict__ ws_ml, ItemArgs items, int mbpr, int hq, int hkv, int splits,
     int split_tokens, int balanced_w, int slots, float scale_log2) {
     constexpr int S = DecodeShape<D>::kSteps;
     constexpr int NV = DecodeShape<D>::kNV;
+    using Cache = std::conditional_t<F8, uint8_t, __bf16>;
+    using Regs = std::conditional_t<F8, ChunkRegsF8<D>, ChunkRegs<D>>;
+    const Cache* __restrict__ k_cache = static_cast<const Cache*>(k_cache_v);
+    const Cache* __restrict__ v_cache = static_cast<const Cache*>(v_cache_v);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wi = blockIdx.x * kWavesPerGroup + wave;
@@ -453,17 +569,23 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
         *p0 = block_id(2 * c);
         *p1 = (2 * c + 1 < nblk) ? block_id(2 * c + 1) : -1;
     };
-    ChunkRegs<D> ra, rb;
+    Regs ra, rb;
+    auto load = [&](Regs& r, int p0, int p1) {
+        if constexpr (F8)
+            load_chunk<D>(r, k_cache, v_cache, k_scale, v_scale, p0, p1, h, hkv, lane);
+        else
+            load_chunk<D>(r, k_cache, v_cache, p0, p1, h, hkv, lane);
+    };
     int a0, a1, b0, b1;
     chunk_blocks(0, &a0, &a1);
-    load_chunk<D>(ra, k_cache, v_cache, a0, a1, h, hkv, lane);
+    load(ra, a0, a1);
     for (int c = 0; c < nchunks; c += 2) {
         chunk_blocks(c + 1, &b0, &b1);
-        load_chunk<D>(rb, k_cache, v_cache, b0, b1, h, hkv, lane);
+        load(rb, b0, b1);
         consume_chunk<D>(st, ra, qop, begin + c * kChunk, end, a0, a1, scale_log2, g);
         if (c + 1 >= nchunks) break;
         chunk_blocks(c + 2, &a0, &a1);
-        load_chunk<D>(ra, k_cache, v_cache, a0, a1, h, hkv, lane);
+        load(ra, a0, a1);
         consume_chunk<D>(st, rb, qop, begin + (c + 1) * kChunk, end, b0, b1, scale_log2, g);
     }
 
@@ -566,8 +688,9 @@ DecodeWs carve(void* workspace, size_t rows, int d) {
     return w;
 }
 
-template <int D>
+template <int D, bool F8>
 hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache,
+                         const float* k_scale, const float* v_scale,
                          const int32_t* block_table, const int32_t* context_lens, void* output,
                          const ItemArgs& it, int mbpr, int hq, int hkv, const DecodePlan& plan,
                          void* workspace, hipStream_t stream) {
@@ -580,9 +703,9 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
     DecodeWs w{};
     if (merge) w = carve(workspace, partial_rows(it.num_items, hq, plan), D);
     const int bw = plan.balanced ? plan.wave_target : 0;
-    decode_split_kernel<D><<<grid, 256, 0, stream>>>(
-        static_cast<const __bf16*>(q), static_cast<const __bf16*>(k_cache),
-        static_cast<const __bf16*>(v_cache), block_table, context_lens,
+    decode_split_kernel<D, F8><<<grid, 256, 0, stream>>>(
+        static_cast<const __bf16*>(q), k_cache, v_cache, k_scale, v_scale, block_table,
+        context_lens,
         static_cast<__bf16*>(output), w.o, w.ml, it, mbpr, hq, hkv, plan.splits,
         plan.split_tokens, bw, plan.slots, scale_log2);
     hipError_t err = hipGetLastError();
@@ -652,17 +775,46 @@ hipError_t decode_attention(const void* q, const void* k_cache, const void* v_ca
                 items.denom_eps, items.zero_invalid ? 1 : 0};
     switch (head_dim) {
         case 64:
-            return launch_decode<64>(q, k_cache, v_cache, block_table, context_lens, output, it,
+            return launch_decode<64, false>(q, k_cache, v_cache, nullptr, nullptr, block_table,
+                                             context_lens, output, it,
                                      max_blocks_per_req, num_q_heads, num_kv_heads, plan,
                                      workspace, stream);
         case 128:
-            return launch_decode<128>(q, k_cache, v_cache, block_table, context_lens, output, it,
+            return launch_decode<128, false>(q, k_cache, v_cache, nullptr, nullptr, block_table,
+                                             context_lens, output, it,
                                       max_blocks_per_req, num_q_heads, num_kv_heads, plan,
                                       workspace, stream);
         case 256:
-            return launch_decode<256>(q, k_cache, v_cache, block_table, context_lens, output, it,
+            return launch_decode<256, false>(q, k_cache, v_cache, nullptr, nullptr, block_table,
+                                             context_lens, output, it,
                                       max_blocks_per_req, num_q_heads, num_kv_heads, plan,
                                       workspace, stream);
+        default:
+            return hipErrorInvalidValue;
+    }
+}
+
+hipError_t decode_attention_fp8(const void* q, const void* k_cache, const void* v_cache,
+                                const float* k_scale, const float* v_scale,
+                                const int32_t* block_table, const int32_t* context_lens,
+                                void* output, const DecodeItems& items, int max_blocks_per_req,
+                                int num_q_heads, int num_kv_heads, int head_dim,
+                                const DecodePlan& plan, void* workspace, hipStream_t stream) {
+    ItemArgs it{items.num_items, items.item_count, items.item_req, items.query_start_loc,
+                items.denom_eps, items.zero_invalid ? 1 : 0};
+    switch (head_dim) {
+        case 64:
+            return launch_decode<64, true>(q, k_cache, v_cache, k_scale, v_scale, block_table,
+                                           context_lens, output, it, max_blocks_per_req,
+                                           num_q_heads, num_kv_heads, plan, workspace, stream);
+        case 128:
+            return launch_decode<128, true>(q, k_cache, v_cache, k_scale, v_scale, block_table,
+                                            context_lens, output, it, max_blocks_per_req,
+                                            num_q_heads, num_kv_heads, plan, workspace, stream);
+        case 256:
+            return launch_decode<256, true>(q, k_cache, v_cache, k_scale, v_scale, block_table,
+                                            context_lens, output, it, max_blocks_per_req,
+                                            num_q_heads, num_kv_heads, plan, workspace, stream);
         default:
             return hipErrorInvalidValue;
     }

@@ -75,6 +75,24 @@ hipError_t prefill_attention(const void* q, const void* k_cache, const void* v_c
                              int num_kv_heads, int head_dim, int block_size, void* workspace,
                              hipStream_t stream);
 
+// ---- fp8 (OCP E4M3) KV cache, one fp32 scale per cache row -------------------------
+// Scale of (slot, kv_head) at ((slot / kFp8Block) * Hkv + kv_head) * kFp8Block + slot % 16.
+constexpr int kFp8Block = 16;
+
+hipError_t write_kv_cache_fp8(const void* k_new, const void* v_new, void* k_cache,
+                              void* v_cache, float* k_scale, float* v_scale,
+                              const int32_t* slot_mapping, int total_tokens, int n_kv_heads,
+                              int head_dim, int max_slots, hipStream_t stream);
+
+// Decode over the fp8 cache: the bf16 decode's plan, workspace and items, with K/V bytes
+// dequantised in registers and the row scales applied to scores (K) and probabilities (V).
+hipError_t decode_attention_fp8(const void* q, const void* k_cache, const void* v_cache,
+                                const float* k_scale, const float* v_scale,
+                                const int32_t* block_table, const int32_t* context_lens,
+                                void* output, const DecodeItems& items, int max_blocks_per_req,
+                                int num_q_heads, int num_kv_heads, int head_dim,
+                                const DecodePlan& plan, void* workspace, hipStream_t stream);
+
 // ---- per-step batch metadata built on the device ------------------------------
 constexpr int kItemDecode = 1;  // item flag: decode item (exactly one new token)
 constexpr int kItemSample = 2;  // item flag: sample the item's last token

@@ -1,0 +1,108 @@
+// KV-cache write into an fp8 (OCP E4M3) cache with one fp32 scale per cache row.
+//
+// There is no counterpart in the reference, whose cache is bf16 only (its KV profile list,
+// src/base/traits.h:117-124, anticipates other element types). The layout keeps the
+// reference's contract -- [slot][kv_head][head_dim], slot = block * 16 + offset -- with one
+// byte per element, plus two fp32 scale arrays (K and V) indexed
+//   ((slot / 16) * Hkv + kv_head) * 16 + slot % 16,
+// so the 16 scales of one block's rows for one head are contiguous (a 64-byte line the
+// decode kernel reads with two 16-byte loads per chunk).
+//
+// Quantisation of one row x[0..D): amax = max |x|; inv = 448 / amax; q = e4m3(clamp(x *
+// inv, +-448)) rounded to nearest even; scale = amax / 448 (an all-zero row stores zeros
+// and scale 0). Dequantised value = q * scale. Per-row scales make appends exact: a decode
+// step writes one new row and never has to requantise earlier rows of the block.
+//
+// One wavefront per (token, kv_head, K or V) row; lane l holds elements 2l, 2l+1 (+128 per
+// step for rows longer than 128).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "attn_common.hpp"
+#include "kernels.hpp"
+
+namespace ccinfer::hipk {
+namespace {
+
+constexpr int kWaves = 4;
+
+__device__ __forceinline__ float wave_max_all(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+template <int kSteps>  // kSteps * 128 elements per row at most
+__global__ __launch_bounds__(256) void write_kv_fp8_kernel(
+    const __bf16* __restrict__ k_new, const __bf16* __restrict__ v_new, uint8_t* __restrict__ k_cache,
+    uint8_t* __restrict__ v_cache, float* __restrict__ k_scale, float* __restrict__ v_scale,
+    const int32_t* __restrict__ slot_mapping, int total_tokens, int hkv, int d, int max_slots) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + wave;  // (t, h, kv)
+    if (row >= static_cast<int64_t>(total_tokens) * hkv * 2) return;
+    const bool is_v = row & 1;
+    const int64_t th = row >> 1;
+    const int t = static_cast<int>(th / hkv);
+    const int h = static_cast<int>(th - static_cast<int64_t>(t) * hkv);
+    const int slot = slot_mapping[t];
+    if (slot < 0 || slot >= max_slots) return;
+    const __bf16* src = (is_v ? v_new : k_new) + th * d;
+    uint8_t* dst = (is_v ? v_cache : k_cache) + (static_cast<int64_t>(slot) * hkv + h) * d;
+
+    float x[kSteps][2];
+    float amax = 0.f;
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+        const int e = s * 128 + 2 * lane;
+        x[s][0] = e < d ? static_cast<float>(src[e]) : 0.f;
+        x[s][1] = e + 1 < d ? static_cast<float>(src[e + 1]) : 0.f;
+        amax = fmaxf(amax, fmaxf(fabsf(x[s][0]), fabsf(x[s][1])));
+    }
+    amax = wave_max_all(amax);
+    const float inv = amax > 0.f ? 448.0f / amax : 0.f;
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+        const int e = s * 128 + 2 * lane;
+        if (e >= d) break;
+        const float a = fminf(fmaxf(x[s][0] * inv, -448.0f), 448.0f);
+        const float b = fminf(fmaxf(x[s][1] * inv, -448.0f), 448.0f);
+        const uint32_t pk = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false));
+        *reinterpret_cast<uint16_t*>(dst + e) = static_cast<uint16_t>(pk & 0xffffu);
+    }
+    if (lane == 0) {
+        const int64_t si = (static_cast<int64_t>(slot / kFp8Block) * hkv + h) * kFp8Block +
+                           slot % kFp8Block;
+        (is_v ? v_scale : k_scale)[si] = amax > 0.f ? amax / 448.0f : 0.f;
+    }
+}
+
+}  // namespace
+
+hipError_t write_kv_cache_fp8(const void* k_new, const void* v_new, void* k_cache,
+                              void* v_cache, float* k_scale, float* v_scale,
+                              const int32_t* slot_mapping, int total_tokens, int n_kv_heads,
+                              int head_dim, int max_slots, hipStream_t stream) {
+    const int64_t rows = static_cast<int64_t>(total_tokens) * n_kv_heads * 2;
+    const unsigned grid = static_cast<unsigned>((rows + kWaves - 1) / kWaves);
+    auto* kn = static_cast<const __bf16*>(k_new);
+    auto* vn = static_cast<const __bf16*>(v_new);
+    auto* kc = static_cast<uint8_t*>(k_cache);
+    auto* vc = static_cast<uint8_t*>(v_cache);
+    if (head_dim <= 128)
+        write_kv_fp8_kernel<1><<<grid, 256, 0, stream>>>(kn, vn, kc, vc, k_scale, v_scale,
+                                                         slot_mapping, total_tokens, n_kv_heads,
+                                                         head_dim, max_slots);
+    else if (head_dim <= 256)
+        write_kv_fp8_kernel<2><<<grid, 256, 0, stream>>>(kn, vn, kc, vc, k_scale, v_scale,
+                                                         slot_mapping, total_tokens, n_kv_heads,
+                                                         head_dim, max_slots);
+    else
+        write_kv_fp8_kernel<4><<<grid, 256, 0, stream>>>(kn, vn, kc, vc, k_scale, v_scale,
+                                                         slot_mapping, total_tokens, n_kv_heads,
+                                                         head_dim, max_slots);
+    return hipGetLastError();
+}
+
+}  // namespace ccinfer::hipk

@@ -2,7 +2,8 @@
 
 Reference interface: DeviceBackend::{write_kv_cache, decode_attention, prefill_attention}
 (plus qkv_prologue, one launch for split_qkv + rms_norm + rope + write_kv_cache, and
-build_batch_metadata, BatchTranslator's per-step arrays built on the device)
+build_batch_metadata, BatchTranslator's per-step arrays built on the device, and an fp8
+KV cache: write_kv_cache_fp8 / decode_attention_fp8)
 (src/backend/backend.h:172-223) with the parameter structs of src/backend/params.h:148-211.
 Argument names, meaning and error behaviour follow it: invalid arguments raise
 CcinferError with code ErrorCode::InvalidArgument (6), the same value the reference returns.
@@ -224,6 +225,70 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     _check(_lib.load().ccinfer_decode_attention(
         _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(block_table), _ptr(context_lens),
         _ptr(output), b, mbpr, hq, hkv, d, cache_block_size, _ptr(ws), ws_bytes, _stream()), op)
+    return output
+
+
+def fp8_scale_numel(max_slots: int, num_kv_heads: int, block_size: int = 16) -> int:
+    """Floats in each scale array of an fp8 cache of `max_slots` slots."""
+    return -(-max_slots // block_size) * block_size * num_kv_heads
+
+
+def write_kv_cache_fp8(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor,
+                       v_cache: torch.Tensor, k_scale: torch.Tensor, v_scale: torch.Tensor,
+                       slot_mapping: torch.Tensor, max_slots: Optional[int] = None) -> None:
+    """write_kv_cache into an fp8 (OCP E4M3) cache with one fp32 scale per cache row.
+    k_cache / v_cache: uint8 [slots, Hkv, D] (or [blocks, 16, Hkv, D]); scales: float32 of
+    fp8_scale_numel(slots, Hkv) elements."""
+    op = "write_kv_cache_fp8"
+    for t in (k_new, v_new):
+        _dev_tensor(t, torch.bfloat16, op)
+    for t in (k_cache, v_cache):
+        _dev_tensor(t, torch.uint8, op)
+    for t in (k_scale, v_scale):
+        _dev_tensor(t, torch.float32, op)
+    _dev_tensor(slot_mapping, torch.int32, op)
+    slots, hkv, d = _kv_shape(k_cache)
+    _require(k_new.shape[-2:] == (hkv, d) and v_new.shape == k_new.shape, op)
+    _require(v_cache.numel() == k_cache.numel(), op)
+    _require(min(k_scale.numel(), v_scale.numel()) >= fp8_scale_numel(slots, hkv), op)
+    total = k_new.numel() // (hkv * d)
+    _require(slot_mapping.numel() == total, op)
+    _check(_lib.load().ccinfer_write_kv_cache_fp8(
+        _ptr(k_new), _ptr(v_new), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale),
+        _ptr(slot_mapping), total, hkv, d, slots if max_slots is None else max_slots,
+        _stream()), op)
+
+
+def decode_attention_fp8(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                         k_scale: torch.Tensor, v_scale: torch.Tensor,
+                         block_table: torch.Tensor, context_lens: torch.Tensor,
+                         output: Optional[torch.Tensor] = None, cache_block_size: int = 16,
+                         workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """decode_attention over an fp8 cache written by write_kv_cache_fp8."""
+    op = "decode_attention_fp8"
+    _dev_tensor(q, torch.bfloat16, op)
+    for t in (k_cache, v_cache):
+        _dev_tensor(t, torch.uint8, op)
+    for t in (k_scale, v_scale):
+        _dev_tensor(t, torch.float32, op)
+    _dev_tensor(block_table, torch.int32, op)
+    _dev_tensor(context_lens, torch.int32, op)
+    _require(q.dim() == 3 and block_table.dim() == 2, op)
+    b, hq, d = q.shape
+    slots, hkv, dk = _kv_shape(k_cache)
+    _require(dk == d and block_table.shape[0] == b and context_lens.numel() == b, op)
+    _require(min(k_scale.numel(), v_scale.numel()) >= fp8_scale_numel(slots, hkv), op)
+    if output is None:
+        output = torch.empty_like(q)
+    _dev_tensor(output, torch.bfloat16, op)
+    _require(output.shape == q.shape, op)
+    mbpr = block_table.shape[1]
+    need = decode_workspace_size(b, mbpr, hq, hkv, d, cache_block_size)
+    ws, ws_bytes = _workspace(need, q.device, workspace)
+    _check(_lib.load().ccinfer_decode_attention_fp8(
+        _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale), _ptr(block_table),
+        _ptr(context_lens), _ptr(output), b, mbpr, hq, hkv, d, cache_block_size, _ptr(ws),
+        ws_bytes, _stream()), op)
     return output
 
 

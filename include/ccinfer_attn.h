@@ -116,6 +116,34 @@ int ccinfer_decode_attention(const void* q, const void* k_cache, const void* v_c
                              int cache_block_size, void* workspace, size_t workspace_bytes,
                              void* stream);
 
+/* fp8 KV cache (no counterpart in the reference, whose cache is bf16 only; its KV profile
+ * list, src/base/traits.h:117-124, anticipates other element types). Same [slot][n_kv_heads]
+ * [head_dim] layout and block-table contract, one OCP E4M3 byte per element, plus one fp32
+ * scale per cache row in k_scale / v_scale, indexed ((slot / 16) * n_kv_heads + kv_head) * 16
+ * + slot % 16 (arrays of ceil(max_slots / 16) * 16 * n_kv_heads floats). A row x is stored
+ * as e4m3(clamp(x * (448 / amax), +-448)) with scale amax / 448 (round to nearest even;
+ * an all-zero row stores zeros and scale 0); its value is byte * scale. Halves decode bytes.
+ *
+ * Replaces launch_write_kv_cache (src/kernel/cuda_kernels.h:80-83) for an fp8 cache:
+ * quantises each new token's K and V rows into its slot; tokens whose slot is outside
+ * [0, max_slots) are skipped. head_dim even, <= 512. */
+int ccinfer_write_kv_cache_fp8(const void* k_new, const void* v_new, void* k_cache,
+                               void* v_cache, float* k_scale, float* v_scale,
+                               const int32_t* slot_mapping, int total_tokens, int n_kv_heads,
+                               int head_dim, int max_slots, void* stream);
+
+/* Replaces launch_decode_attention (src/kernel/cuda_kernels.h:72-77) for an fp8 cache: the
+ * same semantics, plan and workspace (ccinfer_decode_workspace_size) as
+ * ccinfer_decode_attention, with K/V read as byte * row scale. head_dim 64, 128 or 256 and
+ * at most 16 query heads per KV head (CCINFER_ERR_UNSUPPORTED otherwise). */
+int ccinfer_decode_attention_fp8(const void* q, const void* k_cache, const void* v_cache,
+                                 const float* k_scale, const float* v_scale,
+                                 const int32_t* block_table, const int32_t* context_lens,
+                                 void* output, int batch_size, int max_blocks_per_req,
+                                 int num_q_heads, int num_kv_heads, int head_dim,
+                                 int cache_block_size, void* workspace, size_t workspace_bytes,
+                                 void* stream);
+
 /* Workspace bytes ccinfer_prefill_attention needs for this batch shape. */
 size_t ccinfer_prefill_workspace_size(int batch_size, int total_query_tokens,
                                       int max_blocks_per_req, int num_q_heads,

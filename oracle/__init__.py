@@ -50,6 +50,12 @@ def load() -> ctypes.CDLL:
         lib.orc_qkv_prologue.argtypes = [_P] * 11 + [_I] * 6 + [ctypes.c_float]
         lib.orc_build_batch_metadata.argtypes = [_P] * 5 + [_I] * 6 + [_P] * 6
         lib.orc_build_batch_metadata.restype = _I
+        lib.orc_f32_to_e4m3.argtypes = [ctypes.c_float]
+        lib.orc_f32_to_e4m3.restype = ctypes.c_uint8
+        lib.orc_e4m3_to_f32.argtypes = [ctypes.c_uint8]
+        lib.orc_e4m3_to_f32.restype = ctypes.c_float
+        lib.orc_write_kv_cache_fp8.argtypes = [_P] * 7 + [_I] * 5
+        lib.orc_decode_attention_fp8.argtypes = [_P] * 8 + [_I] * 7
         _lib = lib
     return _lib
 
@@ -252,3 +258,50 @@ def build_batch_metadata(kv_written, new_tokens, flags, block_start, blocks, num
     out["positions"] = out["positions"][:num_tokens]
     out["slot_mapping"] = out["slot_mapping"][:num_tokens]
     return int(st), out
+
+
+# ---- fp8 (OCP E4M3) KV cache with one fp32 scale per cache row ----
+
+def fp8_scale_index(slot, kv_head, num_kv_heads: int, block_size: int = 16):
+    slot = np.asarray(slot, np.int64)
+    return ((slot // block_size) * num_kv_heads + kv_head) * block_size + slot % block_size
+
+
+def f32_to_e4m3(x) -> np.ndarray:
+    lib = load()
+    x = np.asarray(x, np.float32)
+    return np.array([lib.orc_f32_to_e4m3(float(v)) for v in x.ravel()], np.uint8).reshape(x.shape)
+
+
+def e4m3_to_f32(b) -> np.ndarray:
+    lib = load()
+    b = np.asarray(b, np.uint8)
+    return np.array([lib.orc_e4m3_to_f32(int(v)) for v in b.ravel()], np.float32).reshape(b.shape)
+
+
+def write_kv_cache_fp8(k_new, v_new, k_cache, v_cache, k_scale, v_scale, slot_mapping,
+                       max_slots=None, block_size: int = 16) -> None:
+    """In place: k_cache/v_cache uint8 [slots, Hkv, D]; k_scale/v_scale float32 [slots*Hkv]."""
+    k, v = _c(k_new, np.uint16), _c(v_new, np.uint16)
+    sm = _c(slot_mapping, np.int32)
+    for a in (k_cache, v_cache, k_scale, v_scale):
+        assert a.flags.c_contiguous
+    t, hkv, d = k.shape
+    load().orc_write_kv_cache_fp8(_p(k), _p(v), _p(k_cache), _p(v_cache), _p(k_scale),
+                                  _p(v_scale), _p(sm), t, hkv, d,
+                                  k_cache.shape[0] if max_slots is None else max_slots,
+                                  block_size)
+
+
+def decode_fp8(q, k_cache, v_cache, k_scale, v_scale, block_table, context_lens,
+               block_size: int = 16, nthreads=None) -> np.ndarray:
+    """fp32 [B, Hq, D] over the fp8 cache."""
+    q = _c(q, np.uint16)
+    b, hq, d = q.shape
+    bt = _c(block_table, np.int32)
+    out = np.zeros((b, hq, d), np.float32)
+    load().orc_decode_attention_fp8(
+        _p(q), _p(_c(k_cache, np.uint8)), _p(_c(v_cache, np.uint8)), _p(_c(k_scale, np.float32)),
+        _p(_c(v_scale, np.float32)), _p(bt), _p(_c(context_lens, np.int32)), _p(out), b,
+        bt.shape[1], hq, k_cache.shape[1], d, block_size, nthreads or default_threads())
+    return out

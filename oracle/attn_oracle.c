@@ -542,3 +542,159 @@ int orc_build_batch_metadata(const int32_t* item_kv_written, const int32_t* item
     if (offset != T) status = 6;
     return status;
 }
+
+/* ------------------------------------------------------------------------- */
+/* fp8 KV cache (no counterpart in the reference, whose cache is bf16 only;    */
+/* src/base/traits.h:117-124 anticipates other KV profiles). OCP E4M3 ("fn": */
+/* no infinities, 0x7f/0xff NaN, largest finite 448), round to nearest even.  */
+/* Each cache row (slot, kv_head) is quantised with its own fp32 scale:        */
+/*   amax = max |x|; inv = 448 / amax; q = e4m3(clamp(x * inv, +-448));        */
+/*   scale = amax / 448 (0 and inv 0 for an all-zero row); value = q * scale.  */
+/* Scales live in [slot / bs][kv_head][slot % bs] order, so the 16 scales of a  */
+/* block's rows for one head are contiguous.                                   */
+/* ------------------------------------------------------------------------- */
+uint8_t orc_f32_to_e4m3(float x) {
+    const uint8_t sign = signbit(x) ? 0x80 : 0x00;
+    float a = fabsf(x);
+    if (!(a == a)) return 0x7f;              /* NaN */
+    if (a >= 448.0f) return sign | 0x7e;     /* saturate */
+    if (a < 0.015625f) {                     /* below 2^-6: subnormal grid m * 2^-9 */
+        const float m = nearbyintf(a * 512.0f);  /* exact scaling, RNE */
+        return sign | (uint8_t)m;                /* m == 8 is the smallest normal 0x08 */
+    }
+    int e;
+    const float f = frexpf(a, &e);           /* a = f * 2^e, f in [0.5, 1) */
+    e -= 1;                                  /* a = (2f) * 2^e, 2f in [1, 2) */
+    float m = nearbyintf((2.0f * f - 1.0f) * 8.0f);  /* exact: 2f has <= 24 bits */
+    if (m == 8.0f) {
+        m = 0.0f;
+        e += 1;
+    }
+    if (e > 8 || (e == 8 && m > 6.0f)) return sign | 0x7e;
+    return sign | (uint8_t)(((e + 7) << 3) | (int)m);
+}
+
+float orc_e4m3_to_f32(uint8_t b) {
+    const int e = (b >> 3) & 15, m = b & 7;
+    float v;
+    if ((b & 0x7f) == 0x7f) return NAN;
+    if (e == 0)
+        v = ldexpf((float)m, -9);
+    else
+        v = ldexpf(1.0f + m / 8.0f, e - 7);
+    return (b & 0x80) ? -v : v;
+}
+
+int64_t orc_fp8_scale_index(int slot, int kv_head, int num_kv_heads, int block_size) {
+    return ((int64_t)(slot / block_size) * num_kv_heads + kv_head) * block_size +
+           slot % block_size;
+}
+
+void orc_quantize_row_fp8(const uint16_t* x, int n, uint8_t* q, float* scale) {
+    float amax = 0.0f;
+    for (int d = 0; d < n; ++d) {
+        const float a = fabsf(orc_bf16_to_f32(x[d]));
+        if (a > amax) amax = a;
+    }
+    const float inv = amax > 0.0f ? 448.0f / amax : 0.0f;
+    *scale = amax > 0.0f ? amax / 448.0f : 0.0f;
+    for (int d = 0; d < n; ++d) {
+        float v = orc_bf16_to_f32(x[d]) * inv;
+        v = v > 448.0f ? 448.0f : (v < -448.0f ? -448.0f : v);
+        q[d] = orc_f32_to_e4m3(v);
+    }
+}
+
+void orc_write_kv_cache_fp8(const uint16_t* k_new, const uint16_t* v_new, uint8_t* k_cache,
+                            uint8_t* v_cache, float* k_scale, float* v_scale,
+                            const int32_t* slot_mapping, int total_tokens, int n_kv_heads,
+                            int head_dim, int max_slots, int block_size) {
+    for (int t = 0; t < total_tokens; ++t) {
+        const int slot = slot_mapping[t];
+        if (slot < 0 || slot >= max_slots) continue;
+        for (int h = 0; h < n_kv_heads; ++h) {
+            const int64_t src = ((int64_t)t * n_kv_heads + h) * head_dim;
+            const int64_t dst = ((int64_t)slot * n_kv_heads + h) * head_dim;
+            const int64_t si = orc_fp8_scale_index(slot, h, n_kv_heads, block_size);
+            orc_quantize_row_fp8(k_new + src, head_dim, k_cache + dst, k_scale + si);
+            orc_quantize_row_fp8(v_new + src, head_dim, v_cache + dst, v_scale + si);
+        }
+    }
+}
+
+/* Decode over the fp8 cache: the reference decode (attend_one) with each K/V element read
+ * as e4m3 value * row scale. */
+static float e4m3_lut[256];
+
+typedef struct {
+    const uint16_t* q;
+    const uint8_t *k, *v;
+    const float *ks, *vs;
+    const int32_t *bt, *ctx;
+    float* out;
+    int B, mbpr, hq, hkv, d, bs;
+} decode_fp8_ctx;
+
+static void decode_one_fp8(int64_t i, void* p, float* scores, int64_t* bases) {
+    const decode_fp8_ctx* c = (const decode_fp8_ctx*)p;
+    const int req = (int)(i / c->hq), qh = (int)(i % c->hq);
+    float* o = c->out + ((int64_t)req * c->hq + qh) * c->d;
+    const int ctx = c->ctx[req];
+    const int nb = ctx > 0 ? (ctx + c->bs - 1) / c->bs : 0;
+    for (int d = 0; d < c->d; ++d) o[d] = 0.0f;
+    if (ctx <= 0 || nb > c->mbpr) return;
+    const int kvh = qh / (c->hq / c->hkv);
+    const uint16_t* qv = c->q + ((int64_t)req * c->hq + qh) * c->d;
+    const int32_t* rb = c->bt + (int64_t)req * c->mbpr;
+    const float scale = 1.0f / sqrtf((float)c->d);
+    float mx = -INFINITY;
+    int any = 0;
+    for (int pos = 0; pos < ctx; ++pos) {
+        const int blk = rb[pos / c->bs];
+        if (blk < 0) {
+            bases[pos] = -1;
+            continue;
+        }
+        const int slot = blk * c->bs + pos % c->bs;
+        bases[pos] = slot;
+        const int64_t row = ((int64_t)slot * c->hkv + kvh) * c->d;
+        const float ks = c->ks[orc_fp8_scale_index(slot, kvh, c->hkv, c->bs)];
+        float s = 0.0f;
+        for (int d = 0; d < c->d; ++d)
+            s += orc_bf16_to_f32(qv[d]) * (e4m3_lut[c->k[row + d]] * ks);
+        s *= scale;
+        scores[pos] = s;
+        if (s > mx) mx = s;
+        any = 1;
+    }
+    if (!any) return;
+    float denom = 0.0f;
+    for (int pos = 0; pos < ctx; ++pos) {
+        if (bases[pos] < 0) continue;
+        scores[pos] = expf(scores[pos] - mx);
+        denom += scores[pos];
+    }
+    const float inv = 1.0f / (denom + 1e-6f);
+    for (int pos = 0; pos < ctx; ++pos) {
+        if (bases[pos] < 0) continue;
+        const int slot = (int)bases[pos];
+        const int64_t row = ((int64_t)slot * c->hkv + kvh) * c->d;
+        const float vs = c->vs[orc_fp8_scale_index(slot, kvh, c->hkv, c->bs)];
+        const float w = scores[pos] * inv;
+        for (int d = 0; d < c->d; ++d) o[d] += w * (e4m3_lut[c->v[row + d]] * vs);
+    }
+}
+
+void orc_decode_attention_fp8(const uint16_t* q, const uint8_t* k_cache, const uint8_t* v_cache,
+                              const float* k_scale, const float* v_scale,
+                              const int32_t* block_table, const int32_t* context_lens,
+                              float* out, int batch_size, int max_blocks_per_req,
+                              int num_q_heads, int num_kv_heads, int head_dim,
+                              int cache_block_size, int nthreads) {
+    for (int b = 0; b < 256; ++b) e4m3_lut[b] = orc_e4m3_to_f32((uint8_t)b);  /* before workers */
+    decode_fp8_ctx c = {q, k_cache, v_cache, k_scale, v_scale, block_table, context_lens, out,
+                        batch_size, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
+                        cache_block_size};
+    run_parallel(decode_one_fp8, &c, (int64_t)batch_size * num_q_heads, nthreads,
+                 max_ctx_of(context_lens, batch_size));
+}

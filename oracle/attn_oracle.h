@@ -24,6 +24,10 @@
  *   - orc_qkv_prologue        : the sequence of src/model/qwen3/qwen3_model.cpp:174-244
  *   - orc_build_batch_metadata: the arrays of src/worker/batch_translator.cpp:213-302 and
  *                               the checks of src/model/model_runner.h:102-171
+ *   - orc_*_fp8 / orc_*e4m3*  : an fp8 (OCP E4M3) KV cache with one fp32 scale per cache
+ *                               row. No counterpart in the reference (its cache is bf16;
+ *                               src/base/traits.h:117-124 anticipates other profiles):
+ *                               pinned by torch.float8_e4m3fn and closed forms instead.
  *
  * Every function is pinned by tests/test_oracle.py (known-answer vectors from the
  * reference tests, closed forms, torch's float64 scaled_dot_product_attention as an
@@ -124,6 +128,23 @@ int orc_build_batch_metadata(const int32_t* item_kv_written, const int32_t* item
                              int32_t* positions, int32_t* slot_mapping, int32_t* block_table,
                              int32_t* query_start_loc, int32_t* context_lens,
                              int32_t* logits_indices);
+
+/* fp8 KV cache: OCP E4M3 values, one fp32 scale per (slot, kv_head) row stored at
+ * orc_fp8_scale_index(slot, kv_head) = ((slot / bs) * Hkv + kv_head) * bs + slot % bs. */
+uint8_t orc_f32_to_e4m3(float x);
+float orc_e4m3_to_f32(uint8_t b);
+int64_t orc_fp8_scale_index(int slot, int kv_head, int num_kv_heads, int block_size);
+void orc_quantize_row_fp8(const uint16_t* x, int n, uint8_t* q, float* scale);
+void orc_write_kv_cache_fp8(const uint16_t* k_new, const uint16_t* v_new, uint8_t* k_cache,
+                            uint8_t* v_cache, float* k_scale, float* v_scale,
+                            const int32_t* slot_mapping, int total_tokens, int n_kv_heads,
+                            int head_dim, int max_slots, int block_size);
+void orc_decode_attention_fp8(const uint16_t* q, const uint8_t* k_cache, const uint8_t* v_cache,
+                              const float* k_scale, const float* v_scale,
+                              const int32_t* block_table, const int32_t* context_lens,
+                              float* out, int batch_size, int max_blocks_per_req,
+                              int num_q_heads, int num_kv_heads, int head_dim,
+                              int cache_block_size, int nthreads);
 
 #ifdef __cplusplus
 }

@@ -169,3 +169,28 @@ def test_build_batch_metadata_validation(lib):
     assert _meta(lib, nb=-1) == INVALID
     assert _meta(lib, b=1 << 16, mbpr=1 << 16) == INVALID      # table entries overflow int
     assert _meta(lib, ncb=1 << 28, bs=16) == INVALID           # cache slots overflow int
+
+
+def test_fp8_validation(lib):
+    w = lib.ccinfer_write_kv_cache_fp8
+    ok = [FAKE] * 7 + [4, 2, 128, 64, None]
+    for i in range(7):
+        a = list(ok)
+        a[i] = None
+        assert w(*a) == INVALID, i
+    for i, bad in ((7, 0), (8, 0), (9, 0), (9, 127), (9, 514), (10, 0)):
+        a = list(ok)
+        a[i] = bad
+        assert w(*a) == INVALID, (i, bad)
+    dec = lib.ccinfer_decode_attention_fp8
+    okd = [FAKE] * 8 + [2, 4, 8, 2, 128, 16, None, 0, None]
+    for i in range(8):
+        a = list(okd)
+        a[i] = None
+        assert dec(*a) == INVALID, i
+    a = list(okd)
+    a[12] = 96  # valid decode head dim, but fp8 has the MFMA path only
+    assert dec(*a) == 26  # CCINFER_ERR_UNSUPPORTED
+    a = list(okd)
+    a[13] = 32
+    assert dec(*a) == INVALID

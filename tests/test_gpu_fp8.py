@@ -1,0 +1,104 @@
+"""fp8 (OCP E4M3) KV cache on the GPU against the oracle: the write is bit-exact (bytes and
+scales); decode over the fp8 cache meets the attention bar (max-abs <= 2e-2, mean-abs <=
+2e-3) against the oracle's fp32 decode over the same fp8 cache."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from ccinfer_amd import (decode_attention, decode_attention_fp8, fp8_scale_numel,
+                         write_kv_cache_fp8)
+from ccinfer_amd import workloads as W
+from tests._util import assert_attn_close, f32, from_u16, say, u16
+
+pytestmark = pytest.mark.gpu
+BS = 16
+
+
+def rnd_bf16(rng, shape, scale=1.0):
+    return oracle.f32_to_bf16((rng.standard_normal(shape) * scale).astype(np.float32))
+
+
+@pytest.mark.parametrize("hkv,d", [(8, 128), (3, 64), (2, 256), (1, 130)])
+def test_write_bit_exact(gpu, hkv, d):
+    say(f"fp8 write hkv={hkv} d={d}")
+    rng = np.random.default_rng(d + hkv)
+    t, slots = 37, 96
+    k = rnd_bf16(rng, (t, hkv, d), 2.0)
+    v = rnd_bf16(rng, (t, hkv, d), 1e-3)
+    k[4] = 0                                       # all-zero rows: scale 0
+    v[6, 0, 1] = oracle.f32_to_bf16(np.float32(1e30))   # one huge element
+    sm = rng.permutation(slots)[:t].astype(np.int32)
+    sm[2], sm[9] = -1, slots + 4                   # skipped
+    nsc = fp8_scale_numel(slots, hkv)
+    kc0 = rng.integers(0, 256, (slots, hkv, d)).astype(np.uint8)
+    vc0 = rng.integers(0, 256, (slots, hkv, d)).astype(np.uint8)
+    ks0 = rng.standard_normal(nsc).astype(np.float32)
+    vs0 = rng.standard_normal(nsc).astype(np.float32)
+    want = [a.copy() for a in (kc0, vc0, ks0, vs0)]
+    oracle.write_kv_cache_fp8(k, v, *want, sm)
+    dev = [torch.from_numpy(a.copy()).to(gpu) for a in (kc0, vc0, ks0, vs0)]
+    write_kv_cache_fp8(from_u16(k, gpu), from_u16(v, gpu), *dev, torch.from_numpy(sm).to(gpu))
+    torch.cuda.synchronize()
+    for name, g, w in zip(("k_cache", "v_cache", "k_scale", "v_scale"), dev, want):
+        got = g.cpu().numpy()
+        if got.dtype == np.float32:
+            assert np.array_equal(got.view(np.uint32), w.view(np.uint32)), name
+        else:
+            assert np.array_equal(got, w), name
+
+
+def quantised_cache(gpu, w, hkv, d):
+    """The workload's bf16 cache quantised into an fp8 cache by the GPU write kernel."""
+    slots = w.k_cache.shape[0]
+    kc = torch.empty((slots, hkv, d), dtype=torch.uint8, device=gpu)
+    vc = torch.empty_like(kc)
+    ks = torch.empty(fp8_scale_numel(slots, hkv), dtype=torch.float32, device=gpu)
+    vs = torch.empty_like(ks)
+    write_kv_cache_fp8(w.k_cache, w.v_cache, kc, vc, ks, vs,
+                       torch.arange(slots, dtype=torch.int32, device=gpu))
+    return kc, vc, ks, vs
+
+
+@pytest.mark.parametrize("name,make", [
+    ("decode_b1_ctx512", lambda dev: W.decode_single(device=dev)),
+    ("decode_b64_ctx128-4096", lambda dev: W.decode_batched(device=dev)),
+    ("decode_b3_gqa4_long", lambda dev: W.decode_batched(device=dev, batch=3, ctx_lo=9000,
+                                                         ctx_hi=20000, hq=32, hkv=8)),
+])
+def test_decode_fp8_matches_oracle(gpu, name, make):
+    say(f"fp8 decode {name}")
+    w = make(gpu)
+    meta = w.device_meta(gpu)
+    kc, vc, ks, vs = quantised_cache(gpu, w, w.hkv, w.d)
+    out = decode_attention_fp8(w.q, kc, vc, ks, vs, meta["block_table"], meta["context_lens"])
+    ref_bf16 = decode_attention(w.q, w.k_cache, w.v_cache, meta["block_table"],
+                                meta["context_lens"])
+    torch.cuda.synchronize()
+    want = oracle.decode_fp8(u16(w.q), kc.cpu().numpy(), vc.cpu().numpy(), ks.cpu().numpy(),
+                             vs.cpu().numpy(), w.block_table, w.context_lens)
+    assert_attn_close(f32(out), want, f"fp8 {name}")
+    # quantisation error against the bf16 cache stays small (informative bound)
+    err = np.abs(f32(out) - f32(ref_bf16))
+    assert err.max() < 0.1 and err.mean() < 0.01, (err.max(), err.mean())
+
+
+def test_decode_fp8_masks_holes_and_bad_rows(gpu):
+    say("fp8 decode holes")
+    rng = np.random.default_rng(5)
+    b, hq, hkv, d, nblk = 4, 16, 8, 128, 64
+    slots = nblk * BS
+    w = W.decode_batched(device=gpu, batch=b, ctx_lo=100, ctx_hi=900)
+    kc, vc, ks, vs = quantised_cache(gpu, w, hkv, d)
+    bt = w.block_table.copy()
+    bt[1, 2] = -1                  # a hole
+    ctx = w.context_lens.copy()
+    ctx[3] = 0                     # invalid row -> zeros
+    out = decode_attention_fp8(w.q, kc, vc, ks, vs, torch.from_numpy(bt).to(gpu),
+                               torch.from_numpy(ctx).to(gpu))
+    torch.cuda.synchronize()
+    want = oracle.decode_fp8(u16(w.q), kc.cpu().numpy(), vc.cpu().numpy(), ks.cpu().numpy(),
+                             vs.cpu().numpy(), bt, ctx)
+    assert_attn_close(f32(out), want, "fp8 holes")
+    assert np.all(f32(out)[3] == 0)
+    assert rng is not None and slots > 0
