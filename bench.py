@@ -432,6 +432,12 @@ def profile(op: str, iters: int) -> None:
         fn = lambda: dst.copy_(src)  # noqa: E731
     elif op == "prologue":
         fn = prologue_call(W.prologue(device=dev, tokens=12288), stream)
+    elif op in ("shared_prefix", "private_prefix"):
+        # 16 sequences x (4096 cached + 256 new): one prefix shared by all, or 16 copies
+        share = tuple((i, 0) for i in range(1, 16)) if op == "shared_prefix" else ()
+        w = W.prefill_prefix(device=dev, seed=11, n_seqs=16, prefix=4096, new=256,
+                             share_pairs=share)
+        fn = Ops(w, dev, stream).prefill
     else:
         w = {"decode": W.decode_batched, "write": W.decode_batched, "prefill": W.prefill_prefix,
              "mixed": W.mixed_step, "long": W.decode_long}[op](device=dev)
@@ -454,7 +460,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=5.0)
     ap.add_argument("--profile-op", choices=["decode", "write", "prefill", "mixed", "long",
-                                             "prologue", "copy"], default=None)
+                                             "prologue", "shared_prefix", "private_prefix",
+                                             "copy"], default=None)
     ap.add_argument("--profile-iters", type=int, default=5)
     args = ap.parse_args()
     if args.gpus != 1:
