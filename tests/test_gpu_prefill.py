@@ -11,7 +11,8 @@ import pytest
 import torch
 
 import oracle
-from ccinfer_amd import decode_attention, prefill_attention, write_kv_cache
+from ccinfer_amd import (decode_attention, prefill_attention, prefill_workspace_size,
+                         write_kv_cache)
 from ccinfer_amd import workloads as W
 from tests._util import assert_attn_close, f32, from_u16, say, u16
 
@@ -201,3 +202,35 @@ def test_deterministic(gpu):
     w = W.prefill_prefix(device=gpu, seed=4, n_seqs=2, prefix=32, new=300, share_pairs=())
     write_new(w, gpu)
     assert np.array_equal(u16(run_prefill(w, gpu)), u16(run_prefill(w, gpu)))
+
+
+def test_mixed_batch_under_graph_capture(gpu):
+    """The decode items run on a side stream forked from the caller's stream and joined
+    back; that fork/join must capture into a graph and replay to the eager result."""
+    say("prefill mixed batch captured in a graph")
+    # 42 requests: at least 32, so the decode items take the side stream
+    w = W.mixed_step(device=gpu, n_chunks=2, chunk=128, n_decode=40, dec_hi=4096)
+    write_new(w, gpu)
+    meta = w.device_meta(gpu)
+    eager = run_prefill(w, gpu).clone()
+    out = torch.zeros_like(w.q)
+    n = prefill_workspace_size(w.batch, w.q.shape[0], w.mbpr, w.hq, w.hkv, w.d)
+    ws = torch.zeros(max(1, n), dtype=torch.uint8, device=gpu)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):  # warm-up outside capture: creates the side stream
+        prefill_attention(w.q, w.k_cache, w.v_cache, meta["block_table"],
+                          meta["query_start_loc"], meta["context_lens"], output=out,
+                          workspace=ws)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        prefill_attention(w.q, w.k_cache, w.v_cache, meta["block_table"],
+                          meta["query_start_loc"], meta["context_lens"], output=out,
+                          workspace=ws)
+    for _ in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
