@@ -13,7 +13,8 @@ The other configurations are reported under "configs"; "6" is the fused decode p
 "8" is decode over an fp8 (E4M3, per-row scale) cache, in bytes actually read and in the
 bf16 bytes the same attention covers. rank 0 prints ONE JSON line.
 
-Timing: W untimed warm-up steps, then exactly K steps bracketed by device synchronisation;
+Timing: about 0.2 s of untimed repetitions (clock settle) and W untimed warm-up steps, then
+exactly K steps bracketed by device synchronisation; CPU baselines run after all GPU timings;
 per-op kernel time is measured with HIP events recorded on the stream the kernels run on.
 cpu_baseline: the CPU oracle (a C restatement of the reference's CPU attention path) on the
 box's host cores, on the same workload. `--profile-op NAME` runs only that op in a loop (for
@@ -87,9 +88,18 @@ class Ops:
         assert rc == 0, rc
 
 
+SETTLE_S = 0.2  # untimed repetitions of the step before its warm-up, so clocks are ramped
+
+
 def time_loop(fn, steps: int, warmup: int, stream: torch.cuda.Stream):
-    """Returns (event ms per step, host-clock ms per step)."""
+    """Returns (event ms per step, host-clock ms per step): SETTLE_S seconds of untimed
+    repetitions, `warmup` untimed steps, then exactly `steps` timed steps."""
     with torch.cuda.stream(stream):
+        t_settle = time.perf_counter()
+        while time.perf_counter() - t_settle < SETTLE_S:
+            for _ in range(4):
+                fn()
+            torch.cuda.synchronize()
         for _ in range(warmup):
             fn()
         torch.cuda.synchronize()
@@ -264,23 +274,29 @@ def run(args):
     out = {}
     head = None
     nt = cpu_threads()
+    # CPU baselines run after every GPU measurement, so no GPU timing follows an idle GPU
+    deferred = []
 
     if 1 in configs:
         w = W.decode_single(device=dev)
         r = bench_decode(w, dev, max(args.steps, 50), args.warmup, False, stream)
-        if not args.no_cpu:
+
+        def cpu1(w=w, r=r):
             s, reps = cpu_decode_baseline(w, 1.0)
             r["cpu_GBps"] = w.kv_bytes() / s / 1e9
+        deferred.append(cpu1)
         out["1_decode_b1_ctx512"] = r
         del w
 
     if 2 in configs:
         w = W.decode_batched(device=dev)
         r = bench_decode(w, dev, args.steps, args.warmup, True, stream)
-        if not args.no_cpu:
+
+        def cpu2(w=w, r=r):
             s, reps = cpu_decode_baseline(w, args.cpu_budget)
             r["cpu_GBps"] = w.kv_bytes() / s / 1e9
             r["cpu_reps"] = reps
+        deferred.append(cpu2)
         head = (w, r)
         out["2_decode_b64_ctx128-4096"] = r
 
@@ -293,13 +309,15 @@ def run(args):
         r = {"ms_per_step": ms, "host_ms_per_step": host_ms, "write_ms": wr_ms, "flops": flops,
              "TFLOPs": flops / (ms * 1e-3) / 1e12}
         r["mfma_frac"] = r["TFLOPs"] * 1e12 / BF16_PEAK
-        if not args.no_cpu:
+
+        def cpu3(w=w, r=r):
             rng = np.random.default_rng(0)
             pairs = np.stack([rng.integers(0, w.q.shape[0], 256), rng.integers(0, w.hq, 256)],
                              1).astype(np.int32)
             s, reps = cpu_prefill_baseline(w, pairs, 1.0)
             r["cpu_TFLOPs"] = prefill_pair_flops(w, pairs) / s / 1e12
             r["cpu_sample"] = "256 random (query row, q_head) pairs"
+        deferred.append(cpu3)
         out["3_prefill_8x(512+1536)"] = r
         del w, ops
 
@@ -319,11 +337,13 @@ def run(args):
     if 5 in configs:
         w = W.decode_long(device=dev)
         r = bench_decode(w, dev, max(5, args.steps // 2), args.warmup, False, stream)
-        if not args.no_cpu:
+
+        def cpu5(w=w, r=r):
             pairs = np.array([[0, h] for h in range(w.hq)], np.int32)
             s, reps = cpu_decode_baseline(w, 1.0, pairs=pairs)
             r["cpu_GBps"] = int(w.context_lens[0]) * w.hkv * w.d * 4 / s / 1e9
             r["cpu_sample"] = "sequence 0, all 32 q-heads"
+        deferred.append(cpu5)
         out["5_decode_b32_ctx32768_gqa4"] = r
         del w
 
@@ -337,10 +357,12 @@ def run(args):
             r = {"ms_per_step": ms, "host_ms_per_step": host_ms, "bytes": w.bytes(),
                  "GBps": w.bytes() / (ms * 1e-3) / 1e9}
             r["hbm_frac"] = r["GBps"] * 1e9 / HBM_PEAK
-            if not args.no_cpu and tokens == 64:
-                s, reps = cpu_prologue_baseline(w, 1.0)
-                r["cpu_GBps"] = w.bytes() / s / 1e9
-                r["cpu_sample"] = "the same 64 tokens, 1 thread"
+            if tokens == 64:
+                def cpu6(w=w, r=r):
+                    s, reps = cpu_prologue_baseline(w, 1.0)
+                    r["cpu_GBps"] = w.bytes() / s / 1e9
+                    r["cpu_sample"] = "the same 64 tokens, 1 thread"
+                deferred.append(cpu6)
             out[key] = r
             del w
 
@@ -416,6 +438,9 @@ def run(args):
             del w, kc, vc, ks, vs
 
     torch.cuda.synchronize()
+    if not args.no_cpu:
+        for f in deferred:
+            f()
     return head, out, nt
 
 
