@@ -13,11 +13,13 @@
 // and scale 0). Dequantised value = q * scale. Per-row scales make appends exact: a decode
 // step writes one new row and never has to requantise earlier rows of the block.
 //
-// One wavefront per (token, kv_head, K or V) row; lane l holds elements 2l, 2l+1 (+128 per
-// step for rows longer than 128).
+// Head dims 64/128/256/512 (aligned buffers): D/8 lanes per row, 8 elements per lane.
+// Other even head dims: one wavefront per (token, kv_head, K or V) row, lane l holding
+// elements 2l, 2l+1 (+128 per step for rows longer than 128).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "attn_common.hpp"
 #include "kernels.hpp"
@@ -78,6 +80,60 @@ __global__ __launch_bounds__(256) void write_kv_fp8_kernel(
     }
 }
 
+// Head dims that are multiples of 8: LPR = D / 8 lanes per row, 8 elements (one 16-byte
+// load, one 8-byte store) per lane, 64 / LPR rows per wavefront. Same arithmetic as above.
+template <int LPR>
+__global__ __launch_bounds__(256) void write_kv_fp8_vec_kernel(
+    const __bf16* __restrict__ k_new, const __bf16* __restrict__ v_new, uint8_t* __restrict__ k_cache,
+    uint8_t* __restrict__ v_cache, float* __restrict__ k_scale, float* __restrict__ v_scale,
+    const int32_t* __restrict__ slot_mapping, int total_tokens, int hkv, int max_slots) {
+    constexpr int D = LPR * 8;
+    constexpr int kRowsPerWave = 64 / LPR;
+    const int lane = threadIdx.x & 63;
+    const int sub = lane % LPR;                 // lane within its row
+    const int64_t row = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) *
+                            kRowsPerWave + lane / LPR;  // (t, h, K/V)
+    const bool live = row < static_cast<int64_t>(total_tokens) * hkv * 2;
+    const bool is_v = row & 1;
+    const int64_t th = row >> 1;
+    const int t = live ? static_cast<int>(th / hkv) : 0;
+    const int h = static_cast<int>(th - static_cast<int64_t>(t) * hkv);
+    const int slot = live ? slot_mapping[t] : -1;
+    const bool write = live && slot >= 0 && slot < max_slots;
+
+    u32x4 w = u32x4{0, 0, 0, 0};
+    if (live) w = load16((is_v ? v_new : k_new) + th * D + sub * 8);
+    float x[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        x[2 * i] = __uint_as_float(w[i] << 16);
+        x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(x[i]));
+#pragma unroll
+    for (int off = LPR / 2; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    const float inv = amax > 0.f ? 448.0f / amax : 0.f;
+    uint32_t q[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        float a[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a[e] = fminf(fmaxf(x[4 * i + e] * inv, -448.0f), 448.0f);
+        const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a[0], a[1], 0, false);
+        q[i] = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a[2], a[3], lo, true));
+    }
+    if (!write) return;
+    uint8_t* dst = (is_v ? v_cache : k_cache) + (static_cast<int64_t>(slot) * hkv + h) * D;
+    *reinterpret_cast<u32x2*>(dst + sub * 8) = u32x2{q[0], q[1]};
+    if (sub == 0) {
+        const int64_t si = (static_cast<int64_t>(slot / kFp8Block) * hkv + h) * kFp8Block +
+                           slot % kFp8Block;
+        (is_v ? v_scale : k_scale)[si] = amax > 0.f ? amax / 448.0f : 0.f;
+    }
+}
+
 }  // namespace
 
 hipError_t write_kv_cache_fp8(const void* k_new, const void* v_new, void* k_cache,
@@ -90,6 +146,23 @@ hipError_t write_kv_cache_fp8(const void* k_new, const void* v_new, void* k_cach
     auto* vn = static_cast<const __bf16*>(v_new);
     auto* kc = static_cast<uint8_t*>(k_cache);
     auto* vc = static_cast<uint8_t*>(v_cache);
+    const bool aligned = reinterpret_cast<uintptr_t>(k_new) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(v_new) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(k_cache) % 8 == 0 &&
+                         reinterpret_cast<uintptr_t>(v_cache) % 8 == 0;
+    auto vec = [&](auto lpr_tag) {
+        constexpr int LPR = decltype(lpr_tag)::value;
+        const int64_t waves = (rows + 64 / LPR - 1) / (64 / LPR);
+        write_kv_fp8_vec_kernel<LPR><<<static_cast<unsigned>((waves + kWaves - 1) / kWaves), 256,
+                                       0, stream>>>(kn, vn, kc, vc, k_scale, v_scale,
+                                                    slot_mapping, total_tokens, n_kv_heads,
+                                                    max_slots);
+        return hipGetLastError();
+    };
+    if (aligned && head_dim == 64) return vec(std::integral_constant<int, 8>{});
+    if (aligned && head_dim == 128) return vec(std::integral_constant<int, 16>{});
+    if (aligned && head_dim == 256) return vec(std::integral_constant<int, 32>{});
+    if (aligned && head_dim == 512) return vec(std::integral_constant<int, 64>{});
     if (head_dim <= 128)
         write_kv_fp8_kernel<1><<<grid, 256, 0, stream>>>(kn, vn, kc, vc, k_scale, v_scale,
                                                          slot_mapping, total_tokens, n_kv_heads,
