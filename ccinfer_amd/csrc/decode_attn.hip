@@ -190,9 +190,7 @@ __device__ bool balanced_lookup(const int32_t* __restrict__ context_lens, const 
 
 // K/V bytes are read once per (request, kv_head) and never again in the launch: streaming
 // (nontemporal) loads keep them from displacing reused lines in the caches. Measured on the
-// box: configs[1] 119 -> 108 us, configs[4] 715 -> 658 us. (The fp8 loads below cover a
-// cache line with several narrow loads and measured slower as nontemporal, so they stay
-// ordinary.)
+// box: configs[1] 119 -> 108 us, configs[4] 715 -> 658 us.
 template <typename T>
 __device__ __forceinline__ T nt_load(const T* p) {
     return __builtin_nontemporal_load(p);
@@ -248,10 +246,14 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<D>& c, const __bf16* __rest
     }
 }
 
-// fp8 cache: the same lane layout with one byte per element (K: 8 bytes per k-step, V: NV
-// bytes per token piece) plus the row scales of the chunk's tokens T(g, e) =
-// 16 * (e / 4) + 4 * g + e % 4: tokens 4g..4g+3 of each block, 16 contiguous bytes of the
-// block's scale line.
+// fp8 cache: one byte per element plus the row scales of the chunk's tokens T(g, e) =
+// 16 * (e / 4) + 4 * g + e % 4 (tokens 4g..4g+3 of each block: 16 contiguous bytes of the
+// block's scale line). K is read 16 bytes per lane: lane (row i, group g) takes bytes
+// 64 k2 + 16 g .. +16 of its row, i.e. dims 64 (kk / 2) + 16 g + 8 (kk % 2) .. +8 for k-step
+// kk; the dot product only needs Q's operand to use the same dim order (it does, F8 only),
+// and the row is covered by half as many, twice as wide loads as the bf16 order would give.
+// V keeps the bf16 layout (NV bytes per token piece; a 16-lane group reads whole rows) and
+// is read nontemporally; K stays cached (measured: configs[1] batch 73 -> 62 us).
 template <int D>
 struct ChunkRegsF8 {
     u32x2 k[2][DecodeShape<D>::kSteps];
@@ -276,8 +278,11 @@ __device__ __forceinline__ void load_chunk(ChunkRegsF8<D>& c, const uint8_t* __r
         const uint8_t* row =
             k_cache + ((static_cast<int64_t>(pbs[kb]) * kBlock + i) * hkv + kv_head) * D;
 #pragma unroll
-        for (int kk = 0; kk < S; ++kk)
-            c.k[kb][kk] = *reinterpret_cast<const u32x2*>(row + (kk * 4 + g) * 8);
+        for (int k2 = 0; k2 < S / 2; ++k2) {
+            const u32x4 w = *reinterpret_cast<const u32x4*>(row + k2 * 64 + g * 16);
+            c.k[kb][2 * k2] = u32x2{w[0], w[1]};
+            c.k[kb][2 * k2 + 1] = u32x2{w[2], w[3]};
+        }
         const int64_t sl = (static_cast<int64_t>(pbs[kb]) * hkv + kv_head) * kBlock + 4 * g;
         c.ks[kb] = *reinterpret_cast<const u32x4*>(k_scale + sl);
         c.vs[kb] = *reinterpret_cast<const u32x4*>(v_scale + sl);
@@ -290,13 +295,13 @@ __device__ __forceinline__ void load_chunk(ChunkRegsF8<D>& c, const uint8_t* __r
             v_cache + ((static_cast<int64_t>(pbs[kb]) * kBlock + off) * hkv + kv_head) * D +
             i * NV;
         if constexpr (NV == 4) {
-            c.v[e][0] = *reinterpret_cast<const uint32_t*>(row);
+            c.v[e][0] = nt_load(reinterpret_cast<const uint32_t*>(row));
         } else if constexpr (NV == 8) {
-            const u32x2 w = *reinterpret_cast<const u32x2*>(row);
+            const u32x2 w = nt_load(reinterpret_cast<const u32x2*>(row));
             c.v[e][0] = w[0];
             c.v[e][1] = w[1];
         } else {
-            const u32x4 w = *reinterpret_cast<const u32x4*>(row);
+            const u32x4 w = nt_load(reinterpret_cast<const u32x4*>(row));
 #pragma unroll
             for (int x = 0; x < 4; ++x) c.v[e][x] = w[x];
         }
@@ -554,14 +559,16 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
         return __builtin_amdgcn_readlane(jb < 64 ? bt_lo : bt_hi, jb & 63);
     };
 
-    // Q^T operand: lane (head j, grp g) holds dims (kk*4+g)*8 .. +8 of head j.
+    // Q^T operand: lane (head j, grp g) holds dims (kk*4+g)*8 .. +8 of head j (fp8: the
+    // permuted order of the fp8 K loads).
     bf16x8 qop[S];
     {
         const bool live = j < G;
         const __bf16* qv = q + (static_cast<int64_t>(qrow) * hq + h * G + (live ? j : 0)) * D;
 #pragma unroll
         for (int kk = 0; kk < S; ++kk) {
-            u32x4 w = load16(qv + (kk * 4 + g) * 8);
+            const int dim0 = F8 ? 64 * (kk >> 1) + 16 * g + 8 * (kk & 1) : (kk * 4 + g) * 8;
+            u32x4 w = load16(qv + dim0);
             if (!live) w = u32x4{0, 0, 0, 0};
             qop[kk] = __builtin_bit_cast(bf16x8, w);
         }
