@@ -4,7 +4,9 @@
 
 Inputs are the reference tests' own known-answer vectors (tests/kernel/test_decode_attn.cu
 :229-311, test_write_kv_cache.cu:15-98, test_prefill_attn.cu:24-105 with the LCG of
-test_naive_attn.cu:67-74) and tiny seeded instances of the benchmark configurations.
+test_naive_attn.cu:67-74, test_rope.cu:118-158, test_batch_translator.cu's mixed batch) and
+tiny seeded instances of the benchmark configurations and of the fused prologue, the batch
+metadata build and the fp8 cache write.
 Expected outputs come from the CPU oracle (oracle/, pinned by tests/test_oracle.py).
 """
 from __future__ import annotations
@@ -22,7 +24,8 @@ if str(ROOT) not in sys.path:
 import oracle  # noqa: E402
 
 NAMES = ["decode_kat", "write_kv_kat", "prefill_kat", "decode_small", "prefill_small",
-         "mixed_small"]
+         "mixed_small", "prologue_rope_kat", "prologue_small", "batch_meta_mixed",
+         "fp8_write_small"]
 
 
 def path(name: str) -> Path:
@@ -74,6 +77,45 @@ def inputs(name: str) -> dict:
                     k=_bf(rng.standard_normal((5 * 16, 8, 128))),
                     v=_bf(rng.standard_normal((5 * 16, 8, 128))), bt=bt,
                     qsl=np.array([0, 20, 21, 22], np.int32), ctx=np.array([36, 30, 9], np.int32))
+    if name == "prologue_rope_kat":
+        # the reference RoPE GQA test (tests/kernel/test_rope.cu:118-158): 2 tokens, 8 q / 2 kv
+        # heads, d=64, positions 5 and 17, a 32-position table with theta 1e4; no norm
+        q = ((np.arange(2 * 8 * 64) % 7) - 2).reshape(2, 8 * 64)
+        k = (((np.arange(2 * 2 * 64) + 3) % 9) - 3).reshape(2, 2 * 64)
+        v = ((np.arange(2 * 2 * 64) % 5) - 2).reshape(2, 2 * 64)
+        return dict(qkv=_bf(np.concatenate([q, k, v], 1)), positions=np.array([5, 17], np.int32),
+                    rope_cache=oracle.rope_cache_table(32, 64, 1e4),
+                    slots=np.array([3, 12], np.int32),
+                    k_cache=np.zeros((16, 2, 64), np.uint16),
+                    v_cache=np.zeros((16, 2, 64), np.uint16), nq=8, nkv=2, hd=64)
+    if name == "prologue_small":
+        # 5 tokens, 16 q / 8 kv heads, d=128, norm weights; one position outside the table and
+        # one skipped slot
+        return dict(qkv=_bf(rng.standard_normal((5, 32 * 128)) * 2),
+                    q_norm_w=_bf(rng.standard_normal(128)), k_norm_w=_bf(rng.standard_normal(128)),
+                    positions=np.array([0, 7, 63, 64, 30], np.int32),
+                    rope_cache=oracle.rope_cache_table(64, 128, 1e6),
+                    slots=np.array([1, -1, 9, 4, 17], np.int32),
+                    k_cache=oracle.lcg_fill(20 * 8 * 128, 9).reshape(20, 8, 128),
+                    v_cache=oracle.lcg_fill(20 * 8 * 128, 10).reshape(20, 8, 128),
+                    nq=16, nkv=8, hd=128)
+    if name == "batch_meta_mixed":
+        # the reference translator's mixed batch (a decode item with 8 cached tokens and a
+        # 16-token prefill chunk), plus a sampled 20-token prefill over two blocks and a
+        # decode item with a prefix-cache hit (16 cached tokens)
+        return dict(kv_written=np.array([8, 0, 0, 16], np.int32),
+                    new_tokens=np.array([1, 16, 20, 1], np.int32),
+                    flags=np.array([1, 0, 2, 1], np.int32),
+                    block_start=np.array([0, 1, 2, 4, 6], np.int32),
+                    blocks=np.array([5, 9, 7, 2, 4, 11], np.int32),
+                    num_tokens=38, mbpr=3, num_cache_blocks=32)
+    if name == "fp8_write_small":
+        k = rng.standard_normal((6, 2, 128)) * np.array([1.0, 300.0])[None, :, None]
+        k[2, 1] = 0.0  # an all-zero row
+        return dict(k_new=_bf(k), v_new=_bf(rng.standard_normal((6, 2, 128)) * 1e-3),
+                    slots=np.array([0, 17, 5, -1, 31, 16], np.int32),
+                    k_cache=np.zeros((32, 2, 128), np.uint8), v_cache=np.zeros((32, 2, 128), np.uint8),
+                    k_scale=np.zeros(64, np.float32), v_scale=np.zeros(64, np.float32))
     raise KeyError(name)
 
 
@@ -83,6 +125,23 @@ def compute(name: str, fx) -> dict:
         kc, vc = np.array(fx["k_cache"]), np.array(fx["v_cache"])
         oracle.write_kv_cache(fx["k_new"], fx["v_new"], kc, vc, fx["slots"])
         return dict(k_out=kc, v_out=vc)
+    if name in ("prologue_rope_kat", "prologue_small"):
+        kc, vc = np.array(fx["k_cache"]), np.array(fx["v_cache"])
+        qw = fx["q_norm_w"] if "q_norm_w" in fx else None
+        kw = fx["k_norm_w"] if "k_norm_w" in fx else None
+        q = oracle.qkv_prologue(fx["qkv"], qw, kw, fx["positions"], fx["rope_cache"], fx["slots"],
+                                kc, vc, int(fx["nq"]), int(fx["nkv"]), int(fx["hd"]), 1e-6)
+        return dict(q_out=q, k_out=kc, v_out=vc)
+    if name == "batch_meta_mixed":
+        st, o = oracle.build_batch_metadata(fx["kv_written"], fx["new_tokens"], fx["flags"],
+                                            fx["block_start"], fx["blocks"], int(fx["num_tokens"]),
+                                            int(fx["mbpr"]), 16, int(fx["num_cache_blocks"]))
+        return dict(status=np.array(st, np.int32), **{f"out_{k}": v for k, v in o.items()})
+    if name == "fp8_write_small":
+        arr = {k: np.array(fx[k]) for k in ("k_cache", "v_cache", "k_scale", "v_scale")}
+        oracle.write_kv_cache_fp8(fx["k_new"], fx["v_new"], arr["k_cache"], arr["v_cache"],
+                                  arr["k_scale"], arr["v_scale"], fx["slots"])
+        return {f"{k}_out": v for k, v in arr.items()}
     if name in ("decode_kat", "decode_small"):
         return dict(out=oracle.decode(fx["q"], fx["k"], fx["v"], fx["bt"], fx["ctx"], nthreads=1))
     out = oracle.prefill(fx["q"], fx["k"], fx["v"], fx["bt"], fx["qsl"], fx["ctx"], nthreads=1)

@@ -294,7 +294,8 @@ def test_threads_do_not_change_results():
 
 
 @pytest.mark.parametrize("name", ["decode_kat", "write_kv_kat", "prefill_kat", "decode_small",
-                                  "prefill_small", "mixed_small"])
+                                  "prefill_small", "mixed_small", "prologue_rope_kat",
+                                  "prologue_small", "batch_meta_mixed", "fp8_write_small"])
 def test_golden_fixtures_reproduce(name):
     """The committed fixtures (tests/golden/make_golden.py) match the current oracle."""
     from tests.golden import make_golden
