@@ -56,6 +56,7 @@ def load() -> ctypes.CDLL:
         lib.orc_e4m3_to_f32.restype = ctypes.c_float
         lib.orc_write_kv_cache_fp8.argtypes = [_P] * 7 + [_I] * 5
         lib.orc_decode_attention_fp8.argtypes = [_P] * 8 + [_I] * 7
+        lib.orc_prefill_attention_fp8.argtypes = [_P] * 9 + [_I] * 8
         _lib = lib
     return _lib
 
@@ -305,3 +306,19 @@ def decode_fp8(q, k_cache, v_cache, k_scale, v_scale, block_table, context_lens,
         _p(_c(v_scale, np.float32)), _p(bt), _p(_c(context_lens, np.int32)), _p(out), b,
         bt.shape[1], hq, k_cache.shape[1], d, block_size, nthreads or default_threads())
     return out
+
+
+def prefill_fp8(q, k_cache, v_cache, k_scale, v_scale, block_table, query_start_loc,
+                context_lens, block_size: int = 16, nthreads=None, out=None) -> np.ndarray:
+    """fp32 [T, Hq, D] over the fp8 cache; rows the reference leaves unwritten keep `out`."""
+    q = _c(q, np.uint16)
+    t, hq, d = q.shape
+    bt = _c(block_table, np.int32)
+    qsl = _c(query_start_loc, np.int32)
+    res = np.zeros((t, hq, d), np.float32) if out is None else _c(out, np.float32).copy()
+    load().orc_prefill_attention_fp8(
+        _p(q), _p(_c(k_cache, np.uint8)), _p(_c(v_cache, np.uint8)), _p(_c(k_scale, np.float32)),
+        _p(_c(v_scale, np.float32)), _p(bt), _p(qsl), _p(_c(context_lens, np.int32)), _p(res),
+        qsl.shape[0] - 1, t, bt.shape[1], hq, k_cache.shape[1], d, block_size,
+        nthreads or default_threads())
+    return res

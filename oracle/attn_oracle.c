@@ -698,3 +698,88 @@ void orc_decode_attention_fp8(const uint16_t* q, const uint8_t* k_cache, const u
     run_parallel(decode_one_fp8, &c, (int64_t)batch_size * num_q_heads, nthreads,
                  max_ctx_of(context_lens, batch_size));
 }
+
+/* Prefill over the fp8 cache: orc_prefill_attention's request lookup and causal range
+ * (prefill_attn.cu:80-241) with each K/V element read as e4m3 value * row scale. */
+typedef struct {
+    const uint16_t* q;
+    const uint8_t *k, *v;
+    const float *ks, *vs;
+    const int32_t *bt, *qsl, *ctx;
+    float* out;
+    int B, T, mbpr, hq, hkv, d, bs;
+} prefill_fp8_ctx;
+
+static void prefill_one_fp8(int64_t i, void* p, float* scores, int64_t* bases) {
+    const prefill_fp8_ctx* c = (const prefill_fp8_ctx*)p;
+    const int g = (int)(i / c->hq), qh = (int)(i % c->hq);
+    int req = 0;
+    while (req + 1 < c->B && c->qsl[req + 1] <= g) ++req;
+    const int qbeg = c->qsl[req];
+    const int qlen = c->qsl[req + 1] - qbeg;
+    const int local = g - qbeg;
+    if (qlen <= 0 || local < 0 || local >= qlen) return;
+    const int context_len = c->ctx[req];
+    const int prefix = context_len - qlen;
+    if (prefix < 0) return;
+    const int visible = prefix + local + 1;
+    if (visible <= 0 || visible > context_len) return;
+    const int kvh = qh / (c->hq / c->hkv);
+    const float scale = 1.0f / sqrtf((float)c->d);
+    const uint16_t* qv = c->q + ((int64_t)g * c->hq + qh) * c->d;
+    const int32_t* rb = c->bt + (int64_t)req * c->mbpr;
+    float* o = c->out + ((int64_t)g * c->hq + qh) * c->d;
+    float mx = -INFINITY;
+    int any = 0;
+    for (int pos = 0; pos < visible; ++pos) {
+        const int lb = pos / c->bs;
+        const int blk = lb < c->mbpr ? rb[lb] : -1;
+        if (blk < 0) {
+            bases[pos] = -1;
+            continue;
+        }
+        const int slot = blk * c->bs + pos % c->bs;
+        bases[pos] = slot;
+        const int64_t row = ((int64_t)slot * c->hkv + kvh) * c->d;
+        const float ks = c->ks[orc_fp8_scale_index(slot, kvh, c->hkv, c->bs)];
+        float s = 0.0f;
+        for (int d = 0; d < c->d; ++d)
+            s += orc_bf16_to_f32(qv[d]) * (e4m3_lut[c->k[row + d]] * ks);
+        s *= scale;
+        scores[pos] = s;
+        if (s > mx) mx = s;
+        any = 1;
+    }
+    for (int d = 0; d < c->d; ++d) o[d] = 0.0f;
+    if (!any) return;
+    float denom = 0.0f;
+    for (int pos = 0; pos < visible; ++pos) {
+        if (bases[pos] < 0) continue;
+        scores[pos] = expf(scores[pos] - mx);
+        denom += scores[pos];
+    }
+    const float inv = 1.0f / denom;
+    for (int pos = 0; pos < visible; ++pos) {
+        if (bases[pos] < 0) continue;
+        const int slot = (int)bases[pos];
+        const int64_t row = ((int64_t)slot * c->hkv + kvh) * c->d;
+        const float vs = c->vs[orc_fp8_scale_index(slot, kvh, c->hkv, c->bs)];
+        const float w = scores[pos] * inv;
+        for (int d = 0; d < c->d; ++d) o[d] += w * (e4m3_lut[c->v[row + d]] * vs);
+    }
+}
+
+void orc_prefill_attention_fp8(const uint16_t* q, const uint8_t* k_cache, const uint8_t* v_cache,
+                               const float* k_scale, const float* v_scale,
+                               const int32_t* block_table, const int32_t* query_start_loc,
+                               const int32_t* context_lens, float* out, int batch_size,
+                               int total_query_tokens, int max_blocks_per_req, int num_q_heads,
+                               int num_kv_heads, int head_dim, int cache_block_size,
+                               int nthreads) {
+    for (int b = 0; b < 256; ++b) e4m3_lut[b] = orc_e4m3_to_f32((uint8_t)b);  /* before workers */
+    prefill_fp8_ctx c = {q, k_cache, v_cache, k_scale, v_scale, block_table, query_start_loc,
+                         context_lens, out, batch_size, total_query_tokens, max_blocks_per_req,
+                         num_q_heads, num_kv_heads, head_dim, cache_block_size};
+    run_parallel(prefill_one_fp8, &c, (int64_t)total_query_tokens * num_q_heads, nthreads,
+                 max_ctx_of(context_lens, batch_size));
+}

@@ -145,6 +145,13 @@ void orc_decode_attention_fp8(const uint16_t* q, const uint8_t* k_cache, const u
                               float* out, int batch_size, int max_blocks_per_req,
                               int num_q_heads, int num_kv_heads, int head_dim,
                               int cache_block_size, int nthreads);
+void orc_prefill_attention_fp8(const uint16_t* q, const uint8_t* k_cache, const uint8_t* v_cache,
+                               const float* k_scale, const float* v_scale,
+                               const int32_t* block_table, const int32_t* query_start_loc,
+                               const int32_t* context_lens, float* out, int batch_size,
+                               int total_query_tokens, int max_blocks_per_req, int num_q_heads,
+                               int num_kv_heads, int head_dim, int cache_block_size,
+                               int nthreads);
 
 #ifdef __cplusplus
 }

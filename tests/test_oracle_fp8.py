@@ -132,3 +132,53 @@ def test_fp8_decode_equals_float64_attention_over_the_dequantised_cache(hq, hkv)
             vv = torch.from_numpy(vd[rows, h // g].astype(np.float64))[None]
             ref = F.scaled_dot_product_attention(qv, kk, vv)[0, 0].numpy()
             np.testing.assert_allclose(got[i, h], ref, rtol=2e-5, atol=2e-6)
+
+
+def test_fp8_prefill_equals_bf16_prefill_on_an_exact_image():
+    # fp8 bytes with scale 1/4 and a bf16 cache holding exactly their values: the two oracles
+    # run the same float operations, so the outputs agree bit for bit
+    rng = np.random.default_rng(21)
+    hq, hkv, d, nblk = 8, 2, 64, 12
+    slots = nblk * BS
+    codes = rng.integers(0, 256, (slots, hkv, d)).astype(np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0x30
+    kc8, vc8 = codes, np.roll(codes, 7)
+    kb = oracle.f32_to_bf16(oracle.e4m3_to_f32(kc8) * np.float32(0.25))
+    vb = oracle.f32_to_bf16(oracle.e4m3_to_f32(vc8) * np.float32(0.25))
+    qsl = np.array([0, 20, 21, 40], np.int32)
+    ctx = np.array([36, 60, 19], np.int32)
+    bt = np.array([[0, 3, 5, 7], [1, 2, 4, 6], [8, 9, -1, -1]], np.int32)
+    q = rnd_bf16(rng, (40, hq, d))
+    quarter = np.full(slots * hkv, 0.25, np.float32)
+    got = oracle.prefill_fp8(q, kc8, vc8, quarter, quarter, bt, qsl, ctx)
+    want = oracle.prefill(q, kb, vb, bt, qsl, ctx)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_fp8_prefill_equals_float64_causal_attention():
+    rng = np.random.default_rng(22)
+    hq, hkv, d, nblk = 4, 2, 128, 10
+    slots = nblk * BS
+    kc = rng.integers(0, 256, (slots, hkv, d)).astype(np.uint8)
+    kc[(kc & 0x7F) == 0x7F] = 0x11
+    vc = rng.integers(0, 256, (slots, hkv, d)).astype(np.uint8)
+    vc[(vc & 0x7F) == 0x7F] = 0x23
+    ks = rng.uniform(1e-3, 1e-2, slots * hkv).astype(np.float32)
+    vs = rng.uniform(1e-3, 1e-2, slots * hkv).astype(np.float32)
+    prefix, qlen = 40, 30
+    bt = rng.permutation(nblk)[:5].astype(np.int32)[None]
+    qsl = np.array([0, qlen], np.int32)
+    ctx = np.array([prefix + qlen], np.int32)
+    q = rnd_bf16(rng, (qlen, hq, d))
+    got = oracle.prefill_fp8(q, kc, vc, ks, vs, bt, qsl, ctx)
+    kd, vd = dequant(kc, ks, hkv), dequant(vc, vs, hkv)
+    pos = np.arange(prefix + qlen)
+    rows = bt[0, pos // BS] * BS + pos % BS
+    for h in range(hq):
+        qq = torch.from_numpy(oracle.bf16_to_f32(q[:, h]).astype(np.float64))[None]
+        kk = torch.from_numpy(kd[rows, h // (hq // hkv)].astype(np.float64))[None]
+        vv = torch.from_numpy(vd[rows, h // (hq // hkv)].astype(np.float64))[None]
+        mask = pos[None, :] <= prefix + np.arange(qlen)[:, None]
+        ref = F.scaled_dot_product_attention(qq, kk, vv,
+                                             attn_mask=torch.from_numpy(mask)[None])[0].numpy()
+        np.testing.assert_allclose(got[:, h], ref, rtol=2e-5, atol=2e-6)
