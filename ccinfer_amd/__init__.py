@@ -13,6 +13,7 @@ from .ops import (  # noqa: F401
     decode_attention_fp8,
     decode_workspace_size,
     prefill_attention,
+    prefill_attention_fp8,
     prefill_workspace_size,
     qkv_prologue,
     write_kv_cache,
@@ -29,6 +30,7 @@ __all__ = [
     "decode_attention_fp8",
     "decode_workspace_size",
     "prefill_attention",
+    "prefill_attention_fp8",
     "prefill_workspace_size",
     "qkv_prologue",
     "write_kv_cache",

@@ -28,6 +28,8 @@ SIGNATURES = {
     ),
     "ccinfer_write_kv_cache_fp8": (_c_int, [_vp] * 7 + [_c_int] * 4 + [_vp]),
     "ccinfer_decode_attention_fp8": (_c_int, [_vp] * 8 + [_c_int] * 6 + [_vp, _c_size, _vp]),
+    "ccinfer_prefill_attention_fp8": (
+        _c_int, [_vp] * 9 + [_c_int] * 7 + [_vp, _c_size, _vp]),
     "ccinfer_prefill_workspace_size": (_c_size, [_c_int] * 7),
     "ccinfer_prefill_attention": (
         _c_int,

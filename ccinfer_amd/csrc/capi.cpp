@@ -283,6 +283,35 @@ int ccinfer_prefill_attention(const void* q, const void* k_cache, const void* v_
                                            as_stream(stream)));
 }
 
+int ccinfer_prefill_attention_fp8(const void* q, const void* k_cache, const void* v_cache,
+                                  const float* k_scale, const float* v_scale,
+                                  const int32_t* block_table, const int32_t* query_start_loc,
+                                  const int32_t* context_lens, void* output, int batch_size,
+                                  int total_query_tokens, int max_blocks_per_req,
+                                  int num_q_heads, int num_kv_heads, int head_dim,
+                                  int cache_block_size, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+    if (!q || !k_cache || !v_cache || !k_scale || !v_scale || !block_table ||
+        !query_start_loc || !context_lens || !output)
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    if (!prefill_shape_ok(batch_size, total_query_tokens, max_blocks_per_req, num_q_heads,
+                          num_kv_heads, head_dim, cache_block_size))
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    // fp8 has the pipelined MFMA path only (head_dim 64 / 128)
+    if (!prefill_uses_fast(batch_size, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
+                           cache_block_size) ||
+        (head_dim != 64 && head_dim != 128))
+        return CCINFER_ERR_UNSUPPORTED;
+    const size_t need =
+        prefill_workspace_bytes(batch_size, total_query_tokens, max_blocks_per_req,
+                                num_q_heads, num_kv_heads, head_dim, cache_block_size);
+    if (workspace == nullptr || workspace_bytes < need) return CCINFER_ERR_INVALID_ARGUMENT;
+    return map_hip_error(prefill_attention_fp8(
+        q, k_cache, v_cache, k_scale, v_scale, block_table, query_start_loc, context_lens,
+        output, batch_size, total_query_tokens, max_blocks_per_req, num_q_heads, num_kv_heads,
+        head_dim, workspace, as_stream(stream)));
+}
+
 const char* ccinfer_error_message(int code) {
     switch (code) {
         case CCINFER_OK: return "ok";

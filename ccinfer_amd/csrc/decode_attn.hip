@@ -308,14 +308,6 @@ __device__ __forceinline__ void load_chunk(ChunkRegsF8<D>& c, const uint8_t* __r
     }
 }
 
-// Two E4M3 bytes (the low or high half of `w`) -> a bf16 pair; exact (every E4M3 value is a
-// bf16 value).
-template <bool kHi>
-__device__ __forceinline__ uint32_t e4m3x2_to_bf16x2(uint32_t w) {
-    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(
-                                            static_cast<int>(w), 1.0f, kHi));
-}
-
 // Online-softmax state of one wavefront: lane (head j, grp g) holds O[j][NV*(4g+r)+n] in
 // acc[n][r], the running max m (base-2 domain, per head, replicated over the 4 grp lanes)
 // and a per-lane partial sum l.

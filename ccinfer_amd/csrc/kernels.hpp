@@ -93,6 +93,16 @@ hipError_t decode_attention_fp8(const void* q, const void* k_cache, const void* 
                                 int num_q_heads, int num_kv_heads, int head_dim,
                                 const DecodePlan& plan, void* workspace, hipStream_t stream);
 
+// Prefill over the fp8 cache (head_dim 64 / 128, the pipelined path): the bf16 prefill's
+// planner, workspace layout and semantics; single-token requests use decode_attention_fp8.
+hipError_t prefill_attention_fp8(const void* q, const void* k_cache, const void* v_cache,
+                                 const float* k_scale, const float* v_scale,
+                                 const int32_t* block_table, const int32_t* query_start_loc,
+                                 const int32_t* context_lens, void* output, int batch_size,
+                                 int total_query_tokens, int max_blocks_per_req,
+                                 int num_q_heads, int num_kv_heads, int head_dim,
+                                 void* workspace, hipStream_t stream);
+
 // ---- per-step batch metadata built on the device ------------------------------
 constexpr int kItemDecode = 1;  // item flag: decode item (exactly one new token)
 constexpr int kItemSample = 2;  // item flag: sample the item's last token

@@ -575,10 +575,15 @@ constexpr int kPipeQT = 2;  // 32 rows per wavefront
 
 __host__ __device__ constexpr bool pipe_head_dim(int d) { return d == 64 || d == 128; }
 
-template <int D, int QTT>
+// F8: the cache holds OCP E4M3 bytes with row scales (k_scale / v_scale). Tiles are then
+// staged as bytes into a two-tile ring and dequantised (byte * row scale, rounded to bf16)
+// into a two-tile ring of bf16 tiles in the same swizzled layout, so everything after the
+// staging is the bf16 kernel.
+template <int D, int QTT, bool F8 = false>
 __global__ __launch_bounds__((PipeShape<D, QTT>::kThreads))
-void prefill_pipe_kernel(const __bf16* __restrict__ q, const __bf16* __restrict__ k_cache,
-                         const __bf16* __restrict__ v_cache,
+void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ k_cache_v,
+                         const void* __restrict__ v_cache_v, const float* __restrict__ k_scale,
+                         const float* __restrict__ v_scale,
                          const int32_t* __restrict__ block_table,
                          const int32_t* __restrict__ qsl,
                          const int32_t* __restrict__ context_lens, __bf16* __restrict__ out,
@@ -593,14 +598,24 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const __bf16* __restrict_
     constexpr int kPipeWaves = Sh::kWaves;
     constexpr int kPipeThreads = Sh::kThreads;
     constexpr int kPipeRows = Sh::kRows;
+    const __bf16* __restrict__ k_cache = static_cast<const __bf16*>(k_cache_v);
+    const __bf16* __restrict__ v_cache = static_cast<const __bf16*>(v_cache_v);
     // Three K/V buffers as distinct arrays (see prefill_tile_kernel: the compiler then knows
-    // the direct-to-LDS loads into one buffer never alias reads of another).
-    __shared__ __attribute__((aligned(16))) __bf16 lds_k0[kKeysPerTile * D];
-    __shared__ __attribute__((aligned(16))) __bf16 lds_k1[kKeysPerTile * D];
-    __shared__ __attribute__((aligned(16))) __bf16 lds_k2[kKeysPerTile * D];
-    __shared__ __attribute__((aligned(16))) __bf16 lds_v0[kKeysPerTile * D];
-    __shared__ __attribute__((aligned(16))) __bf16 lds_v1[kKeysPerTile * D];
-    __shared__ __attribute__((aligned(16))) __bf16 lds_v2[kKeysPerTile * D];
+    // the direct-to-LDS loads into one buffer never alias reads of another). fp8 uses two
+    // bf16 buffers plus two byte-staging buffers.
+    constexpr int kTileElems = kKeysPerTile * D;
+    constexpr int kBuf2 = F8 ? 8 : kTileElems;
+    constexpr int kF8Bytes = F8 ? kTileElems : 16;
+    __shared__ __attribute__((aligned(16))) __bf16 lds_k0[kTileElems];
+    __shared__ __attribute__((aligned(16))) __bf16 lds_k1[kTileElems];
+    __shared__ __attribute__((aligned(16))) __bf16 lds_k2[kBuf2];
+    __shared__ __attribute__((aligned(16))) __bf16 lds_v0[kTileElems];
+    __shared__ __attribute__((aligned(16))) __bf16 lds_v1[kTileElems];
+    __shared__ __attribute__((aligned(16))) __bf16 lds_v2[kBuf2];
+    __shared__ __attribute__((aligned(16))) uint8_t lds_k8_0[kF8Bytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds_k8_1[kF8Bytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds_v8_0[kF8Bytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds_v8_1[kF8Bytes];
     __shared__ uint8_t lds_valid0[kKeysPerTile];
     __shared__ uint8_t lds_valid1[kKeysPerTile];
     __shared__ uint8_t lds_valid2[kKeysPerTile];
@@ -657,11 +672,24 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const __bf16* __restrict_
     // Zero the K/V buffers once: slots that are never loaded must hold finite values.
     {
         constexpr int kWords = kKeysPerTile * D / 8;  // 16-byte words per buffer
-        __bf16* bufs[6] = {lds_k0, lds_k1, lds_k2, lds_v0, lds_v1, lds_v2};
+        if constexpr (F8) {
+            __bf16* bufs[4] = {lds_k0, lds_k1, lds_v0, lds_v1};
 #pragma unroll
-        for (int bi = 0; bi < 6; ++bi)
-            for (int i = threadIdx.x; i < kWords; i += kPipeThreads)
-                reinterpret_cast<u32x4*>(bufs[bi])[i] = u32x4{0, 0, 0, 0};
+            for (int bi = 0; bi < 4; ++bi)
+                for (int i = threadIdx.x; i < kWords; i += kPipeThreads)
+                    reinterpret_cast<u32x4*>(bufs[bi])[i] = u32x4{0, 0, 0, 0};
+            uint8_t* bufs8[4] = {lds_k8_0, lds_k8_1, lds_v8_0, lds_v8_1};
+#pragma unroll
+            for (int bi = 0; bi < 4; ++bi)
+                for (int i = threadIdx.x; i < kWords / 2; i += kPipeThreads)
+                    reinterpret_cast<u32x4*>(bufs8[bi])[i] = u32x4{0, 0, 0, 0};
+        } else {
+            __bf16* bufs[6] = {lds_k0, lds_k1, lds_k2, lds_v0, lds_v1, lds_v2};
+#pragma unroll
+            for (int bi = 0; bi < 6; ++bi)
+                for (int i = threadIdx.x; i < kWords; i += kPipeThreads)
+                    reinterpret_cast<u32x4*>(bufs[bi])[i] = u32x4{0, 0, 0, 0};
+        }
     }
 
     // Staging constants. Load x of a wavefront fills the 64 16-byte LDS slots starting at
@@ -729,6 +757,79 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const __bf16* __restrict_
                 lvalid[row] = static_cast<uint8_t>(pb >= 0 && in_range);
         }
     };
+
+    // ---- fp8 staging: tile t's bytes (16 per lane, linear in LDS) and its row scales ----
+    // Thread p (< kCh8) later converts 16-byte chunk p of the tile: row p / CPR8, dims
+    // 16 (p % CPR8) .. +16; it also fetches that row's two scales when the tile is staged.
+    constexpr int CPR8 = D / 16;
+    constexpr int kCh8 = kKeysPerTile * CPR8;
+    constexpr int NL8 = (kCh8 + kPipeThreads - 1) / kPipeThreads;
+    const uint8_t* __restrict__ k_cache8 = static_cast<const uint8_t*>(k_cache_v);
+    const uint8_t* __restrict__ v_cache8 = static_cast<const uint8_t*>(v_cache_v);
+    const int64_t blk_bytes8 = static_cast<int64_t>(kBlock) * hkv * D;
+    auto stage8 = [&](int t, uint8_t* lk8, uint8_t* lv8, uint8_t* lvalid, float& sk, float& sv)
+                      __attribute__((always_inline)) {
+        const int key_base = t * kKeysPerTile;
+#pragma unroll
+        for (int x = 0; x < NL8; ++x) {
+            const int slot0 = (x * kPipeWaves + wave) * 64;
+            if (slot0 >= kCh8) break;  // wave-uniform
+            const int p = slot0 + lane;
+            const int row = p / CPR8;
+            const int pb = __builtin_amdgcn_readfirstlane(
+                lds_bt[t * (kKeysPerTile / kBlock) + ((slot0 / CPR8) >> 4)]);
+            const bool in_range = key_base + row < kv_end;
+            if (pb >= 0 && in_range) {
+                const int64_t off = static_cast<int64_t>(pb) * blk_bytes8 +
+                                    ((row & (kBlock - 1)) * hkv + kvh) * D + (p % CPR8) * 16;
+                __builtin_amdgcn_global_load_lds(
+                    (void*)(k_cache8 + off),
+                    (__attribute__((address_space(3))) void*)(lk8 + slot0 * 16), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(
+                    (void*)(v_cache8 + off),
+                    (__attribute__((address_space(3))) void*)(lv8 + slot0 * 16), 16, 0, 0);
+            }
+            if ((p % CPR8) == 0) lvalid[row] = static_cast<uint8_t>(pb >= 0 && in_range);
+        }
+        sk = 0.f;
+        sv = 0.f;
+        if (static_cast<int>(threadIdx.x) < kCh8) {
+            const int row = threadIdx.x / CPR8;
+            const int pb = lds_bt[t * (kKeysPerTile / kBlock) + (row >> 4)];
+            if (pb >= 0 && key_base + row < kv_end) {
+                const int64_t si = (static_cast<int64_t>(pb) * hkv + kvh) * kBlock + (row & 15);
+                sk = k_scale[si];
+                sv = v_scale[si];
+            }
+        }
+    };
+    // Bytes of one staged tile -> bf16 tile (byte * row scale, rounded to bf16), written in
+    // the swizzled layout the operand reads expect.
+    auto convert8 = [&](const uint8_t* lk8, const uint8_t* lv8, __bf16* lk, __bf16* lv,
+                        float sk, float sv) __attribute__((always_inline)) {
+        const int p = threadIdx.x;
+        if (p >= kCh8) return;
+        const int row = p / CPR8;
+        const int c = p % CPR8;
+        auto deq = [&](const uint8_t* src, __bf16* dst, float sc) __attribute__((always_inline)) {
+            const u32x4 w = *reinterpret_cast<const u32x4*>(src + p * 16);
+            u32x4 o[2];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t lo = e4m3x2_to_bf16x2<false>(w[i]);
+                const uint32_t hi = e4m3x2_to_bf16x2<true>(w[i]);
+                o[i >> 1][(i & 1) * 2] =
+                    pack_bf16x2(__uint_as_float(lo << 16) * sc, __uint_as_float(lo & 0xffff0000u) * sc);
+                o[i >> 1][(i & 1) * 2 + 1] =
+                    pack_bf16x2(__uint_as_float(hi << 16) * sc, __uint_as_float(hi & 0xffff0000u) * sc);
+            }
+            *reinterpret_cast<u32x4*>(dst + lds_off<D>(row, 2 * c)) = o[0];
+            *reinterpret_cast<u32x4*>(dst + lds_off<D>(row, 2 * c + 1)) = o[1];
+        };
+        deq(lk8, lk, sk);
+        deq(lv8, lv, sv);
+    };
+    float sk8[2] = {0.f, 0.f}, sv8[2] = {0.f, 0.f};  // scales of the tiles staged in ring slot
 
     // Q^T operands: lane (query j, grp g) holds dims (kk*4+g)*8.. of row tw + qt*16 + j.
     bf16x8 qop[QT][S];
@@ -909,12 +1010,20 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const __bf16* __restrict_
     float mt[QT];
 
     // Prologue: tiles 0 and 1 in flight, S of tile 0 / half 0 formed, masked and maxed.
-    stage(0, lds_k0, lds_v0, lds_valid0);
-    if (ntiles > 1) {
-        stage(1, lds_k1, lds_v1, lds_valid1);
-        __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * NL));  // tile 0 landed (vmcnt <= tile 1's)
-    } else {
+    if constexpr (F8) {
+        stage8(0, lds_k8_0, lds_v8_0, lds_valid0, sk8[0], sv8[0]);
+        if (ntiles > 1) stage8(1, lds_k8_1, lds_v8_1, lds_valid1, sk8[1], sv8[1]);
         __builtin_amdgcn_s_waitcnt(0x0F70);
+        __syncthreads();
+        convert8(lds_k8_0, lds_v8_0, lds_k0, lds_v0, sk8[0], sv8[0]);
+    } else {
+        stage(0, lds_k0, lds_v0, lds_valid0);
+        if (ntiles > 1) {
+            stage(1, lds_k1, lds_v1, lds_valid1);
+            __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * NL));  // tile 0 landed (vmcnt <= tile 1's)
+        } else {
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+        }
     }
     __syncthreads();
     qk_half(lds_k0, 0, sc);
@@ -930,6 +1039,7 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const __bf16* __restrict_
         constexpr int BL = decltype(ld)::value;
         constexpr bool kMask = decltype(mask_tag)::value;
         constexpr bool kLast = decltype(last_tag)::value;
+        static_assert(!F8 || (BC < 2 && BN < 2 && BL < 2), "fp8 runs a two-tile ring");
         const __bf16* kc = BC == 0 ? lds_k0 : (BC == 1 ? lds_k1 : lds_k2);
         const __bf16* vc = BC == 0 ? lds_v0 : (BC == 1 ? lds_v1 : lds_v2);
         const uint8_t* valc = BC == 0 ? lds_valid0 : (BC == 1 ? lds_valid1 : lds_valid2);
@@ -957,7 +1067,18 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const __bf16* __restrict_
         if constexpr (!kLast) {
             __builtin_amdgcn_s_waitcnt(0x0F70);  // this wavefront's loads of tile t+1 landed
             __syncthreads();                     // ... and everyone's; tile t-1 is free
-            if (t + 2 < ntiles) stage(t + 2, kl, vl, vall);
+            if constexpr (F8) {
+                // tile t+1: bytes (ring slot BN) -> bf16 (slot BN, which held tile t-1);
+                // then tile t+2's bytes go to slot BL (= BC, converted one step ago)
+                convert8(BN == 0 ? lds_k8_0 : lds_k8_1, BN == 0 ? lds_v8_0 : lds_v8_1,
+                         BN == 0 ? lds_k0 : lds_k1, BN == 0 ? lds_v0 : lds_v1, sk8[BN], sv8[BN]);
+                __syncthreads();
+                if (t + 2 < ntiles)
+                    stage8(t + 2, BL == 0 ? lds_k8_0 : lds_k8_1, BL == 0 ? lds_v8_0 : lds_v8_1,
+                           vall, sk8[BL], sv8[BL]);
+            } else {
+                if (t + 2 < ntiles) stage(t + 2, kl, vl, vall);
+            }
         }
         // X: exp of (t, 1) || QK of (t+1, 0)
         __builtin_amdgcn_sched_barrier(0);
@@ -987,6 +1108,25 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const __bf16* __restrict_
     const int mask_free_tiles = holes ? 0 : (prefix + t0 + 1) / kKeysPerTile;
     const int mf_steps = max(0, min(ntiles - 1, mask_free_tiles - 1));
     int t = 0;
+    if constexpr (F8) {
+        // two-tile ring: tile t in slot t % 2; the stage target of step t is slot t % 2 too
+        for (; t + 2 <= mf_steps; t += 2) {
+            step(t, B0{}, B1{}, B0{}, F{}, F{});
+            step(t + 1, B1{}, B0{}, B1{}, F{}, F{});
+        }
+        for (;;) {
+            if (t >= ntiles - 1) break;
+            step(t, B0{}, B1{}, B0{}, T{}, F{});
+            ++t;
+            if (t >= ntiles - 1) break;
+            step(t, B1{}, B0{}, B1{}, T{}, F{});
+            ++t;
+        }
+        if (t % 2 == 0)
+            step(t, B0{}, B1{}, B0{}, T{}, T{});
+        else
+            step(t, B1{}, B0{}, B1{}, T{}, T{});
+    } else {
     for (; t + 3 <= mf_steps; t += 3) {
         step(t, B0{}, B1{}, B2{}, F{}, F{});
         step(t + 1, B1{}, B2{}, B0{}, F{}, F{});
@@ -1007,6 +1147,7 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const __bf16* __restrict_
         case 0: step(t, B0{}, B1{}, B2{}, T{}, T{}); break;
         case 1: step(t, B1{}, B2{}, B0{}, T{}, T{}); break;
         default: step(t, B2{}, B0{}, B1{}, T{}, T{}); break;
+    }
     }
 
     // Epilogue: lane (j, g) holds O[row][16n + 4g + r] = acc[qt][n][r].
@@ -1064,8 +1205,9 @@ PrefillLayout prefill_layout(int batch_size, int total_query_tokens, int max_blo
     return L;
 }
 
-template <int D>
+template <int D, bool F8>
 hipError_t launch_tiles(const void* q, const void* k_cache, const void* v_cache,
+                        const float* k_scale, const float* v_scale,
                         const int32_t* block_table, const int32_t* qsl,
                         const int32_t* context_lens, void* output, int total_query_tokens,
                         int mbpr, int hq, int hkv, int block_size, const int32_t* counts,
@@ -1076,13 +1218,15 @@ hipError_t launch_tiles(const void* q, const void* k_cache, const void* v_cache,
     const int64_t grid = static_cast<int64_t>(max_tiles) * U;
     const float scale_log2 = kLog2e / sqrtf(static_cast<float>(D));
     if constexpr (pipe_head_dim(D)) {
-        prefill_pipe_kernel<D, kPipeQT>
+        prefill_pipe_kernel<D, kPipeQT, F8>
             <<<static_cast<unsigned>(grid), PipeShape<D, kPipeQT>::kThreads, 0, stream>>>(
-            static_cast<const __bf16*>(q), static_cast<const __bf16*>(k_cache),
-            static_cast<const __bf16*>(v_cache), block_table, qsl, context_lens,
+            static_cast<const __bf16*>(q), k_cache, v_cache, k_scale, v_scale, block_table, qsl,
+            context_lens,
             static_cast<__bf16*>(output), counts, tiles, total_query_tokens, mbpr, hq, hkv,
             scale_log2);
         return hipGetLastError();
+    } else if constexpr (F8) {
+        return hipErrorInvalidValue;  // fp8 has the pipelined path only
     } else {
         prefill_tile_kernel<D><<<static_cast<unsigned>(grid), kThreads, 0, stream>>>(
             static_cast<const __bf16*>(q), static_cast<const __bf16*>(k_cache),
@@ -1184,12 +1328,15 @@ class SideStream {
 
 }  // namespace
 
-hipError_t prefill_attention(const void* q, const void* k_cache, const void* v_cache,
-                             const int32_t* block_table, const int32_t* query_start_loc,
-                             const int32_t* context_lens, void* output, int batch_size,
-                             int total_query_tokens, int max_blocks_per_req, int num_q_heads,
-                             int num_kv_heads, int head_dim, int block_size, void* workspace,
-                             hipStream_t stream) {
+namespace {
+
+template <bool F8>
+hipError_t prefill_impl(const void* q, const void* k_cache, const void* v_cache,
+                        const float* k_scale, const float* v_scale, const int32_t* block_table,
+                        const int32_t* query_start_loc, const int32_t* context_lens,
+                        void* output, int batch_size, int total_query_tokens,
+                        int max_blocks_per_req, int num_q_heads, int num_kv_heads, int head_dim,
+                        int block_size, void* workspace, hipStream_t stream) {
     if (batch_size > kMaxPlanRequests) return hipErrorInvalidValue;
     const PrefillLayout L = prefill_layout(batch_size, total_query_tokens, max_blocks_per_req,
                                            num_q_heads, num_kv_heads, head_dim, block_size);
@@ -1218,9 +1365,15 @@ hipError_t prefill_attention(const void* q, const void* k_cache, const void* v_c
     items.denom_eps = 0.0f;
     items.zero_invalid = false;
     auto launch_decode_items = [&](hipStream_t s) {
-        return decode_attention(q, k_cache, v_cache, block_table, context_lens, output, items,
-                                max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
-                                block_size, L.plan, ws + L.decode_ws_off, s);
+        if constexpr (F8)
+            return decode_attention_fp8(q, k_cache, v_cache, k_scale, v_scale, block_table,
+                                        context_lens, output, items, max_blocks_per_req,
+                                        num_q_heads, num_kv_heads, head_dim, L.plan,
+                                        ws + L.decode_ws_off, s);
+        else
+            return decode_attention(q, k_cache, v_cache, block_table, context_lens, output,
+                                    items, max_blocks_per_req, num_q_heads, num_kv_heads,
+                                    head_dim, block_size, L.plan, ws + L.decode_ws_off, s);
     };
     std::optional<SideStream> side;
     if (batch_size >= kOverlapMinRequests) {
@@ -1231,19 +1384,22 @@ hipError_t prefill_attention(const void* q, const void* k_cache, const void* v_c
     }
     switch (head_dim) {
         case 64:
-            err = launch_tiles<64>(q, k_cache, v_cache, block_table, query_start_loc,
+            err = launch_tiles<64, F8>(q, k_cache, v_cache, k_scale, v_scale, block_table,
+                                        query_start_loc,
                                    context_lens, output, total_query_tokens, max_blocks_per_req,
                                    num_q_heads, num_kv_heads, block_size, counts, tiles,
                                    zero_row, L.max_tiles, stream);
             break;
         case 128:
-            err = launch_tiles<128>(q, k_cache, v_cache, block_table, query_start_loc,
+            err = launch_tiles<128, F8>(q, k_cache, v_cache, k_scale, v_scale, block_table,
+                                        query_start_loc,
                                     context_lens, output, total_query_tokens, max_blocks_per_req,
                                     num_q_heads, num_kv_heads, block_size, counts, tiles,
                                     zero_row, L.max_tiles, stream);
             break;
         case 256:
-            err = launch_tiles<256>(q, k_cache, v_cache, block_table, query_start_loc,
+            err = launch_tiles<256, F8>(q, k_cache, v_cache, k_scale, v_scale, block_table,
+                                        query_start_loc,
                                     context_lens, output, total_query_tokens, max_blocks_per_req,
                                     num_q_heads, num_kv_heads, block_size, counts, tiles,
                                     zero_row, L.max_tiles, stream);
@@ -1253,6 +1409,34 @@ hipError_t prefill_attention(const void* q, const void* k_cache, const void* v_c
     }
     if (err != hipSuccess) return err;
     return side ? side->join() : launch_decode_items(stream);
+}
+
+}  // namespace
+
+hipError_t prefill_attention(const void* q, const void* k_cache, const void* v_cache,
+                             const int32_t* block_table, const int32_t* query_start_loc,
+                             const int32_t* context_lens, void* output, int batch_size,
+                             int total_query_tokens, int max_blocks_per_req, int num_q_heads,
+                             int num_kv_heads, int head_dim, int block_size, void* workspace,
+                             hipStream_t stream) {
+    return prefill_impl<false>(q, k_cache, v_cache, nullptr, nullptr, block_table,
+                               query_start_loc, context_lens, output, batch_size,
+                               total_query_tokens, max_blocks_per_req, num_q_heads, num_kv_heads,
+                               head_dim, block_size, workspace, stream);
+}
+
+hipError_t prefill_attention_fp8(const void* q, const void* k_cache, const void* v_cache,
+                                 const float* k_scale, const float* v_scale,
+                                 const int32_t* block_table, const int32_t* query_start_loc,
+                                 const int32_t* context_lens, void* output, int batch_size,
+                                 int total_query_tokens, int max_blocks_per_req,
+                                 int num_q_heads, int num_kv_heads, int head_dim,
+                                 void* workspace, hipStream_t stream) {
+    if (!pipe_head_dim(head_dim)) return hipErrorInvalidValue;
+    return prefill_impl<true>(q, k_cache, v_cache, k_scale, v_scale, block_table,
+                              query_start_loc, context_lens, output, batch_size,
+                              total_query_tokens, max_blocks_per_req, num_q_heads, num_kv_heads,
+                              head_dim, kBlock, workspace, stream);
 }
 
 }  // namespace ccinfer::hipk

@@ -292,6 +292,41 @@ def decode_attention_fp8(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.
     return output
 
 
+def prefill_attention_fp8(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                          k_scale: torch.Tensor, v_scale: torch.Tensor,
+                          block_table: torch.Tensor, query_start_loc: torch.Tensor,
+                          context_lens: torch.Tensor, output: Optional[torch.Tensor] = None,
+                          cache_block_size: int = 16,
+                          workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """prefill_attention over an fp8 cache written by write_kv_cache_fp8."""
+    op = "prefill_attention_fp8"
+    _dev_tensor(q, torch.bfloat16, op)
+    for t in (k_cache, v_cache):
+        _dev_tensor(t, torch.uint8, op)
+    for t in (k_scale, v_scale):
+        _dev_tensor(t, torch.float32, op)
+    for t in (block_table, query_start_loc, context_lens):
+        _dev_tensor(t, torch.int32, op)
+    _require(q.dim() == 3 and block_table.dim() == 2, op)
+    total, hq, d = q.shape
+    slots, hkv, dk = _kv_shape(k_cache)
+    b = block_table.shape[0]
+    _require(dk == d and query_start_loc.numel() == b + 1 and context_lens.numel() == b, op)
+    _require(min(k_scale.numel(), v_scale.numel()) >= fp8_scale_numel(slots, hkv), op)
+    if output is None:
+        output = torch.empty_like(q)
+    _dev_tensor(output, torch.bfloat16, op)
+    _require(output.shape == q.shape, op)
+    mbpr = block_table.shape[1]
+    need = prefill_workspace_size(b, total, mbpr, hq, hkv, d, cache_block_size)
+    ws, ws_bytes = _workspace(need, q.device, workspace)
+    _check(_lib.load().ccinfer_prefill_attention_fp8(
+        _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale), _ptr(block_table),
+        _ptr(query_start_loc), _ptr(context_lens), _ptr(output), b, total, mbpr, hq, hkv, d,
+        cache_block_size, _ptr(ws), ws_bytes, _stream()), op)
+    return output
+
+
 def prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                       block_table: torch.Tensor, query_start_loc: torch.Tensor,
                       context_lens: torch.Tensor, output: Optional[torch.Tensor] = None,

@@ -162,6 +162,20 @@ int ccinfer_prefill_attention(const void* q, const void* k_cache, const void* v_
                               int num_kv_heads, int head_dim, int cache_block_size,
                               void* workspace, size_t workspace_bytes, void* stream);
 
+/* Replaces launch_prefill_attention (src/kernel/cuda_kernels.h:61-66) for an fp8 cache
+ * (layout and scales as for ccinfer_write_kv_cache_fp8): the same semantics, planner and
+ * workspace (ccinfer_prefill_workspace_size) as ccinfer_prefill_attention, with K/V read as
+ * byte * row scale; single-token requests of a mixed batch go through the fp8 decode.
+ * head_dim 64 or 128 on the MFMA path (CCINFER_ERR_UNSUPPORTED otherwise). */
+int ccinfer_prefill_attention_fp8(const void* q, const void* k_cache, const void* v_cache,
+                                  const float* k_scale, const float* v_scale,
+                                  const int32_t* block_table, const int32_t* query_start_loc,
+                                  const int32_t* context_lens, void* output, int batch_size,
+                                  int total_query_tokens, int max_blocks_per_req,
+                                  int num_q_heads, int num_kv_heads, int head_dim,
+                                  int cache_block_size, void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
 /* Human-readable text for a status code (the reference's error_message()). */
 const char* ccinfer_error_message(int code);
 

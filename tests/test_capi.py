@@ -194,3 +194,27 @@ def test_fp8_validation(lib):
     a = list(okd)
     a[13] = 32
     assert dec(*a) == INVALID
+
+
+def test_prefill_fp8_validation(lib):
+    pf = lib.ccinfer_prefill_attention_fp8
+    need = lib.ccinfer_prefill_workspace_size(2, 64, 8, 16, 8, 128, 16)
+    ok = [FAKE] * 9 + [2, 64, 8, 16, 8, 128, 16, FAKE, need, None]
+    assert need > 0
+    for i in range(9):
+        a = list(ok)
+        a[i] = None
+        assert pf(*a) == INVALID, i
+    for i in range(9, 16):
+        a = list(ok)
+        a[i] = 0
+        assert pf(*a) == INVALID, i
+    a = list(ok)
+    a[14] = 96                   # a valid bf16 prefill head dim; fp8 is MFMA-only (64 / 128)
+    assert pf(*a) == 26          # CCINFER_ERR_UNSUPPORTED
+    a = list(ok)
+    a[17] = need - 1
+    assert pf(*a) == INVALID
+    a = list(ok)
+    a[16] = None
+    assert pf(*a) == INVALID

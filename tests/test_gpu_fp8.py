@@ -102,3 +102,59 @@ def test_decode_fp8_masks_holes_and_bad_rows(gpu):
     assert_attn_close(f32(out), want, "fp8 holes")
     assert np.all(f32(out)[3] == 0)
     assert rng is not None and slots > 0
+
+
+def _dequant_bf16(kc, ks, hkv):
+    """bf16(byte * row scale) of every cache row, rounded as the fp8 prefill's LDS pass does
+    (float32 product, then round to nearest even bf16)."""
+    slots = kc.shape[0]
+    vals = oracle.e4m3_to_f32(kc.reshape(-1)).reshape(kc.shape).astype(np.float32)
+    idx = oracle.fp8_scale_index(np.arange(slots)[:, None], np.arange(hkv)[None, :], hkv)
+    return oracle.f32_to_bf16((vals * ks[idx][..., None]).astype(np.float32))
+
+
+@pytest.mark.parametrize("hq,hkv,d,n_seqs,prefix,new", [
+    (16, 8, 128, 3, 64, 200), (16, 4, 128, 2, 48, 130), (8, 8, 64, 3, 16, 90),
+])
+def test_prefill_fp8_equals_bf16_prefill_of_its_dequantised_cache(gpu, hq, hkv, d, n_seqs,
+                                                                    prefix, new):
+    """After staging, the fp8 prefill runs the bf16 pipeline on bf16(byte * scale) tiles:
+    its output is bit-identical to the bf16 prefill over a cache holding those values."""
+    from ccinfer_amd import prefill_attention, prefill_attention_fp8
+    say(f"fp8 prefill exact hq={hq} hkv={hkv} d={d}")
+    w = W.prefill_prefix(device=gpu, seed=hq + d + new, n_seqs=n_seqs, prefix=prefix, new=new,
+                         hq=hq, hkv=hkv, d=d)
+    meta = w.device_meta(gpu)
+    kc, vc, ks, vs = quantised_cache(gpu, w, hkv, d)
+    out8 = prefill_attention_fp8(w.q, kc, vc, ks, vs, meta["block_table"],
+                                 meta["query_start_loc"], meta["context_lens"])
+    kb = from_u16(_dequant_bf16(kc.cpu().numpy(), ks.cpu().numpy(), hkv), gpu)
+    vb = from_u16(_dequant_bf16(vc.cpu().numpy(), vs.cpu().numpy(), hkv), gpu)
+    out16 = prefill_attention(w.q, kb, vb, meta["block_table"], meta["query_start_loc"],
+                              meta["context_lens"])
+    torch.cuda.synchronize()
+    assert torch.equal(out8, out16)
+    want = oracle.prefill_fp8(u16(w.q), kc.cpu().numpy(), vc.cpu().numpy(), ks.cpu().numpy(),
+                              vs.cpu().numpy(), w.block_table, w.query_start_loc, w.context_lens)
+    assert_attn_close(f32(out8), want, "fp8 prefill vs oracle")
+
+
+def test_prefill_fp8_mixed_batch_with_side_stream_decode_items(gpu):
+    from ccinfer_amd import prefill_attention_fp8
+    say("fp8 prefill mixed batch")
+    w = W.mixed_step(device=gpu, n_chunks=2, chunk=128, n_decode=40, dec_hi=4096)
+    meta = w.device_meta(gpu)
+    kc, vc, ks, vs = quantised_cache(gpu, w, w.hkv, w.d)
+    out = prefill_attention_fp8(w.q, kc, vc, ks, vs, meta["block_table"],
+                                meta["query_start_loc"], meta["context_lens"])
+    torch.cuda.synchronize()
+    want = oracle.prefill_fp8(u16(w.q), kc.cpu().numpy(), vc.cpu().numpy(), ks.cpu().numpy(),
+                              vs.cpu().numpy(), w.block_table, w.query_start_loc, w.context_lens)
+    assert_attn_close(f32(out), want, "fp8 mixed")
+    # the decode items equal the fp8 decode operator on the same rows
+    nc = 2
+    rows = torch.from_numpy(w.query_start_loc[nc:-1].astype(np.int64)).to(gpu)
+    dec = decode_attention_fp8(w.q[rows].contiguous(), kc, vc, ks, vs,
+                               meta["block_table"][nc:].contiguous(),
+                               meta["context_lens"][nc:].contiguous())
+    assert_attn_close(f32(out)[w.query_start_loc[nc:-1]], f32(dec), "fp8 mixed decode items")
