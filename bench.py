@@ -11,7 +11,7 @@ The other configurations are reported under "configs"; "6" is the fused decode p
 (split QKV + q/k RMSNorm + RoPE + KV write in one launch), in algorithmic bytes per second;
 "7" is the per-step batch metadata built on the device, beside the reference's host path;
 "8" is decode over an fp8 (E4M3, per-row scale) cache, in bytes actually read and in the
-bf16 bytes the same attention covers. rank 0 prints ONE JSON line.
+bf16 bytes the same attention covers, and the configs[2] prefill over an fp8 cache. rank 0 prints ONE JSON line.
 
 Timing: about 0.2 s of untimed repetitions (clock settle) and W untimed warm-up steps, then
 exactly K steps bracketed by device synchronisation; CPU baselines run after all GPU timings;
@@ -400,9 +400,7 @@ def run(args):
         # fp8 KV cache: the configs[1] and configs[4] batches with their caches quantised by
         # the fp8 write kernel; bytes = K+V bytes plus the row scales actually read
         lib = _lib.load()
-        for key, make in (("8_fp8_decode_b64_ctx128-4096", W.decode_batched),
-                          ("8_fp8_decode_b32_ctx32768_gqa4", W.decode_long)):
-            w = make(device=dev)
+        def quantise(w):
             slots = w.k_cache.shape[0]
             kc = torch.empty((slots, w.hkv, w.d), dtype=torch.uint8, device=dev)
             vc = torch.empty_like(kc)
@@ -415,6 +413,12 @@ def run(args):
                 ks.data_ptr(), vs.data_ptr(), ident.data_ptr(), slots, w.hkv, w.d, slots,
                 stream.cuda_stream)
             assert rc == 0, rc
+            return kc, vc, ks, vs
+
+        for key, make in (("8_fp8_decode_b64_ctx128-4096", W.decode_batched),
+                          ("8_fp8_decode_b32_ctx32768_gqa4", W.decode_long)):
+            w = make(device=dev)
+            kc, vc, ks, vs = quantise(w)
             meta = w.device_meta(dev)
             outp = torch.empty_like(w.q)
             n = lib.ccinfer_decode_workspace_size(w.batch, w.mbpr, w.hq, w.hkv, w.d, 16)
@@ -436,6 +440,30 @@ def run(args):
             r["hbm_frac"] = r["GBps"] * 1e9 / HBM_PEAK
             out[key] = r
             del w, kc, vc, ks, vs
+
+        # prefill over the fp8 cache: the configs[2] batch (same FLOPs as "3")
+        w = W.prefill_prefix(device=dev)
+        kc, vc, ks, vs = quantise(w)
+        meta = w.device_meta(dev)
+        outp = torch.empty_like(w.q)
+        T = w.q.shape[0]
+        n = lib.ccinfer_prefill_workspace_size(w.batch, T, w.mbpr, w.hq, w.hkv, w.d, 16)
+        ws = torch.zeros(max(1, n), dtype=torch.uint8, device=dev)
+
+        def pre8():
+            rc = lib.ccinfer_prefill_attention_fp8(
+                w.q.data_ptr(), kc.data_ptr(), vc.data_ptr(), ks.data_ptr(), vs.data_ptr(),
+                meta["block_table"].data_ptr(), meta["query_start_loc"].data_ptr(),
+                meta["context_lens"].data_ptr(), outp.data_ptr(), w.batch, T, w.mbpr, w.hq,
+                w.hkv, w.d, 16, ws.data_ptr(), n, stream.cuda_stream)
+            assert rc == 0, rc
+        ms, host_ms = time_loop(pre8, args.steps, args.warmup, stream)
+        flops = W.prefill_flops(w)
+        r = {"ms_per_step": ms, "host_ms_per_step": host_ms, "flops": flops,
+             "TFLOPs": flops / (ms * 1e-3) / 1e12}
+        r["mfma_frac"] = r["TFLOPs"] * 1e12 / BF16_PEAK
+        out["8_fp8_prefill_8x(512+1536)"] = r
+        del w, kc, vc, ks, vs
 
     torch.cuda.synchronize()
     if not args.no_cpu:
