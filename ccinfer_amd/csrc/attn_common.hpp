@@ -14,6 +14,7 @@ namespace ccinfer::hipk {
 
 using bf16x8 = __bf16 __attribute__((ext_vector_type(8)));
 using f32x4 = float __attribute__((ext_vector_type(4)));
+using f32x16 = float __attribute__((ext_vector_type(16)));
 using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
 using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
 
@@ -73,6 +74,13 @@ __device__ __forceinline__ float wave_max_swap16_32(float v) {
     return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
+// Max over lanes l and l^32 (one permlane32_swap).
+__device__ __forceinline__ float wave_max_swap32(float v) {
+    const uint32_t u = __float_as_uint(v);
+    const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+}
+
 __device__ __forceinline__ float wave_sum_xor16_32(float v) {
     v += __shfl_xor(v, 16);
     v += __shfl_xor(v, 32);
@@ -81,6 +89,11 @@ __device__ __forceinline__ float wave_sum_xor16_32(float v) {
 
 __device__ __forceinline__ f32x4 mfma16x16x32(const bf16x8& a, const bf16x8& b, const f32x4& c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 mfma32x32x16(const bf16x8& a, const bf16x8& b,
+                                               const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
 // Two OCP E4M3 bytes (the low or high half of `w`) -> a bf16 pair; exact (every E4M3

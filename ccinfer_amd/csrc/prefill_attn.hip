@@ -188,13 +188,19 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(
 // over any 16 consecutive rows, so the K operand read (16 rows, one logical chunk) hits 16
 // distinct chunk positions, and for any 4 rows 4g..4g+3 and chunk pair {2n, 2n+1} -- one
 // transposing V read -- the 8 (row, chunk) pieces land on 8 distinct positions.
-__device__ __forceinline__ int chunk_swizzle(int row) { return row & 15; }
+template <int D>
+__device__ __forceinline__ int chunk_swizzle(int row) {
+    if constexpr (D == 128)
+        return 4 * (row & 3) + 2 * ((row >> 2) & 1) + ((row >> 3) & 1);
+    else
+        return row & 15;
+}
 
 template <int D>
 __device__ __forceinline__ int lds_off(int row, int chunk) {
     // Element offset of logical 16-byte chunk `chunk` of key row `row`.
     constexpr int kMask = PrefillShape<D>::kCPR - 1;
-    return row * D + ((chunk ^ (chunk_swizzle(row) & kMask)) << 3);
+    return row * D + ((chunk ^ (chunk_swizzle<D>(row) & kMask)) << 3);
 }
 
 // Direct global->LDS staging of one 64-key K/V tile (gfx950 global_load_lds_dwordx4): an
@@ -218,7 +224,7 @@ __device__ __forceinline__ void stage_issue(__bf16* lk, __bf16* lv, uint8_t* lva
         const int slot0 = (x * kWaves + wave) * 64;  // first 16-byte LDS slot of this load
         const int p = slot0 + lane;
         const int row = p / CPR;
-        const int lchunk = (p % CPR) ^ (chunk_swizzle(row) & (CPR - 1));
+        const int lchunk = (p % CPR) ^ (chunk_swizzle<D>(row) & (CPR - 1));
         const int key = key_base + row;
         const int lb = key >> 4;
         int pb = -1;
@@ -550,23 +556,26 @@ __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
 //
 // One workgroup = 8 wavefronts (two per SIMD, <= 256 VGPRs each); each wavefront owns 32
 // query rows of one q-head and the workgroup covers the Hq/Hkv heads that share a KV head,
-// so every K/V tile staged in LDS feeds all of them. Work advances in 32-key halves through
-// a software pipeline so that each wavefront always has independent MFMA and VALU work:
-//     X_i: P_i = exp2(S_i * scale - m)           ||  S_{i+1} = K_{i+1} . Q^T
-//     Y_i: O  += V_i^T . P_i^T                   ||  mask + row max of S_{i+1}
-// with the instruction interleave pinned by sched_group_barrier. K/V tiles are
+// so every K/V tile staged in LDS feeds all of them. The matrix work uses the 32x32x16 bf16
+// MFMA: per 32-key half, S^T = K . Q^T is one 32x32 accumulator (keys x query rows) and
+// O^T += V^T . P^T runs over D/32 dim tiles x 2 key steps. Per MFMA the 32x32x16 shape
+// leaves twice the VALU issue room of the 16x16x32 one, which the softmax needs. Work
+// advances in 32-key halves through a software pipeline so that each wavefront always has
+// independent MFMA and VALU work:
+//     X_i: P_i (first key step) = exp2(S_i * scale - m)  ||  S_{i+1} = K_{i+1} . Q^T
+//     Y_i: O += V_i^T . P_i^T, with the second key step's exp beside the first PV MFMAs
+//                                                         ||  row max of S_{i+1}
+// with the instruction interleave pinned by sched_group_barrier. Masked halves seed the
+// S accumulator with 0 / -inf instead of masking the scores afterwards. K/V tiles are
 // triple-buffered in LDS: at the barrier in the middle of tile t every wavefront has
 // finished tile t-1 and tile t+1 has landed, so tile t+2 streams into the freed buffer
 // while tiles t and t+1 are read.
 // ---------------------------------------------------------------------------
 template <int D, int QT>
 struct PipeShape {
-    static constexpr int kQT = QT;
     static constexpr int kRows = 16 * QT;                // query rows per wavefront
     static constexpr int kWaves = 8;
     static constexpr int kThreads = 64 * kWaves;
-    static constexpr int kSteps = D / 32;                // QK k-steps
-    static constexpr int kNT = D / 16;                   // PV dim tiles
     static constexpr int kCPR = D / 8;                   // 16-byte chunks per K/V row
     static constexpr int kLoads = kKeysPerTile * kCPR / kThreads;  // per K or V
     static_assert(kKeysPerTile * kCPR % kThreads == 0, "staging must split evenly");
@@ -590,9 +599,8 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
                          const int32_t* __restrict__ counts, const TileEntry* __restrict__ tiles,
                          int total_tokens, int mbpr, int hq, int hkv, float scale_log2) {
     using Sh = PipeShape<D, QTT>;
-    constexpr int QT = Sh::kQT;
-    constexpr int S = Sh::kSteps;
-    constexpr int NT = Sh::kNT;
+    constexpr int S2 = D / 16;   // QK k-steps (32x32x16 MFMA)
+    constexpr int NT2 = D / 32;  // PV dim tiles
     constexpr int CPR = Sh::kCPR;
     constexpr int NL = Sh::kLoads;
     constexpr int kPipeWaves = Sh::kWaves;
@@ -652,8 +660,6 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
     const int head_local = wave / WPH;
     const int tw = t0 + (wave % WPH) * kPipeRows;
     const int q_head = kvh * G + hg * HPW + head_local;
-    const int j = lane & 15;
-    const int g = lane >> 4;
     const int32_t* req_blocks = block_table + static_cast<int64_t>(req) * mbpr;
 
     // Block-table slice in LDS: entries for every block the tiles touch, -1 past the
@@ -703,27 +709,32 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
     for (int x = 0; x < NL; ++x) {
         const int p = (x * kPipeWaves + wave) * 64 + lane;
         const int row = p / CPR;
-        const int lch = (p % CPR) ^ (chunk_swizzle(row) & (CPR - 1));
+        const int lch = (p % CPR) ^ (chunk_swizzle<D>(row) & (CPR - 1));
         st_row[x] = row;
         st_off[x] = static_cast<uint32_t>((((row & (kBlock - 1)) * hkv + kvh) * D + lch * 8) * 2);
     }
     const int64_t blk_bytes = static_cast<int64_t>(kBlock) * hkv * D * 2;
 
-    // Per-lane LDS read offsets (elements). Rows 16 apart share a swizzle, so one offset per
-    // k-step (K reads: row j, chunk 4kk+g) and per dim tile (transposing V reads: rows
-    // 4g + s/4, chunk 2n + (s/2)%2) serves every half, 16-row block and buffer; the rest is
-    // a constant the compiler folds into the instruction.
-    int koff[S];
+    // Per-lane LDS read offsets (elements); lane l = 32 h + c (c = l % 32, h = l / 32).
+    // K operand of k-step kk: key row c, logical chunk 2 kk + h. Rows 16 apart share a
+    // swizzle, so one offset per k-step serves both 32-key halves and every buffer.
+    // V^T operand of dim tile n, k-step s: two transposing reads, of key rows
+    // 16 s + 4 h + (c%16)/4 and 8 rows further, dims 32 n + 16 (c/16) + 4 (c%4) .. +3 (the
+    // 16-lane group's 4 x 16 block, transposed so lane c receives one dim for 4 keys).
+    const int c32 = lane & 31;
+    const int h32 = lane >> 5;
+    int koff[S2];
 #pragma unroll
-    for (int kk = 0; kk < S; ++kk) koff[kk] = lds_off<D>(j, kk * 4 + g);
-    int voff[NT];
+    for (int kk = 0; kk < S2; ++kk) koff[kk] = lds_off<D>(c32, kk * 2 + h32);
+    int voffa[NT2], voffb[NT2];
     {
         const int s16 = lane & 15;
-        const int row0 = 4 * g + (s16 >> 2);
+        const int row0 = 4 * h32 + (s16 >> 2);
 #pragma unroll
-        for (int n = 0; n < NT; ++n) {
-            const int dim = 16 * n + 4 * (s16 & 3);
-            voff[n] = lds_off<D>(row0, dim >> 3) + (dim & 7);
+        for (int n = 0; n < NT2; ++n) {
+            const int dim = 32 * n + 16 * ((lane >> 4) & 1) + 4 * (s16 & 3);
+            voffa[n] = lds_off<D>(row0, dim >> 3) + (dim & 7);
+            voffb[n] = lds_off<D>(row0 + 8, dim >> 3) + (dim & 7);
         }
     }
 
@@ -743,6 +754,9 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
                 const int64_t boff = static_cast<int64_t>(pb) * blk_bytes;
                 const char* kb = reinterpret_cast<const char*>(k_cache) + boff;
                 const char* vb = reinterpret_cast<const char*>(v_cache) + boff;
+                // Opaque scalar bases: keeps the address as SGPR base + 32-bit lane offset
+                // (otherwise the compiler hoists 64-bit per-lane sums out of the loop).
+                asm("" : "+s"(kb), "+s"(vb));
                 if (in_range) {
                     __builtin_amdgcn_global_load_lds(
                         (void*)(kb + st_off[x]),  // a char* argument makes clang drop the
@@ -831,158 +845,144 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
     };
     float sk8[2] = {0.f, 0.f}, sv8[2] = {0.f, 0.f};  // scales of the tiles staged in ring slot
 
-    // Q^T operands: lane (query j, grp g) holds dims (kk*4+g)*8.. of row tw + qt*16 + j.
-    bf16x8 qop[QT][S];
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-        const int tq = tw + qt * 16 + j;
+    // Q^T operands: lane (c, h) holds dims 16 kk + 8 h .. +8 of query row tw + c.
+    bf16x8 qop[S2];
+    {
+        const int tq = tw + c32;
         const bool live = tq < rows;
         const __bf16* qv = q + (static_cast<int64_t>(qb + (live ? tq : 0)) * hq + q_head) * D;
 #pragma unroll
-        for (int kk = 0; kk < S; ++kk) {
-            u32x4 w = load16(qv + (kk * 4 + g) * 8);
+        for (int kk = 0; kk < S2; ++kk) {
+            u32x4 w = load16(qv + kk * 16 + h32 * 8);
             if (!live) w = u32x4{0, 0, 0, 0};
-            qop[qt][kk] = __builtin_bit_cast(bf16x8, w);
+            qop[kk] = __builtin_bit_cast(bf16x8, w);
         }
     }
     __syncthreads();  // block table staged
     const bool holes = s_holes != 0 || nblk_vis > mbpr;
 
-    f32x4 acc[QT][NT];
-    f32x4 lsum[QT];
-    float m[QT];
-    int limit[QT];  // last key visible to query row tw + 16 qt + j
-    const bf16x8 ones = __builtin_bit_cast(
-        bf16x8, u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
+    // O^T: lane (c, h), element v of dim tile n holds dim 32 n + 8 (v/4) + 4 h + v%4 of
+    // query row tw + c. lsum: this lane's share of the row sum of query row tw + c (the
+    // bf16 probabilities it holds); lanes c and c + 32 together hold the whole sum.
+    f32x16 acc[NT2];
+    float lsum = 0.f;
+    // A finite "no key yet" reference: exp2(s - m) needs no -inf guard, the first half with
+    // a visible key always outgrows it (rescale with alpha = 0), and fully masked scores
+    // (-inf) still give probability 0.
+    float m = kMaxInit;
+    const int limit = prefix + tw + c32;  // last key visible to query row tw + c
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-        // A finite "no key yet" reference: exp2(s - m) needs no -inf guard, the first half
-        // with a visible key always outgrows it (rescale with alpha = 0), and fully masked
-        // scores (-inf) still give probability 0.
-        m[qt] = kMaxInit;
-        lsum[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        limit[qt] = prefix + tw + qt * 16 + j;
+    for (int n = 0; n < NT2; ++n)
 #pragma unroll
-        for (int n = 0; n < NT; ++n) acc[qt][n] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+        for (int v = 0; v < 16; ++v) acc[n][v] = 0.f;
 
-    // ---- pipeline pieces (h = 32-key half of a 64-key tile) ----
-    // S^T of one half: st[kbl][qt] lane (j, g) holds keys 32h + 16 kbl + 4g + r.
-    auto qk_half = [&](const __bf16* lk, int h, f32x4 (&st)[2][QT])
+    // ---- pipeline pieces (hh = 32-key half of a 64-key tile) ----
+    // S^T of one half: lane (c, h), element v holds key 8 (v/4) + 4 h + v%4 of the half.
+    // The accumulator starts at 0, or, for a masked half, at the seed mask_seed wrote
+    // (0 where visible, -inf where masked: -inf + finite products stays -inf).
+    auto qk_half = [&](const __bf16* lk, int hh, f32x16& st, auto seeded_tag)
                        __attribute__((always_inline)) {
+        if constexpr (!decltype(seeded_tag)::value) {
 #pragma unroll
-        for (int kbl = 0; kbl < 2; ++kbl) {
+            for (int v = 0; v < 16; ++v) st[v] = 0.f;
+        }
 #pragma unroll
-            for (int qt = 0; qt < QT; ++qt) st[kbl][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int kk = 0; kk < S; ++kk) {
-                const bf16x8 kop = __builtin_bit_cast(
-                    bf16x8, *reinterpret_cast<const u32x4*>(lk + (h * 32 + kbl * 16) * D +
-                                                            koff[kk]));
-#pragma unroll
-                for (int qt = 0; qt < QT; ++qt)
-                    st[kbl][qt] = mfma16x16x32(kop, qop[qt][kk], st[kbl][qt]);
-            }
+        for (int kk = 0; kk < S2; ++kk) {
+            const bf16x8 kop = __builtin_bit_cast(
+                bf16x8, *reinterpret_cast<const u32x4*>(lk + hh * 32 * D + koff[kk]));
+            st = mfma32x32x16(kop, qop[kk], st);
         }
     };
-    // Causal / validity mask of one half; key0 = first key of the half, vbits = validity
-    // of its 32 keys.
-    auto mask_half = [&](f32x4 (&st)[2][QT], int key0, uint32_t vbits)
+    // Mask seed of one half (key0 = its first key): 0 for visible keys, -inf for keys past
+    // the row's causal limit and, with kBits, for keys whose validity bit is clear (only
+    // needed when the table has holes: otherwise every key past kv_end is past every row's
+    // limit too).
+    auto mask_seed = [&](f32x16& st, int key0, uint32_t vbits, auto bits_tag)
                          __attribute__((always_inline)) {
+        constexpr bool kBits = decltype(bits_tag)::value;
+        const int thr = limit - key0 - 4 * h32;
+        const uint32_t vb = kBits ? (vbits >> (4 * h32)) : 0u;
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt) {
-#pragma unroll
-            for (int kbl = 0; kbl < 2; ++kbl) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int kt = kbl * 16 + g * 4 + r;
-                    const bool ok = key0 + kt <= limit[qt] && ((vbits >> kt) & 1u);
-                    st[kbl][qt][r] = ok ? st[kbl][qt][r] : kNegInf;
-                }
-            }
+        for (int v = 0; v < 16; ++v) {
+            const int kt = 8 * (v >> 2) + (v & 3);
+            bool ok = kt <= thr;
+            if constexpr (kBits) ok = ok && ((vb >> kt) & 1u);
+            st[v] = ok ? 0.f : kNegInf;
         }
     };
-    // Row max of one half (scaled, log2 units); returns whether any row outgrew the slack.
-    auto max_half = [&](const f32x4 (&st)[2][QT], float (&mt)[QT])
-                        __attribute__((always_inline)) {
-        bool grow = false;
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) {
-            float x = fmaxf(fmaxf(fmaxf(st[0][qt][0], st[0][qt][1]),
-                                  fmaxf(st[0][qt][2], st[0][qt][3])),
-                            fmaxf(fmaxf(st[1][qt][0], st[1][qt][1]),
-                                  fmaxf(st[1][qt][2], st[1][qt][3])));
-            x = wave_max_swap16_32(x) * scale_log2;
-            mt[qt] = x;
-            grow |= x > m[qt] + kRescaleSlack;
-        }
-        return grow;
+    // Row max of one half (scaled, log2 units); returns whether the row outgrew the slack.
+    auto max_half = [&](const f32x16& st, float& mt) __attribute__((always_inline)) {
+        float x0 = fmaxf(fmaxf(st[0], st[1]), st[2]);
+        float x1 = fmaxf(fmaxf(st[3], st[4]), st[5]);
+        float x2 = fmaxf(fmaxf(st[6], st[7]), st[8]);
+        float x3 = fmaxf(fmaxf(st[9], st[10]), st[11]);
+        float x4 = fmaxf(fmaxf(st[12], st[13]), st[14]);
+        float x = fmaxf(fmaxf(x0, x1), fmaxf(fmaxf(x2, x3), fmaxf(x4, st[15])));
+        x = wave_max_swap32(x) * scale_log2;
+        mt = x;
+        return x > m + kRescaleSlack;
     };
-    auto rescale = [&](bool grow, const float (&mt)[QT]) __attribute__((always_inline)) {
+    auto rescale = [&](bool grow, const float& mt) __attribute__((always_inline)) {
         if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+            const float m_new = fmaxf(m, mt);
+            const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+            lsum = lsum * alpha;
 #pragma unroll
-            for (int qt = 0; qt < QT; ++qt) {
-                const float m_new = fmaxf(m[qt], mt[qt]);
-                const float alpha = __builtin_amdgcn_exp2f(m[qt] - m_new);
-                lsum[qt] = lsum[qt] * alpha;
-#pragma unroll
-                for (int n = 0; n < NT; ++n) acc[qt][n] = acc[qt][n] * alpha;
-                m[qt] = m_new;
-            }
+            for (int n = 0; n < NT2; ++n) acc[n] = acc[n] * alpha;
+            m = m_new;
         }
     };
-    // P^T operands of one half (keys T(g, e) = 16(e/4) + 4g + e%4) and their row sums.
-    auto exp_half = [&](const f32x4 (&st)[2][QT], bf16x8 (&pop)[QT])
-                        __attribute__((always_inline)) {
+    // P^T operands of one half: pop[s] holds elements 8 s .. 8 s + 7 (keys 16 s + 8 (e/4) +
+    // 4 h + e%4, e = 0..7), the B operand of PV k-step s. The lane's share of the row sum
+    // adds the same bf16 probabilities (v_dot2 with ones on each packed pair).
+    auto exp_part = [&](const f32x16& st, int s, bf16x8& pops) __attribute__((always_inline)) {
+        using bf16x2 = __bf16 __attribute__((ext_vector_type(2)));
+        const bf16x2 one2 = __builtin_bit_cast(bf16x2, 0x3f803f80u);
+        const float mneg = -m;
+        u32x4 pw;
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt) {
-            const float mneg = -m[qt];
-            u32x4 pw;
-#pragma unroll
-            for (int x = 0; x < 4; ++x) {
-                const int e = 2 * x;
-                const float p0 = __builtin_amdgcn_exp2f(
-                    __builtin_fmaf(st[e >> 2][qt][e & 3], scale_log2, mneg));
-                const float p1 = __builtin_amdgcn_exp2f(
-                    __builtin_fmaf(st[(e + 1) >> 2][qt][(e + 1) & 3], scale_log2, mneg));
-                pw[x] = pack_bf16x2(p0, p1);
-            }
-            pop[qt] = __builtin_bit_cast(bf16x8, pw);
+        for (int x = 0; x < 4; ++x) {
+            const float p0 =
+                __builtin_amdgcn_exp2f(__builtin_fmaf(st[8 * s + 2 * x], scale_log2, mneg));
+            const float p1 =
+                __builtin_amdgcn_exp2f(__builtin_fmaf(st[8 * s + 2 * x + 1], scale_log2, mneg));
+            const uint32_t pk = pack_bf16x2(p0, p1);
+            lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk), one2, lsum,
+                                                   false);
+            pw[x] = pk;
         }
+        pops = __builtin_bit_cast(bf16x8, pw);
     };
-    auto sum_half = [&](const bf16x8 (&pop)[QT]) __attribute__((always_inline)) {
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) lsum[qt] = mfma16x16x32(ones, pop[qt], lsum[qt]);
-    };
-    auto pv_half = [&](const __bf16* lv, int h, const bf16x8 (&pop)[QT])
+    // V^T operand (A, 32 dims x 16 keys): lane (c, h) holds dim c of the tile for keys
+    // 16 s + 4 h + r (r < 4) and 16 s + 8 + 4 h + r, matching pop[s]'s key order.
+    auto pv_part = [&](const __bf16* lv, int hh, int s, const bf16x8& pops)
                        __attribute__((always_inline)) {
         using v4s = short __attribute__((ext_vector_type(4)));
         using v8s = short __attribute__((ext_vector_type(8)));
 #pragma unroll
-        for (int n = 0; n < NT; ++n) {
-            const __bf16* p0 = lv + h * 32 * D + voff[n];
+        for (int n = 0; n < NT2; ++n) {
+            const __bf16* base = lv + (hh * 32 + 16 * s) * D;
             const v4s a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (__attribute__((address_space(3))) v4s*)(p0));
+                (__attribute__((address_space(3))) v4s*)(base + voffa[n]));
             const v4s b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (__attribute__((address_space(3))) v4s*)(p0 + 16 * D));
+                (__attribute__((address_space(3))) v4s*)(base + voffb[n]));
             const v8s ab = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-            const bf16x8 vop = __builtin_bit_cast(bf16x8, ab);
-#pragma unroll
-            for (int qt = 0; qt < QT; ++qt) acc[qt][n] = mfma16x16x32(vop, pop[qt], acc[qt][n]);
+            acc[n] = mfma32x32x16(__builtin_bit_cast(bf16x8, ab), pops, acc[n]);
         }
     };
-    auto vbits_of = [&](const uint8_t* lvalid, int h) __attribute__((always_inline)) {
+    auto vbits_of = [&](const uint8_t* lvalid, int hh) __attribute__((always_inline)) {
         const uint64_t v = __builtin_amdgcn_ballot_w64(lvalid[lane] != 0);
-        return static_cast<uint32_t>(v >> (32 * h));
+        return static_cast<uint32_t>(v >> (32 * hh));
     };
 
     // Interleave patterns for the two pipeline phases (igrouplp masks: 0x8 MFMA, 0x100 DS
-    // read, 0x402 VALU incl. transcendental). X: 2 MFMAs of the next half's QK per K read,
-    // with the exp work of the current half spread between them. Y: one V^T operand (two
-    // transposing reads) per QT MFMAs, with the next half's mask / max work in between.
-    constexpr int kXGroups = 2 * S;            // K operand reads in a QK half
-    constexpr int kXValu = (QT * 20 + kXGroups - 1) / kXGroups;
-    constexpr int kYValu = (QT * 16 + NT - 1) / NT;
+    // read, 0x402 VALU incl. transcendental). X: one QK MFMA per K read, with the exp work
+    // of the current half spread between them. Y: one PV MFMA per V^T operand (two
+    // transposing reads), with the next half's mask / max work in between.
+    constexpr int kXGroups = S2;
+    constexpr int kXValu = 3;
+    constexpr int kYValuA = 6;  // exp of the second P operand beside PV k-step 0
+    constexpr int kYValuB = 3;  // next half's row max beside PV k-step 1
     constexpr int kXPre = 2;  // K operand reads issued ahead of the MFMAs using them
     constexpr int kYPre = 2;  // V^T operands read ahead
     auto interleave_x = [&]() __attribute__((always_inline)) {
@@ -990,180 +990,201 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
 #pragma unroll
         for (int i = 0; i < kXGroups; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x402, kXValu, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, QT, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             if (i + kXPre < kXGroups) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
     };
     auto interleave_y = [&]() __attribute__((always_inline)) {
         __builtin_amdgcn_sched_group_barrier(0x100, 2 * kYPre, 0);
 #pragma unroll
-        for (int i = 0; i < NT; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x402, kYValu, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, QT, 0);
-            if (i + kYPre < NT) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        for (int i = 0; i < 2 * NT2; ++i) {
+            if (i < NT2)
+                __builtin_amdgcn_sched_group_barrier(0x402, kYValuA, 0);
+            else
+                __builtin_amdgcn_sched_group_barrier(0x402, kYValuB, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (i + kYPre < 2 * NT2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
         }
     };
 
-    f32x4 sc[2][QT];  // S of the half being exponentiated
-    f32x4 sn[2][QT];  // S of the next half
-    bf16x8 pop[QT];
-    float mt[QT];
-
-    // Prologue: tiles 0 and 1 in flight, S of tile 0 / half 0 formed, masked and maxed.
-    if constexpr (F8) {
-        stage8(0, lds_k8_0, lds_v8_0, lds_valid0, sk8[0], sv8[0]);
-        if (ntiles > 1) stage8(1, lds_k8_1, lds_v8_1, lds_valid1, sk8[1], sv8[1]);
-        __builtin_amdgcn_s_waitcnt(0x0F70);
-        __syncthreads();
-        convert8(lds_k8_0, lds_v8_0, lds_k0, lds_v0, sk8[0], sv8[0]);
-    } else {
-        stage(0, lds_k0, lds_v0, lds_valid0);
-        if (ntiles > 1) {
-            stage(1, lds_k1, lds_v1, lds_valid1);
-            __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * NL));  // tile 0 landed (vmcnt <= tile 1's)
-        } else {
+    f32x16 sc;  // S of the half being exponentiated
+    f32x16 sn;  // S of the next half
+    bf16x8 pop[2];
+    float mt;
+    // The tile loop, compiled twice: with the per-key validity bits (tables with holes) and
+    // without; each workgroup runs one of them.
+    auto run = [&](auto holes_tag) __attribute__((always_inline)) {
+        // Prologue: tiles 0 and 1 in flight, S of tile 0 / half 0 formed, masked and maxed.
+        if constexpr (F8) {
+            stage8(0, lds_k8_0, lds_v8_0, lds_valid0, sk8[0], sv8[0]);
+            if (ntiles > 1) stage8(1, lds_k8_1, lds_v8_1, lds_valid1, sk8[1], sv8[1]);
             __builtin_amdgcn_s_waitcnt(0x0F70);
-        }
-    }
-    __syncthreads();
-    qk_half(lds_k0, 0, sc);
-    mask_half(sc, 0, vbits_of(lds_valid0, 0));
-    rescale(max_half(sc, mt), mt);
-
-    // One tile step. Entering: sc = S of (tile t, half 0), already masked and rescaled for.
-    // kLast: tile t is the last one (no next tile to start).
-    auto step = [&](int t, auto cur, auto nxt, auto ld, auto mask_tag, auto last_tag)
-                    __attribute__((always_inline)) {
-        constexpr int BC = decltype(cur)::value;
-        constexpr int BN = decltype(nxt)::value;
-        constexpr int BL = decltype(ld)::value;
-        constexpr bool kMask = decltype(mask_tag)::value;
-        constexpr bool kLast = decltype(last_tag)::value;
-        static_assert(!F8 || (BC < 2 && BN < 2 && BL < 2), "fp8 runs a two-tile ring");
-        const __bf16* kc = BC == 0 ? lds_k0 : (BC == 1 ? lds_k1 : lds_k2);
-        const __bf16* vc = BC == 0 ? lds_v0 : (BC == 1 ? lds_v1 : lds_v2);
-        const uint8_t* valc = BC == 0 ? lds_valid0 : (BC == 1 ? lds_valid1 : lds_valid2);
-        const __bf16* kn = BN == 0 ? lds_k0 : (BN == 1 ? lds_k1 : lds_k2);
-        const uint8_t* valn = BN == 0 ? lds_valid0 : (BN == 1 ? lds_valid1 : lds_valid2);
-        __bf16* kl = BL == 0 ? lds_k0 : (BL == 1 ? lds_k1 : lds_k2);
-        __bf16* vl = BL == 0 ? lds_v0 : (BL == 1 ? lds_v1 : lds_v2);
-        uint8_t* vall = BL == 0 ? lds_valid0 : (BL == 1 ? lds_valid1 : lds_valid2);
-        const int key0 = t * kKeysPerTile;
-
-        // X: exp of (t, 0) || QK of (t, 1)
-        __builtin_amdgcn_sched_barrier(0);
-        exp_half(sc, pop);
-        qk_half(kc, 1, sn);
-        sum_half(pop);
-        interleave_x();
-        // Y: PV of (t, 0) || mask + max of (t, 1)
-        __builtin_amdgcn_sched_barrier(0);
-        pv_half(vc, 0, pop);
-        if constexpr (kMask) mask_half(sn, key0 + 32, vbits_of(valc, 1));
-        const bool grow1 = max_half(sn, mt);
-        interleave_y();
-        __builtin_amdgcn_sched_barrier(0);
-        rescale(grow1, mt);
-        if constexpr (!kLast) {
-            __builtin_amdgcn_s_waitcnt(0x0F70);  // this wavefront's loads of tile t+1 landed
-            __syncthreads();                     // ... and everyone's; tile t-1 is free
-            if constexpr (F8) {
-                // tile t+1: bytes (ring slot BN) -> bf16 (slot BN, which held tile t-1);
-                // then tile t+2's bytes go to slot BL (= BC, converted one step ago)
-                convert8(BN == 0 ? lds_k8_0 : lds_k8_1, BN == 0 ? lds_v8_0 : lds_v8_1,
-                         BN == 0 ? lds_k0 : lds_k1, BN == 0 ? lds_v0 : lds_v1, sk8[BN], sv8[BN]);
-                __syncthreads();
-                if (t + 2 < ntiles)
-                    stage8(t + 2, BL == 0 ? lds_k8_0 : lds_k8_1, BL == 0 ? lds_v8_0 : lds_v8_1,
-                           vall, sk8[BL], sv8[BL]);
+            __syncthreads();
+            convert8(lds_k8_0, lds_v8_0, lds_k0, lds_v0, sk8[0], sv8[0]);
+        } else {
+            stage(0, lds_k0, lds_v0, lds_valid0);
+            if (ntiles > 1) {
+                stage(1, lds_k1, lds_v1, lds_valid1);
+                __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * NL));  // tile 0 landed (vmcnt <= tile 1's)
             } else {
-                if (t + 2 < ntiles) stage(t + 2, kl, vl, vall);
+                __builtin_amdgcn_s_waitcnt(0x0F70);
             }
         }
-        // X: exp of (t, 1) || QK of (t+1, 0)
-        __builtin_amdgcn_sched_barrier(0);
-        exp_half(sn, pop);
-        if constexpr (!kLast) qk_half(kn, 0, sc);
-        sum_half(pop);
-        if constexpr (!kLast) interleave_x();
-        // Y: PV of (t, 1) || mask + max of (t+1, 0)
-        __builtin_amdgcn_sched_barrier(0);
-        pv_half(vc, 1, pop);
-        if constexpr (!kLast) {
-            if constexpr (kMask) mask_half(sc, key0 + kKeysPerTile, vbits_of(valn, 0));
-            const bool grow0 = max_half(sc, mt);
+        __syncthreads();
+        mask_seed(sc, 0, vbits_of(lds_valid0, 0), holes_tag);
+        qk_half(lds_k0, 0, sc, std::true_type{});
+        const bool grow_first = max_half(sc, mt);
+        rescale(grow_first, mt);
+
+        // One tile step. Entering: sc = S of (tile t, half 0), already masked and rescaled for.
+        // kLast: tile t is the last one (no next tile to start).
+        auto step = [&](int t, auto cur, auto nxt, auto ld, auto mask_tag, auto last_tag)
+                        __attribute__((always_inline)) {
+            constexpr int BC = decltype(cur)::value;
+            constexpr int BN = decltype(nxt)::value;
+            constexpr int BL = decltype(ld)::value;
+            constexpr bool kMask = decltype(mask_tag)::value;
+            constexpr bool kLast = decltype(last_tag)::value;
+            static_assert(!F8 || (BC < 2 && BN < 2 && BL < 2), "fp8 runs a two-tile ring");
+            const __bf16* kc = BC == 0 ? lds_k0 : (BC == 1 ? lds_k1 : lds_k2);
+            const __bf16* vc = BC == 0 ? lds_v0 : (BC == 1 ? lds_v1 : lds_v2);
+            const uint8_t* valc = BC == 0 ? lds_valid0 : (BC == 1 ? lds_valid1 : lds_valid2);
+            const __bf16* kn = BN == 0 ? lds_k0 : (BN == 1 ? lds_k1 : lds_k2);
+            const uint8_t* valn = BN == 0 ? lds_valid0 : (BN == 1 ? lds_valid1 : lds_valid2);
+            __bf16* kl = BL == 0 ? lds_k0 : (BL == 1 ? lds_k1 : lds_k2);
+            __bf16* vl = BL == 0 ? lds_v0 : (BL == 1 ? lds_v1 : lds_v2);
+            uint8_t* vall = BL == 0 ? lds_valid0 : (BL == 1 ? lds_valid1 : lds_valid2);
+            const int key0 = t * kKeysPerTile;
+
+            // X: exp of (t, 0) || QK of (t, 1)
+            __builtin_amdgcn_sched_barrier(0);
+            exp_part(sc, 0, pop[0]);
+            if constexpr (kMask) mask_seed(sn, key0 + 32, vbits_of(valc, 1), holes_tag);
+            qk_half(kc, 1, sn, mask_tag);
+            interleave_x();
+            // Y: PV of (t, 0), exp of its second P operand || max of (t, 1)
+            __builtin_amdgcn_sched_barrier(0);
+            pv_part(vc, 0, 0, pop[0]);
+            exp_part(sc, 1, pop[1]);
+            pv_part(vc, 0, 1, pop[1]);
+            const bool grow1 = max_half(sn, mt);
             interleave_y();
             __builtin_amdgcn_sched_barrier(0);
-            rescale(grow0, mt);
-        }
-    };
-    using B0 = std::integral_constant<int, 0>;
-    using B1 = std::integral_constant<int, 1>;
-    using B2 = std::integral_constant<int, 2>;
-    using F = std::false_type;
-    using T = std::true_type;
+            rescale(grow1, mt);
+            if constexpr (!kLast) {
+                __builtin_amdgcn_s_waitcnt(0x0F70);  // this wavefront's loads of tile t+1 landed
+                __syncthreads();                     // ... and everyone's; tile t-1 is free
+                if constexpr (F8) {
+                    // tile t+1: bytes (ring slot BN) -> bf16 (slot BN, which held tile t-1);
+                    // then tile t+2's bytes go to slot BL (= BC, converted one step ago)
+                    convert8(BN == 0 ? lds_k8_0 : lds_k8_1, BN == 0 ? lds_v8_0 : lds_v8_1,
+                             BN == 0 ? lds_k0 : lds_k1, BN == 0 ? lds_v0 : lds_v1, sk8[BN], sv8[BN]);
+                    __syncthreads();
+                    if (t + 2 < ntiles)
+                        stage8(t + 2, BL == 0 ? lds_k8_0 : lds_k8_1, BL == 0 ? lds_v8_0 : lds_v8_1,
+                               vall, sk8[BL], sv8[BL]);
+                } else {
+                    if (t + 2 < ntiles) stage(t + 2, kl, vl, vall);
+                }
+            }
+            // X: exp of (t, 1) || QK of (t+1, 0)
+            __builtin_amdgcn_sched_barrier(0);
+            exp_part(sn, 0, pop[0]);
+            if constexpr (!kLast) {
+                if constexpr (kMask)
+                    mask_seed(sc, key0 + kKeysPerTile, vbits_of(valn, 0), holes_tag);
+                qk_half(kn, 0, sc, mask_tag);
+            }
+            if constexpr (!kLast) interleave_x();
+            // Y: PV of (t, 1), exp of its second P operand || max of (t+1, 0)
+            __builtin_amdgcn_sched_barrier(0);
+            pv_part(vc, 1, 0, pop[0]);
+            exp_part(sn, 1, pop[1]);
+            pv_part(vc, 1, 1, pop[1]);
+            if constexpr (!kLast) {
+                const bool grow0 = max_half(sc, mt);
+                interleave_y();
+                __builtin_amdgcn_sched_barrier(0);
+                rescale(grow0, mt);
+            }
+        };
+        using B0 = std::integral_constant<int, 0>;
+        using B1 = std::integral_constant<int, 1>;
+        using B2 = std::integral_constant<int, 2>;
+        using F = std::false_type;
+        using T = std::true_type;
 
-    // Steps whose tiles t and t+1 lie wholly below the workgroup's first query row need no
-    // mask (unless the table has holes); they run in triples so buffer roles stay static.
-    const int mask_free_tiles = holes ? 0 : (prefix + t0 + 1) / kKeysPerTile;
-    const int mf_steps = max(0, min(ntiles - 1, mask_free_tiles - 1));
-    int t = 0;
-    if constexpr (F8) {
-        // two-tile ring: tile t in slot t % 2; the stage target of step t is slot t % 2 too
-        for (; t + 2 <= mf_steps; t += 2) {
-            step(t, B0{}, B1{}, B0{}, F{}, F{});
-            step(t + 1, B1{}, B0{}, B1{}, F{}, F{});
+        // Steps whose tiles t and t+1 lie wholly below the workgroup's first query row need no
+        // mask (unless the table has holes); they run in triples so buffer roles stay static.
+        const int mask_free_tiles = holes ? 0 : (prefix + t0 + 1) / kKeysPerTile;
+        const int mf_steps = max(0, min(ntiles - 1, mask_free_tiles - 1));
+        int t = 0;
+        if constexpr (F8) {
+            // two-tile ring: tile t in slot t % 2; the stage target of step t is slot t % 2 too
+            for (; t + 2 <= mf_steps; t += 2) {
+                step(t, B0{}, B1{}, B0{}, F{}, F{});
+                step(t + 1, B1{}, B0{}, B1{}, F{}, F{});
+            }
+            for (;;) {
+                if (t >= ntiles - 1) break;
+                step(t, B0{}, B1{}, B0{}, T{}, F{});
+                ++t;
+                if (t >= ntiles - 1) break;
+                step(t, B1{}, B0{}, B1{}, T{}, F{});
+                ++t;
+            }
+            if (t % 2 == 0)
+                step(t, B0{}, B1{}, B0{}, T{}, T{});
+            else
+                step(t, B1{}, B0{}, B1{}, T{}, T{});
+        } else {
+        for (; t + 3 <= mf_steps; t += 3) {
+            step(t, B0{}, B1{}, B2{}, F{}, F{});
+            step(t + 1, B1{}, B2{}, B0{}, F{}, F{});
+            step(t + 2, B2{}, B0{}, B1{}, F{}, F{});
         }
         for (;;) {
             if (t >= ntiles - 1) break;
-            step(t, B0{}, B1{}, B0{}, T{}, F{});
+            step(t, B0{}, B1{}, B2{}, T{}, F{});
             ++t;
             if (t >= ntiles - 1) break;
-            step(t, B1{}, B0{}, B1{}, T{}, F{});
+            step(t, B1{}, B2{}, B0{}, T{}, F{});
+            ++t;
+            if (t >= ntiles - 1) break;
+            step(t, B2{}, B0{}, B1{}, T{}, F{});
             ++t;
         }
-        if (t % 2 == 0)
-            step(t, B0{}, B1{}, B0{}, T{}, T{});
-        else
-            step(t, B1{}, B0{}, B1{}, T{}, T{});
-    } else {
-    for (; t + 3 <= mf_steps; t += 3) {
-        step(t, B0{}, B1{}, B2{}, F{}, F{});
-        step(t + 1, B1{}, B2{}, B0{}, F{}, F{});
-        step(t + 2, B2{}, B0{}, B1{}, F{}, F{});
-    }
-    for (;;) {
-        if (t >= ntiles - 1) break;
-        step(t, B0{}, B1{}, B2{}, T{}, F{});
-        ++t;
-        if (t >= ntiles - 1) break;
-        step(t, B1{}, B2{}, B0{}, T{}, F{});
-        ++t;
-        if (t >= ntiles - 1) break;
-        step(t, B2{}, B0{}, B1{}, T{}, F{});
-        ++t;
-    }
-    switch (t % 3) {
-        case 0: step(t, B0{}, B1{}, B2{}, T{}, T{}); break;
-        case 1: step(t, B1{}, B2{}, B0{}, T{}, T{}); break;
-        default: step(t, B2{}, B0{}, B1{}, T{}, T{}); break;
-    }
-    }
+        switch (t % 3) {
+            case 0: step(t, B0{}, B1{}, B2{}, T{}, T{}); break;
+            case 1: step(t, B1{}, B2{}, B0{}, T{}, T{}); break;
+            default: step(t, B2{}, B0{}, B1{}, T{}, T{}); break;
+        }
+        }
+    };
+    if (holes)
+        run(std::true_type{});
+    else
+        run(std::false_type{});
 
-    // Epilogue: lane (j, g) holds O[row][16n + 4g + r] = acc[qt][n][r].
+    // Epilogue: lane (c, h) holds O[tw + c][32 n + 8 i + 4 h + r] = acc[n][4 i + r].
+    {
+        const float l_tot = lsum + __uint_as_float(__builtin_amdgcn_permlane32_swap(
+                                           __float_as_uint(lsum), __float_as_uint(lsum),
+                                           false, false)[h32 ? 0 : 1]);
+        const int tq = tw + c32;
+        if (tq < rows) {
+            const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+            __bf16* o = out + (static_cast<int64_t>(qb + tq) * hq + q_head) * D;
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-        const float l_tot = lsum[qt][0];
-        const int tq = tw + qt * 16 + j;
-        if (tq >= rows) continue;
-        const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-        __bf16* o = out + (static_cast<int64_t>(qb + tq) * hq + q_head) * D;
+            for (int n = 0; n < NT2; ++n) {
 #pragma unroll
-        for (int n = 0; n < NT; ++n) {
-            u32x2 w;
-            w[0] = pack_bf16x2(acc[qt][n][0] * inv, acc[qt][n][1] * inv);
-            w[1] = pack_bf16x2(acc[qt][n][2] * inv, acc[qt][n][3] * inv);
-            *reinterpret_cast<u32x2*>(o + 16 * n + 4 * g) = w;
+                for (int i = 0; i < 4; ++i) {
+                    u32x2 w;
+                    w[0] = pack_bf16x2(acc[n][4 * i] * inv, acc[n][4 * i + 1] * inv);
+                    w[1] = pack_bf16x2(acc[n][4 * i + 2] * inv, acc[n][4 * i + 3] * inv);
+                    *reinterpret_cast<u32x2*>(o + 32 * n + 8 * i + 4 * h32) = w;
+                }
+            }
         }
     }
 }
