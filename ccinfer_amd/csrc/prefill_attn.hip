@@ -64,9 +64,21 @@ struct TileEntry {
     int t0;
 };
 
+// Inclusive prefix sum over the 64 lanes of a wavefront (shuffles, no LDS).
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int t = __shfl_up(v, off, 64);
+        if (lane >= off) v += t;
+    }
+    return v;
+}
+
 // In-place inclusive prefix sum of a[0..n) (n <= 4 * blockDim.x) by a 1024-thread block.
-// Each thread scans up to 4 consecutive entries, then a Hillis-Steele pass over the
-// per-thread totals adds the carries. Must be called by every thread of the block.
+// Each thread scans up to 4 consecutive entries; the per-thread totals are scanned within
+// each wavefront by shuffles and across the 16 wavefronts through `part` (>= 16 ints).
+// Must be called by every thread of the block.
 __device__ void block_inclusive_scan(int* a, int n, int* part) {
     const int tid = threadIdx.x;
     const int nt = blockDim.x;
@@ -78,15 +90,18 @@ __device__ void block_inclusive_scan(int* a, int n, int* part) {
         run += a[x];
         a[x] = run;
     }
-    part[tid] = run;
+    const int incl = wave_inclusive_scan(run);
+    const int wave = tid >> 6;
+    if ((tid & 63) == 63) part[wave] = incl;
     __syncthreads();
-    for (int off = 1; off < nt; off <<= 1) {
-        const int v = tid >= off ? part[tid - off] : 0;
-        __syncthreads();
-        part[tid] += v;
-        __syncthreads();
+    if (tid < 64) {
+        const int nw = nt >> 6;
+        const int w = tid < nw ? part[tid] : 0;
+        const int wi = wave_inclusive_scan(w);
+        if (tid < nw) part[tid] = wi - w;  // exclusive offset of wavefront tid
     }
-    const int carry = tid > 0 ? part[tid - 1] : 0;
+    __syncthreads();
+    const int carry = part[wave] + incl - run;
     for (int x = lo; x < hi; ++x) a[x] += carry;
     __syncthreads();
 }
@@ -104,7 +119,7 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(
     __shared__ int s_scan[kMaxPlanRequests];
     __shared__ int s_hist[kBuckets];
     __shared__ int s_hscan[kBuckets];
-    __shared__ int s_part[1024];
+    __shared__ int s_part[16];
     __shared__ int s_ndec;
     __shared__ int s_total;
     const int tid = threadIdx.x;

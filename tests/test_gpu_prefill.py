@@ -126,6 +126,20 @@ def test_mixed_chunked_prefill_and_decode(gpu):
     assert_attn_close(got[w.query_start_loc[nc:-1]], f32(dec), "mixed decode items")
 
 
+def test_plan_with_thousands_of_requests(gpu):
+    # 2600 requests: the planner's scans take several entries per thread, its histogram
+    # sorts 1100 query tiles, and 1500 single-token requests become decode items
+    say("prefill plan 1100 chunks + 1500 decodes (sampled rows)")
+    w = W.mixed_step(device=gpu, seed=9, n_chunks=1100, chunk=16, prefix_hi=96,
+                     n_decode=1500, dec_lo=16, dec_hi=400)
+    write_new(w, gpu)
+    got = f32(run_prefill(w, gpu))
+    pairs = sample_pairs(w, 512, 9)
+    want = oracle_prefill(w, pairs=pairs)
+    r, h = pairs[:, 0], pairs[:, 1]
+    assert_attn_close(got[r, h], want[r, h], "many requests")
+
+
 @pytest.mark.parametrize("hq,hkv,d,new,prefix", [
     (16, 8, 128, 200, 48), (4, 4, 128, 70, 0), (16, 4, 128, 130, 32), (8, 8, 64, 90, 16),
     (16, 8, 256, 75, 32), (6, 2, 128, 40, 16), (16, 8, 96, 37, 16), (4, 2, 80, 33, 0),
