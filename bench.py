@@ -142,11 +142,11 @@ def u16(t: torch.Tensor) -> np.ndarray:
     return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
 
 
-def cpu_decode_baseline(w: W.PagedWorkload, budget_s: float, pairs=None):
+def cpu_decode_baseline(w: W.PagedWorkload, budget_s: float, pairs=None, nthreads=None):
     """Times the oracle decode on the host (all rows, or `pairs`); returns (s/step, reps)."""
     import oracle  # test infrastructure: the baseline being reported, never the product
     q, k, v = u16(w.q), u16(w.k_cache), u16(w.v_cache)
-    nt = cpu_threads()
+    nt = nthreads or cpu_threads()
     reps, t0 = 0, time.perf_counter()
     while True:
         oracle.decode(q, k, v, w.block_table, w.context_lens, nthreads=nt, pairs=pairs)
@@ -296,6 +296,11 @@ def run(args):
             s, reps = cpu_decode_baseline(w, args.cpu_budget)
             r["cpu_GBps"] = w.kv_bytes() / s / 1e9
             r["cpu_reps"] = reps
+            # the faithful single-thread loop, on sequences 0-7 (all q-heads)
+            pairs = np.array([[b, h] for b in range(8) for h in range(w.hq)], np.int32)
+            s1, _ = cpu_decode_baseline(w, 2.0, pairs=pairs, nthreads=1)
+            r["cpu_1thread_GBps"] = (int(w.context_lens[:8].astype(np.int64).sum()) * w.hkv *
+                                     w.d * 4 / s1 / 1e9)
         deferred.append(cpu2)
         head = (w, r)
         out["2_decode_b64_ctx128-4096"] = r
@@ -559,7 +564,9 @@ def main():
         "cpu_baseline": None if "cpu_GBps" not in r else {
             "value": round(r["cpu_GBps"], 3), "unit": "GB/s", "cores": nt, "kind": "port",
             "sample": f"full configs[1] batch (all 1024 (seq, q_head) rows), {r['cpu_reps']} "
-                      f"repetition(s), oracle/attn_oracle.c over {nt} threads, {cpu_model()}"},
+                      f"repetition(s), oracle/attn_oracle.c over {nt} threads, {cpu_model()}",
+            "single_thread_value": round(r.get("cpu_1thread_GBps", 0.0), 3),
+            "single_thread_sample": "sequences 0-7, all 16 q-heads, 1 thread"},
         "configs": {k: {kk: (round(vv, 5) if isinstance(vv, float) else vv)
                         for kk, vv in v.items()} for k, v in out.items()},
     }
