@@ -690,29 +690,6 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
         if (lb < nblk && pb < 0) s_holes = 1;
     }
 
-    // Zero the K/V buffers once: slots that are never loaded must hold finite values.
-    {
-        constexpr int kWords = kKeysPerTile * D / 8;  // 16-byte words per buffer
-        if constexpr (F8) {
-            __bf16* bufs[4] = {lds_k0, lds_k1, lds_v0, lds_v1};
-#pragma unroll
-            for (int bi = 0; bi < 4; ++bi)
-                for (int i = threadIdx.x; i < kWords; i += kPipeThreads)
-                    reinterpret_cast<u32x4*>(bufs[bi])[i] = u32x4{0, 0, 0, 0};
-            uint8_t* bufs8[4] = {lds_k8_0, lds_k8_1, lds_v8_0, lds_v8_1};
-#pragma unroll
-            for (int bi = 0; bi < 4; ++bi)
-                for (int i = threadIdx.x; i < kWords / 2; i += kPipeThreads)
-                    reinterpret_cast<u32x4*>(bufs8[bi])[i] = u32x4{0, 0, 0, 0};
-        } else {
-            __bf16* bufs[6] = {lds_k0, lds_k1, lds_k2, lds_v0, lds_v1, lds_v2};
-#pragma unroll
-            for (int bi = 0; bi < 6; ++bi)
-                for (int i = threadIdx.x; i < kWords; i += kPipeThreads)
-                    reinterpret_cast<u32x4*>(bufs[bi])[i] = u32x4{0, 0, 0, 0};
-        }
-    }
-
     // Staging constants. Load x of a wavefront fills the 64 16-byte LDS slots starting at
     // slot0 = (x * waves + wave) * 64: rows slot0/CPR .. +64/CPR-1, which lie in one 16-row
     // cache block, so the block id is wave-uniform and each address is a scalar block base
@@ -782,6 +759,12 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
                         (__attribute__((address_space(3))) void*)(lv + slot0 * 8), 16, 0, 0);
                 }
             }
+            // Slots not loaded get zeros (LDS holds undefined bits at workgroup start; the
+            // mask gives these rows probability 0, and 0 * V must stay finite).
+            if (!(pb >= 0 && in_range)) {
+                *reinterpret_cast<u32x4*>(lk + (slot0 + lane) * 8) = u32x4{0, 0, 0, 0};
+                *reinterpret_cast<u32x4*>(lv + (slot0 + lane) * 8) = u32x4{0, 0, 0, 0};
+            }
             if (((slot0 + lane) % CPR) == 0)
                 lvalid[row] = static_cast<uint8_t>(pb >= 0 && in_range);
         }
@@ -817,6 +800,10 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
                 __builtin_amdgcn_global_load_lds(
                     (void*)(v_cache8 + off),
                     (__attribute__((address_space(3))) void*)(lv8 + slot0 * 16), 16, 0, 0);
+            }
+            if (!(pb >= 0 && in_range)) {  // zero bytes: row scale 0 must give 0, not NaN
+                *reinterpret_cast<u32x4*>(lk8 + (slot0 + lane) * 16) = u32x4{0, 0, 0, 0};
+                *reinterpret_cast<u32x4*>(lv8 + (slot0 + lane) * 16) = u32x4{0, 0, 0, 0};
             }
             if ((p % CPR8) == 0) lvalid[row] = static_cast<uint8_t>(pb >= 0 && in_range);
         }
@@ -868,9 +855,8 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
         const __bf16* qv = q + (static_cast<int64_t>(qb + (live ? tq : 0)) * hq + q_head) * D;
 #pragma unroll
         for (int kk = 0; kk < S2; ++kk) {
-            u32x4 w = load16(qv + kk * 16 + h32 * 8);
-            if (!live) w = u32x4{0, 0, 0, 0};
-            qop[kk] = __builtin_bit_cast(bf16x8, w);
+            // rows past the tile's end read row 0 (finite) and are never stored
+            qop[kk] = __builtin_bit_cast(bf16x8, load16(qv + kk * 16 + h32 * 8));
         }
     }
     __syncthreads();  // block table staged
