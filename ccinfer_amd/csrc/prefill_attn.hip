@@ -730,8 +730,8 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
         }
     }
 
-    // Rows past kv_end or in unmapped blocks are not loaded: their LDS slots keep earlier,
-    // finite contents (the buffers are zeroed first) and the mask gives them probability 0.
+    // Rows past kv_end or in unmapped blocks are not loaded: their LDS slots are written with
+    // zeros instead, and the mask gives them probability 0.
     auto stage = [&](int t, __bf16* lk, __bf16* lv, uint8_t* lvalid)
                      __attribute__((always_inline)) {
         const int key_base = t * kKeysPerTile;
