@@ -38,9 +38,6 @@ __device__ __forceinline__ int64_t kv_row_offset(int ctx_pos, int kv_head, int h
     return (slot * num_kv_heads + kv_head) * static_cast<int64_t>(head_dim);
 }
 
-__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
-__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-
 // Round-to-nearest-even fp32 -> bf16 pair (gfx950 has a native packed convert).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     using bf16x2 = __bf16 __attribute__((ext_vector_type(2)));
@@ -60,18 +57,6 @@ __device__ __forceinline__ float wave_max_xor16_32(float v) {
     v = fmaxf(v, __shfl_xor(v, 16));
     v = fmaxf(v, __shfl_xor(v, 32));
     return v;
-}
-
-// Max over lanes l, l^16, l^32, l^48 with the gfx950 lane-swap instructions (no LDS
-// round trip): permlane32_swap on two copies leaves {x[l%32], x[l%32+32]} in the pair,
-// permlane16_swap then pairs 16-lane rows 0/1 and 2/3.
-__device__ __forceinline__ float wave_max_swap16_32(float v) {
-    const uint32_t u = __float_as_uint(v);
-    const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-    const float m32 = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-    const uint32_t w = __float_as_uint(m32);
-    const auto b = __builtin_amdgcn_permlane16_swap(w, w, false, false);
-    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 // Max over lanes l and l^32 (one permlane32_swap).

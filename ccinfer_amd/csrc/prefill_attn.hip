@@ -586,16 +586,15 @@ __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
 // finished tile t-1 and tile t+1 has landed, so tile t+2 streams into the freed buffer
 // while tiles t and t+1 are read.
 // ---------------------------------------------------------------------------
-template <int D, int QT>
+template <int D>
 struct PipeShape {
-    static constexpr int kRows = 16 * QT;                // query rows per wavefront
+    static constexpr int kRows = 32;                     // query rows per wavefront
     static constexpr int kWaves = 8;
     static constexpr int kThreads = 64 * kWaves;
     static constexpr int kCPR = D / 8;                   // 16-byte chunks per K/V row
     static constexpr int kLoads = kKeysPerTile * kCPR / kThreads;  // per K or V
     static_assert(kKeysPerTile * kCPR % kThreads == 0, "staging must split evenly");
 };
-constexpr int kPipeQT = 2;  // 32 rows per wavefront
 
 __host__ __device__ constexpr bool pipe_head_dim(int d) { return d == 64 || d == 128; }
 
@@ -603,8 +602,8 @@ __host__ __device__ constexpr bool pipe_head_dim(int d) { return d == 64 || d ==
 // staged as bytes into a two-tile ring and dequantised (byte * row scale, rounded to bf16)
 // into a two-tile ring of bf16 tiles in the same swizzled layout, so everything after the
 // staging is the bf16 kernel.
-template <int D, int QTT, bool F8 = false>
-__global__ __launch_bounds__((PipeShape<D, QTT>::kThreads))
+template <int D, bool F8 = false>
+__global__ __launch_bounds__((PipeShape<D>::kThreads))
 void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ k_cache_v,
                          const void* __restrict__ v_cache_v, const float* __restrict__ k_scale,
                          const float* __restrict__ v_scale,
@@ -613,7 +612,7 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
                          const int32_t* __restrict__ context_lens, __bf16* __restrict__ out,
                          const int32_t* __restrict__ counts, const TileEntry* __restrict__ tiles,
                          int total_tokens, int mbpr, int hq, int hkv, float scale_log2) {
-    using Sh = PipeShape<D, QTT>;
+    using Sh = PipeShape<D>;
     constexpr int S2 = D / 16;   // QK k-steps (32x32x16 MFMA)
     constexpr int NT2 = D / 32;  // PV dim tiles
     constexpr int CPR = Sh::kCPR;
@@ -1201,7 +1200,7 @@ size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
 int tile_tokens_for(int head_dim, int G) {
     if (pipe_head_dim(head_dim))
-        return (PipeShape<64, kPipeQT>::kWaves / heads_per_wg(G)) * PipeShape<64, kPipeQT>::kRows;
+        return (PipeShape<64>::kWaves / heads_per_wg(G)) * PipeShape<64>::kRows;
     return (kWaves / heads_per_wg(G)) * PrefillShape<256>::kQW;
 }
 
@@ -1240,8 +1239,8 @@ hipError_t launch_tiles(const void* q, const void* k_cache, const void* v_cache,
     const int64_t grid = static_cast<int64_t>(max_tiles) * U;
     const float scale_log2 = kLog2e / sqrtf(static_cast<float>(D));
     if constexpr (pipe_head_dim(D)) {
-        prefill_pipe_kernel<D, kPipeQT, F8>
-            <<<static_cast<unsigned>(grid), PipeShape<D, kPipeQT>::kThreads, 0, stream>>>(
+        prefill_pipe_kernel<D, F8>
+            <<<static_cast<unsigned>(grid), PipeShape<D>::kThreads, 0, stream>>>(
             static_cast<const __bf16*>(q), k_cache, v_cache, k_scale, v_scale, block_table, qsl,
             context_lens,
             static_cast<__bf16*>(output), counts, tiles, total_query_tokens, mbpr, hq, hkv,
