@@ -13,8 +13,9 @@
 //   Split length: batches of 4..256 items use the balanced plan -- every wavefront reads the
 //   items' context lengths, derives the split length from the actual total (so ragged
 //   batches get equal-length splits instead of splits sized for the longest possible
-//   context) and finds its (item, split) with a wave-wide prefix scan; the merge kernel
-//   repeats the same computation. This also covers the decode items of a mixed prefill
+//   context) and finds its (item, split) with a wave-wide prefix scan. Split 0 of every
+//   row writes a merge descriptor (first partial slot, split count) that the merge kernel
+//   reads, so the merge does not repeat the scan. This also covers the decode items of a mixed prefill
 //   batch, whose list and count the prefill planner writes on the device. Other batches use
 //   a fixed split length chosen on the host from the longest possible context.
 //
@@ -66,6 +67,14 @@ struct ItemArgs {
     const int32_t* qsl;
     float eps;
     int zero_invalid;
+};
+
+// Per (item, q_head) row: how many splits its partials span and where they start. Written
+// by split 0 of the row's kv_head group on every launch; the merge reads it instead of
+// re-deriving the plan (ns <= 1: nothing to merge).
+struct MergeDesc {
+    int64_t base;
+    int64_t ns;
 };
 
 template <int D>
@@ -486,8 +495,8 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     const void* __restrict__ v_cache_v, const float* __restrict__ k_scale,
     const float* __restrict__ v_scale, const int32_t* __restrict__ block_table,
     const int32_t* __restrict__ context_lens, __bf16* __restrict__ out, float* __restrict__ ws_o,
-    float* __restrict__ ws_ml, ItemArgs items, int mbpr, int hq, int hkv, int splits,
-    int split_tokens, int balanced_w, int slots, float scale_log2) {
+    float* __restrict__ ws_ml, MergeDesc* __restrict__ desc, ItemArgs items, int mbpr, int hq,
+    int hkv, int splits, int split_tokens, int balanced_w, int slots, float scale_log2) {
     constexpr int S = DecodeShape<D>::kSteps;
     constexpr int NV = DecodeShape<D>::kNV;
     using Cache = std::conditional_t<F8, uint8_t, __bf16>;
@@ -526,6 +535,15 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     const int G = hq / hkv;
     const int j = lane & 15;
     const int g = lane >> 4;
+    const int ns = balanced_w > 0 ? ns_bal
+                                  : (ctx > 0 ? (ctx + split_tokens - 1) / split_tokens : 0);
+    if (desc != nullptr && s == 0 && lane < G) {
+        const int head = h * G + lane;
+        desc[static_cast<int64_t>(item) * hq + head] = MergeDesc{
+            balanced_w > 0 ? static_cast<int64_t>(head) * slots + first_slot
+                           : (static_cast<int64_t>(item) * hq + head) * splits,
+            ctx > 0 ? ns : 0};
+    }
 
     if (ctx < 0) {
         // Decode semantics: invalid context -> zeros (written once, by split 0).
@@ -539,7 +557,6 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     const int begin = s * split_tokens;
     if (begin >= ctx) return;
     const int end = min(ctx, begin + split_tokens);
-    const int ns = balanced_w > 0 ? ns_bal : (ctx + split_tokens - 1) / split_tokens;
     const int32_t* req_blocks = block_table + static_cast<int64_t>(req) * mbpr;
 
     // Block ids of this split, one per lane (two registers cover 128 blocks).
@@ -650,38 +667,26 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
 // One wavefront per (item, q_head) row with more than one split: log-sum-exp merge.
 template <int D>
 __global__ __launch_bounds__(256) void decode_merge_kernel(
-    const int32_t* __restrict__ context_lens, __bf16* __restrict__ out,
-    const float* __restrict__ ws_o, const float* __restrict__ ws_ml, ItemArgs items, int mbpr,
-    int hq, int splits, int split_tokens, int balanced_w, int slots) {
+    __bf16* __restrict__ out, const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
+    const MergeDesc* __restrict__ desc, ItemArgs items, int hq) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wi = blockIdx.x * kWavesPerGroup + wave;
     const int head = wi % hq;
     const int item = wi / hq;
+    if (item >= items.num_items) return;
+    const MergeDesc d = desc[static_cast<int64_t>(item) * hq + head];
     int req, qrow;
     if (!resolve_item(items, item, &req, &qrow)) return;
-    const int ctx = effective_ctx(context_lens[req], mbpr, items.zero_invalid);
-    if (ctx < 0) return;  // zeros already written (decode) / row untouched (prefill)
-    int ns;
-    int64_t base;
-    if (balanced_w > 0) {
-        BalancedSplit bs;
-        if (!balanced_lookup(context_lens, items, mbpr, balanced_w, item, true, lane, &bs))
-            return;
-        ns = bs.nsplit;
-        base = static_cast<int64_t>(head) * slots + bs.first_slot;
-    } else {
-        ns = (ctx + split_tokens - 1) / split_tokens;
-        base = (static_cast<int64_t>(item) * hq + head) * splits;
-    }
-    if (ns <= 1) return;  // written directly by the split kernel
-    merge_row<D>(ws_o, ws_ml, base, ns, items.eps,
+    if (d.ns <= 1) return;  // invalid row, or written directly by the split kernel
+    merge_row<D>(ws_o, ws_ml, d.base, static_cast<int>(d.ns), items.eps,
                  out + (static_cast<int64_t>(qrow) * hq + head) * D, lane);
 }
 
 struct DecodeWs {
     float* o;
     float* ml;
+    MergeDesc* desc;
 };
 
 // Partial rows of the plan: (item, q_head, split) in fixed mode, (q_head, slot) balanced.
@@ -690,11 +695,17 @@ size_t partial_rows(int num_items, int hq, const DecodePlan& plan) {
                          : static_cast<size_t>(num_items) * hq * plan.splits;
 }
 
+// Partials (O rows, then (m, l) pairs), then one MergeDesc per (item, q_head) row.
+size_t desc_offset(size_t rows, int d) {
+    return (rows * (d + 2) * sizeof(float) + 15) & ~static_cast<size_t>(15);
+}
+
 DecodeWs carve(void* workspace, size_t rows, int d) {
     DecodeWs w{};
     char* p = static_cast<char*>(workspace);
     w.o = reinterpret_cast<float*>(p);
     w.ml = reinterpret_cast<float*>(p + rows * d * sizeof(float));
+    w.desc = reinterpret_cast<MergeDesc*>(p + desc_offset(rows, d));
     return w;
 }
 
@@ -716,15 +727,14 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
     decode_split_kernel<D, F8><<<grid, 256, 0, stream>>>(
         static_cast<const __bf16*>(q), k_cache, v_cache, k_scale, v_scale, block_table,
         context_lens,
-        static_cast<__bf16*>(output), w.o, w.ml, it, mbpr, hq, hkv, plan.splits,
+        static_cast<__bf16*>(output), w.o, w.ml, w.desc, it, mbpr, hq, hkv, plan.splits,
         plan.split_tokens, bw, plan.slots, scale_log2);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess || !merge) return err;
     const int64_t rows = static_cast<int64_t>(it.num_items) * hq;
     const int mgrid = static_cast<int>((rows + kWavesPerGroup - 1) / kWavesPerGroup);
-    decode_merge_kernel<D><<<mgrid, 256, 0, stream>>>(context_lens, static_cast<__bf16*>(output),
-                                                      w.o, w.ml, it, mbpr, hq, plan.splits,
-                                                      plan.split_tokens, bw, plan.slots);
+    decode_merge_kernel<D><<<mgrid, 256, 0, stream>>>(static_cast<__bf16*>(output), w.o, w.ml,
+                                                      w.desc, it, hq);
     return hipGetLastError();
 }
 
@@ -764,8 +774,9 @@ DecodePlan plan_decode(int num_items, int num_kv_heads, int max_ctx, bool allow_
 size_t decode_workspace_bytes(int num_items, int num_q_heads, int head_dim,
                               const DecodePlan& plan) {
     if (!plan.balanced && plan.splits <= 1) return 0;
-    // partial O + (m, l) per partial row
-    return partial_rows(num_items, num_q_heads, plan) * (head_dim + 2) * sizeof(float);
+    // partial O + (m, l) per partial row, then the merge descriptors
+    return desc_offset(partial_rows(num_items, num_q_heads, plan), head_dim) +
+           static_cast<size_t>(num_items) * num_q_heads * sizeof(MergeDesc);
 }
 
 bool decode_fast_supported(int num_q_heads, int num_kv_heads, int head_dim, int block_size) {

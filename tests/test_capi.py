@@ -83,10 +83,11 @@ def test_decode_workspace_size(lib):
     assert f(0, 4, 8, 2, 128, 16) == 0            # invalid shape -> 0
     assert f(1, 1, 8, 2, 128, 16) == 0            # one 16-token block: single split, no scratch
     assert f(7, 2, 8, 2, 128, 16) == 0            # 32 tokens: one chunk per request
-    n = f(32, 2048, 32, 8, 128, 16)
+    # partials ((D + 2) floats per partial row), then a 16-byte merge descriptor per (B, Hq)
+    n = f(32, 2048, 32, 8, 128, 16) - 32 * 32 * 16
     assert n > 0 and n % (32 * 130 * 4) == 0      # Hq * partial slots * (D + 2) floats
     assert n <= 32 * 32 * 2048 * 130 * 4          # never more than one slot per 32 tokens
-    big = f(300, 2048, 32, 8, 128, 16)            # past the balanced-plan batch limit
+    big = f(300, 2048, 32, 8, 128, 16) - 300 * 32 * 16  # past the balanced-plan batch limit
     assert big > 0 and big % (300 * 32 * 130 * 4) == 0  # B * Hq * splits * (D + 2) floats
     assert f(32, 2048, 32, 8, 80, 16) == 0        # generic head_dim path uses no scratch
 
