@@ -524,8 +524,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
-              "(the attention path shards by (sequence, kv_head) with no exchange, see "
-              "DESIGN.md).", file=sys.stderr)
+              "(each GPU would own whole sequences or whole kv_heads, with no exchange "
+              "inside attention; only the one-GPU share is built).", file=sys.stderr)
         sys.exit(2)
     if args.profile_op:
         profile(args.profile_op, args.profile_iters)
