@@ -158,3 +158,23 @@ def test_prefill_fp8_mixed_batch_with_side_stream_decode_items(gpu):
                                meta["block_table"][nc:].contiguous(),
                                meta["context_lens"][nc:].contiguous())
     assert_attn_close(f32(out)[w.query_start_loc[nc:-1]], f32(dec), "fp8 mixed decode items")
+
+
+def test_prefill_fp8_config3_equals_bf16_prefill_of_dequantised_cache(gpu):
+    """Full configs[2] size (8 x (512 + 1536), shared prefix): bit-identical to the bf16
+    prefill over the dequantised cache, whose own full-size parity is tested against the
+    oracle on sampled rows."""
+    from ccinfer_amd import prefill_attention, prefill_attention_fp8
+    say("fp8 prefill config3 size vs bf16 over the dequantised cache")
+    w = W.prefill_prefix(device=gpu)
+    meta = w.device_meta(gpu)
+    kc, vc, ks, vs = quantised_cache(gpu, w, w.hkv, w.d)
+    out8 = prefill_attention_fp8(w.q, kc, vc, ks, vs, meta["block_table"],
+                                 meta["query_start_loc"], meta["context_lens"])
+    kb = from_u16(_dequant_bf16(kc.cpu().numpy(), ks.cpu().numpy(), w.hkv), gpu)
+    vb = from_u16(_dequant_bf16(vc.cpu().numpy(), vs.cpu().numpy(), w.hkv), gpu)
+    out16 = prefill_attention(w.q, kb, vb, meta["block_table"], meta["query_start_loc"],
+                              meta["context_lens"])
+    torch.cuda.synchronize()
+    assert torch.equal(out8, out16)
+    assert bool(torch.isfinite(out8.float()).all())
