@@ -178,3 +178,16 @@ def test_prefill_fp8_config3_equals_bf16_prefill_of_dequantised_cache(gpu):
     torch.cuda.synchronize()
     assert torch.equal(out8, out16)
     assert bool(torch.isfinite(out8.float()).all())
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(8, 2, 64), (16, 8, 256), (12, 4, 64)])
+def test_decode_fp8_other_head_dims(gpu, hq, hkv, d):
+    say(f"fp8 decode hq={hq} hkv={hkv} d={d}")
+    w = W.decode_batched(device=gpu, batch=12, ctx_lo=20, ctx_hi=1500, hq=hq, hkv=hkv, d=d)
+    meta = w.device_meta(gpu)
+    kc, vc, ks, vs = quantised_cache(gpu, w, hkv, d)
+    out = decode_attention_fp8(w.q, kc, vc, ks, vs, meta["block_table"], meta["context_lens"])
+    torch.cuda.synchronize()
+    want = oracle.decode_fp8(u16(w.q), kc.cpu().numpy(), vc.cpu().numpy(), ks.cpu().numpy(),
+                             vs.cpu().numpy(), w.block_table, w.context_lens)
+    assert_attn_close(f32(out), want, f"fp8 d={d}")
