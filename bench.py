@@ -509,6 +509,43 @@ def profile(op: str, iters: int) -> None:
     torch.cuda.synchronize()
 
 
+def sweep(kind: str) -> None:
+    """Prints a markdown table of the decode or prefill op across shapes beyond the fixed
+    configs (synthetic data, event timing as in the configs)."""
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream()
+    print(f"| {kind} shape | time (us) | achieved | fraction of peak |")
+    print("|---|---|---|---|")
+    if kind == "decode":
+        for hq, hkv in ((16, 8), (32, 8)):
+            for batch, ctx in ((1, 4096), (8, 4096), (32, 4096), (64, 1024), (64, 4096),
+                               (128, 2048), (256, 1024), (16, 32768), (64, 16384)):
+                w = W.decode_batched(device=dev, batch=batch, ctx_lo=ctx, ctx_hi=ctx, hq=hq,
+                                     hkv=hkv, with_write=False)
+                ops = Ops(w, dev, stream)
+                ms, _ = time_loop(ops.decode, 20, 3, stream)
+                gbs = w.kv_bytes() / (ms * 1e-3) / 1e9
+                print(f"| B={batch} ctx={ctx} Hq/Hkv={hq}/{hkv} | {ms * 1e3:.1f} | "
+                      f"{gbs:.0f} GB/s | {gbs * 1e9 / HBM_PEAK:.0%} HBM |", flush=True)
+                del w, ops
+                torch.cuda.empty_cache()
+    else:
+        for n_seqs, prefix, new, hq, hkv in ((8, 512, 1536, 16, 8), (8, 0, 2048, 16, 8),
+                                             (4, 4096, 2048, 16, 8), (2, 16384, 2048, 16, 8),
+                                             (8, 512, 1536, 32, 8), (8, 512, 1536, 32, 4),
+                                             (16, 0, 512, 16, 8), (1, 0, 8192, 32, 8)):
+            w = W.prefill_prefix(device=dev, n_seqs=n_seqs, prefix=prefix, new=new, hq=hq,
+                                 hkv=hkv, share_pairs=())
+            ops = Ops(w, dev, stream)
+            ms, _ = time_loop(ops.prefill, 20, 3, stream)
+            tf = W.prefill_flops(w) / (ms * 1e-3) / 1e12
+            print(f"| {n_seqs} x ({prefix} cached + {new} new) Hq/Hkv={hq}/{hkv} | "
+                  f"{ms * 1e3:.1f} | {tf:.0f} TFLOP/s | {tf * 1e12 / BF16_PEAK:.0%} bf16 MFMA |",
+                  flush=True)
+            del w, ops
+            torch.cuda.empty_cache()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -517,6 +554,8 @@ def main():
     ap.add_argument("--configs", default="1,2,3,4,5,6,7,8")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=5.0)
+    ap.add_argument("--sweep", choices=("decode", "prefill"),
+                    help="print a table of the op across shapes and exit")
     ap.add_argument("--profile-op", choices=["decode", "write", "prefill", "mixed", "long",
                                              "prologue", "shared_prefix", "private_prefix",
                                              "copy"], default=None)
@@ -527,6 +566,9 @@ def main():
               "(each GPU would own whole sequences or whole kv_heads, with no exchange "
               "inside attention; only the one-GPU share is built).", file=sys.stderr)
         sys.exit(2)
+    if args.sweep:
+        sweep(args.sweep)
+        return
     if args.profile_op:
         profile(args.profile_op, args.profile_iters)
         return
