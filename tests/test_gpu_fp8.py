@@ -191,3 +191,40 @@ def test_decode_fp8_other_head_dims(gpu, hq, hkv, d):
     want = oracle.decode_fp8(u16(w.q), kc.cpu().numpy(), vc.cpu().numpy(), ks.cpu().numpy(),
                              vs.cpu().numpy(), w.block_table, w.context_lens)
     assert_attn_close(f32(out), want, f"fp8 d={d}")
+
+
+def test_prefill_fp8_holes_ragged_and_untouched_rows(gpu):
+    """Table holes, a context longer than the table row, ragged tile ends and a prefix < 0
+    row (left untouched): staging writes zero bytes for the slots it does not load, so
+    stale LDS contents never reach the output."""
+    from ccinfer_amd import prefill_attention_fp8
+    say("fp8 prefill edge cases")
+    rng = np.random.default_rng(13)
+    hq, hkv, d, mbpr, pool = 16, 8, 128, 16, 160
+    qlen = np.array([2, 1, 3, 5, 130, 1, 64, 90], np.int32)
+    ctx = np.array([40, 17, 3, 2, 200, 1, 300, 250], np.int32)  # seq 3: prefix < 0
+    bt = rng.permutation(pool)[:len(qlen) * mbpr].reshape(len(qlen), mbpr).astype(np.int32)
+    bt[4, 3] = -1            # hole inside a long prefill
+    bt[6, 15] = -1           # hole in the last block
+    bt[7, 10:] = -1          # table row shorter than the visible range
+    qsl = np.concatenate([[0], np.cumsum(qlen)]).astype(np.int32)
+    total = int(qsl[-1])
+    g = torch.Generator(device=gpu)
+    g.manual_seed(6)
+    q = W.randn_bf16((total, hq, d), g, gpu)
+    w = W.PagedWorkload("edge8", hq, hkv, d, ctx, bt, pool, q,
+                        W.randn_bf16((pool * BS, hkv, d), g, gpu),
+                        W.randn_bf16((pool * BS, hkv, d), g, gpu), query_start_loc=qsl)
+    kc, vc, ks, vs = quantised_cache(gpu, w, hkv, d)
+    meta = w.device_meta(gpu)
+    out = torch.full_like(q, 7.0)
+    prefill_attention_fp8(q, kc, vc, ks, vs, meta["block_table"], meta["query_start_loc"],
+                          meta["context_lens"], output=out)
+    torch.cuda.synchronize()
+    got = f32(out)
+    want = oracle.prefill_fp8(u16(q), kc.cpu().numpy(), vc.cpu().numpy(), ks.cpu().numpy(),
+                              vs.cpu().numpy(), bt, qsl, ctx,
+                              out=np.full((total, hq, d), 7.0, np.float32))
+    assert np.all(got[qsl[3]:qsl[4]] == 7.0)
+    assert np.all(np.isfinite(got))
+    assert_attn_close(got, want, "fp8 edge")
