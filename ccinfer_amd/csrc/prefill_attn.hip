@@ -1056,19 +1056,37 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
             uint8_t* vall = BL == 0 ? lds_valid0 : (BL == 1 ? lds_valid1 : lds_valid2);
             const int key0 = t * kKeysPerTile;
 
+            // Halves wholly above this wavefront's last row contribute nothing: in masked
+            // steps their MFMAs and exps are skipped (wave-uniform; skip0 -> skip1 -> skipn0).
+            const int wave_lim = prefix + tw + kPipeRows - 1;
+            const bool skip0 = kMask && key0 > wave_lim;
+            const bool skip1 = kMask && key0 + 32 > wave_lim;
+            const bool skipn0 = kMask && key0 + kKeysPerTile > wave_lim;
+            auto fill_neg_inf = [](f32x16& st) __attribute__((always_inline)) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) st[v] = kNegInf;
+            };
             // X: exp of (t, 0) || QK of (t, 1)
             __builtin_amdgcn_sched_barrier(0);
-            exp_part(sc, 0, pop[0]);
-            if constexpr (kMask) mask_seed(sn, key0 + 32, vbits_of(valc, 1), holes_tag);
-            qk_half(kc, 1, sn, mask_tag);
-            interleave_x();
+            if (!skip1) {
+                exp_part(sc, 0, pop[0]);
+                if constexpr (kMask) mask_seed(sn, key0 + 32, vbits_of(valc, 1), holes_tag);
+                qk_half(kc, 1, sn, mask_tag);
+                interleave_x();
+            } else {
+                if (!skip0) exp_part(sc, 0, pop[0]);
+                fill_neg_inf(sn);
+            }
             // Y: PV of (t, 0), exp of its second P operand || max of (t, 1)
             __builtin_amdgcn_sched_barrier(0);
-            pv_part(vc, 0, 0, pop[0]);
-            exp_part(sc, 1, pop[1]);
-            pv_part(vc, 0, 1, pop[1]);
-            const bool grow1 = max_half(sn, mt);
-            interleave_y();
+            bool grow1 = false;  // skip0: S of (t, 1) is -inf, its max cannot grow
+            if (!skip0) {
+                pv_part(vc, 0, 0, pop[0]);
+                exp_part(sc, 1, pop[1]);
+                pv_part(vc, 0, 1, pop[1]);
+                grow1 = max_half(sn, mt);
+                interleave_y();
+            }
             __builtin_amdgcn_sched_barrier(0);
             rescale(grow1, mt);
             if constexpr (!kLast) {
@@ -1089,21 +1107,31 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
             }
             // X: exp of (t, 1) || QK of (t+1, 0)
             __builtin_amdgcn_sched_barrier(0);
-            exp_part(sn, 0, pop[0]);
-            if constexpr (!kLast) {
-                if constexpr (kMask)
-                    mask_seed(sc, key0 + kKeysPerTile, vbits_of(valn, 0), holes_tag);
-                qk_half(kn, 0, sc, mask_tag);
+            if (!skipn0) {
+                exp_part(sn, 0, pop[0]);
+                if constexpr (!kLast) {
+                    if constexpr (kMask)
+                        mask_seed(sc, key0 + kKeysPerTile, vbits_of(valn, 0), holes_tag);
+                    qk_half(kn, 0, sc, mask_tag);
+                }
+                if constexpr (!kLast) interleave_x();
+            } else {
+                if (!skip1) exp_part(sn, 0, pop[0]);
+                if constexpr (!kLast) fill_neg_inf(sc);
             }
-            if constexpr (!kLast) interleave_x();
             // Y: PV of (t, 1), exp of its second P operand || max of (t+1, 0)
             __builtin_amdgcn_sched_barrier(0);
-            pv_part(vc, 1, 0, pop[0]);
-            exp_part(sn, 1, pop[1]);
-            pv_part(vc, 1, 1, pop[1]);
+            bool grow0 = false;  // skip1 -> skipn0: S of (t+1, 0) is -inf
+            if (!skip1) {
+                pv_part(vc, 1, 0, pop[0]);
+                exp_part(sn, 1, pop[1]);
+                pv_part(vc, 1, 1, pop[1]);
+                if constexpr (!kLast) {
+                    grow0 = max_half(sc, mt);
+                    interleave_y();
+                }
+            }
             if constexpr (!kLast) {
-                const bool grow0 = max_half(sc, mt);
-                interleave_y();
                 __builtin_amdgcn_sched_barrier(0);
                 rescale(grow0, mt);
             }
