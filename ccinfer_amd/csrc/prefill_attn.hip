@@ -683,10 +683,15 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
     __syncthreads();
     const int nblk_vis = (kv_end + kBlock - 1) / kBlock;
     const int nblk = min(nblk_vis, mbpr);
+    // Block ids whose byte offset does not fit the 32-bit buffer offset of the fast staging
+    // path are treated like holes (the checked path addresses with 64 bits).
+    const int max_fast_pb = static_cast<int>(
+        min(static_cast<int64_t>(0x7fffffff),
+            static_cast<int64_t>(0xffffffffll / (static_cast<int64_t>(kBlock) * hkv * D * 2)) - 1));
     for (int lb = threadIdx.x; lb < ntiles * (kKeysPerTile / kBlock); lb += kPipeThreads) {
         const int pb = lb < nblk ? req_blocks[lb] : -1;
         lds_bt[lb] = pb;
-        if (lb < nblk && pb < 0) s_holes = 1;
+        if (lb < nblk && (pb < 0 || pb > max_fast_pb)) s_holes = 1;
     }
 
     // Staging constants. Load x of a wavefront fills the 64 16-byte LDS slots starting at
@@ -731,15 +736,60 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
 
     // Rows past kv_end or in unmapped blocks are not loaded: their LDS slots are written with
     // zeros instead, and the mask gives them probability 0.
-    auto stage = [&](int t, __bf16* lk, __bf16* lv, uint8_t* lvalid)
+    // Block ids this wavefront stages, held in one register: lane i has the id of load
+    // i % NL's cache block in tile kWin * bt_win + i / NL. A stage reads its ids with
+    // readlane (no LDS round trip); the window is reloaded from the LDS table every kWin
+    // tiles.
+    constexpr int kWin = 64 / NL;
+#if defined(__HIP_DEVICE_COMPILE__)
+    // (device pass only: the host pass cannot type the buffer builtins, and a kernel
+    // template that fails there loses its launch stub silently)
+    const __amdgpu_buffer_rsrc_t k_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)k_cache, 0, -1, 0x00020000);
+    const __amdgpu_buffer_rsrc_t v_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)v_cache, 0, -1, 0x00020000);
+#endif
+    int btw;
+    int bt_win = -1;
+    auto bt_window = [&](int win) __attribute__((always_inline)) {
+        const int x = lane % NL;
+        const int blk = ((x * kPipeWaves + wave) * 64 / CPR) >> 4;
+        btw = lds_bt[min((win * kWin + lane / NL) * (kKeysPerTile / kBlock) + blk,
+                         kMaxTableLds - 1)];
+        bt_win = win;
+    };
+    // kHoles: the table has holes in the visible range; then every tile goes through the
+    // checked path, which also records per-row validity for the mask. Otherwise only a tile
+    // that reaches past kv_end does (its rows past kv_end are zero-filled).
+    auto stage = [&](int t, __bf16* lk, __bf16* lv, uint8_t* lvalid, auto holes_tag)
                      __attribute__((always_inline)) {
+        constexpr bool kHoles = decltype(holes_tag)::value;
         const int key_base = t * kKeysPerTile;
+        if (t / kWin != bt_win) bt_window(t / kWin);  // wave-uniform, once per kWin tiles
+#if defined(__HIP_DEVICE_COMPILE__)
+        if (!kHoles && key_base + kKeysPerTile <= kv_end) {
+            // Buffer loads: the block's byte offset is the scalar offset, the lane's offset
+            // inside the block the vector offset (every id here fits 32 bits, see above).
+#pragma unroll
+            for (int x = 0; x < NL; ++x) {
+                const int slot0 = (x * kPipeWaves + wave) * 64;
+                const int pb = __builtin_amdgcn_readlane(btw, (t % kWin) * NL + x);
+                const int soff = pb * static_cast<int>(blk_bytes);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    k_rsrc, (__attribute__((address_space(3))) void*)(lk + slot0 * 8), 16,
+                    st_off[x], soff, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    v_rsrc, (__attribute__((address_space(3))) void*)(lv + slot0 * 8), 16,
+                    st_off[x], soff, 0, 0);
+            }
+            return;
+        }
+#endif
 #pragma unroll
         for (int x = 0; x < NL; ++x) {
             const int slot0 = (x * kPipeWaves + wave) * 64;
             const int row = st_row[x];
-            const int pb = __builtin_amdgcn_readfirstlane(
-                lds_bt[t * (kKeysPerTile / kBlock) + ((slot0 / CPR) >> 4)]);
+            const int pb = __builtin_amdgcn_readlane(btw, (t % kWin) * NL + x);
             const bool in_range = key_base + row < kv_end;
             if (pb >= 0) {
                 const int64_t boff = static_cast<int64_t>(pb) * blk_bytes;
@@ -764,7 +814,7 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
                 *reinterpret_cast<u32x4*>(lk + (slot0 + lane) * 8) = u32x4{0, 0, 0, 0};
                 *reinterpret_cast<u32x4*>(lv + (slot0 + lane) * 8) = u32x4{0, 0, 0, 0};
             }
-            if (((slot0 + lane) % CPR) == 0)
+            if (kHoles && ((slot0 + lane) % CPR) == 0)
                 lvalid[row] = static_cast<uint8_t>(pb >= 0 && in_range);
         }
     };
@@ -897,11 +947,22 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
     // the row's causal limit and, with kBits, for keys whose validity bit is clear (only
     // needed when the table has holes: otherwise every key past kv_end is past every row's
     // limit too).
-    auto mask_seed = [&](f32x16& st, int key0, uint32_t vbits, auto bits_tag)
+    auto vbits_of = [&](const uint8_t* lvalid, int hh) __attribute__((always_inline)) {
+        const uint64_t v = __builtin_amdgcn_ballot_w64(lvalid[lane] != 0);
+        return static_cast<uint32_t>(v >> (32 * hh));
+    };
+    auto mask_seed = [&](f32x16& st, int key0, const uint8_t* lvalid, int hh, auto bits_tag)
                          __attribute__((always_inline)) {
         constexpr bool kBits = decltype(bits_tag)::value;
+        if (!kBits && key0 + 31 <= prefix + tw) {  // wave-uniform: every key visible
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+                st[v] = 0.f;
+            return;
+        }
         const int thr = limit - key0 - 4 * h32;
-        const uint32_t vb = kBits ? (vbits >> (4 * h32)) : 0u;
+        uint32_t vb = 0u;
+        if constexpr (kBits) vb = vbits_of(lvalid, hh) >> (4 * h32);
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
             const int kt = 8 * (v >> 2) + (v & 3);
@@ -970,10 +1031,6 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
             acc[n] = mfma32x32x16(__builtin_bit_cast(bf16x8, ab), pops, acc[n]);
         }
     };
-    auto vbits_of = [&](const uint8_t* lvalid, int hh) __attribute__((always_inline)) {
-        const uint64_t v = __builtin_amdgcn_ballot_w64(lvalid[lane] != 0);
-        return static_cast<uint32_t>(v >> (32 * hh));
-    };
 
     // Interleave patterns for the two pipeline phases (igrouplp masks: 0x8 MFMA, 0x100 DS
     // read, 0x402 VALU incl. transcendental). X: one QK MFMA per K read, with the exp work
@@ -1013,6 +1070,11 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
     float mt;
     // The tile loop, compiled twice: with the per-key validity bits (tables with holes) and
     // without; each workgroup runs one of them.
+    // Whether stage(t) issues exactly 2 NL loads per wavefront (the unchecked path), so a
+    // vmcnt bound can wait for older tiles only.
+    auto full_stage = [&](int t) __attribute__((always_inline)) {
+        return !holes && t < ntiles && (t + 1) * kKeysPerTile <= kv_end;
+    };
     auto run = [&](auto holes_tag) __attribute__((always_inline)) {
         // Prologue: tiles 0 and 1 in flight, S of tile 0 / half 0 formed, masked and maxed.
         if constexpr (F8) {
@@ -1022,16 +1084,17 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
             __syncthreads();
             convert8(lds_k8_0, lds_v8_0, lds_k0, lds_v0, sk8[0], sv8[0]);
         } else {
-            stage(0, lds_k0, lds_v0, lds_valid0);
-            if (ntiles > 1) {
-                stage(1, lds_k1, lds_v1, lds_valid1);
-                __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * NL));  // tile 0 landed (vmcnt <= tile 1's)
-            } else {
+            stage(0, lds_k0, lds_v0, lds_valid0, holes_tag);
+            if (ntiles > 1) stage(1, lds_k1, lds_v1, lds_valid1, holes_tag);
+            // Tile 0 landed: vmcnt bounded by tile 1's loads when their count is exact (the
+            // checked path may issue fewer), else everything.
+            if (full_stage(1))
+                __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * NL));
+            else
                 __builtin_amdgcn_s_waitcnt(0x0F70);
-            }
         }
         __syncthreads();
-        mask_seed(sc, 0, vbits_of(lds_valid0, 0), holes_tag);
+        mask_seed(sc, 0, lds_valid0, 0, holes_tag);
         qk_half(lds_k0, 0, sc, std::true_type{});
         const bool grow_first = max_half(sc, mt);
         rescale(grow_first, mt);
@@ -1070,7 +1133,7 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
             __builtin_amdgcn_sched_barrier(0);
             if (!skip1) {
                 exp_part(sc, 0, pop[0]);
-                if constexpr (kMask) mask_seed(sn, key0 + 32, vbits_of(valc, 1), holes_tag);
+                if constexpr (kMask) mask_seed(sn, key0 + 32, valc, 1, holes_tag);
                 qk_half(kc, 1, sn, mask_tag);
                 interleave_x();
             } else {
@@ -1102,7 +1165,7 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
                         stage8(t + 2, BL == 0 ? lds_k8_0 : lds_k8_1, BL == 0 ? lds_v8_0 : lds_v8_1,
                                vall, sk8[BL], sv8[BL]);
                 } else {
-                    if (t + 2 < ntiles) stage(t + 2, kl, vl, vall);
+                    if (t + 2 < ntiles) stage(t + 2, kl, vl, vall, holes_tag);
                 }
             }
             // X: exp of (t, 1) || QK of (t+1, 0)
@@ -1111,7 +1174,7 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
                 exp_part(sn, 0, pop[0]);
                 if constexpr (!kLast) {
                     if constexpr (kMask)
-                        mask_seed(sc, key0 + kKeysPerTile, vbits_of(valn, 0), holes_tag);
+                        mask_seed(sc, key0 + kKeysPerTile, valn, 0, holes_tag);
                     qk_half(kn, 0, sc, mask_tag);
                 }
                 if constexpr (!kLast) interleave_x();
