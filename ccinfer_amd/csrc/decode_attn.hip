@@ -59,6 +59,9 @@ constexpr int kMaxSplitTokens = 2048;  // 128 blocks: two table entries per lane
 // Wavefronts the split plan aims for: two resident per SIMD on 1024 SIMDs, two rounds.
 constexpr int64_t kTargetWaves = 4096;
 constexpr int kBalancedMinItems = 4;
+// Longest table row (positions) of the single-launch group plan: parts of at most 512
+// positions at 8 wavefronts (1024 at 4), within one split's 2048.
+constexpr int kGroupMaxCtx = 4096;
 
 struct ItemArgs {
     int num_items;
@@ -488,6 +491,91 @@ __device__ void merge_row(const float* __restrict__ ws_o, const float* __restric
     for (int x = 0; x < kPer; ++x) o[lane * kPer + x] = static_cast<__bf16>(acc[x] * inv);
 }
 
+// Per-split inputs: the split's block ids, one per lane (two registers cover 128 blocks),
+// and the Q^T operand: lane (head j, grp g) holds dims (kk*4+g)*8 .. +8 of head j (fp8:
+// the permuted order of the fp8 K loads).
+template <int D>
+struct SplitInputs {
+    int bt_lo;
+    int bt_hi;
+    bf16x8 qop[DecodeShape<D>::kSteps];
+};
+
+// Loads the inputs of a split starting at position `begin` whose table entries end at
+// position tbl_end (no more than 2048 positions).
+template <int D, bool F8>
+__device__ __forceinline__ void load_split_inputs(const __bf16* __restrict__ q,
+                                                  const int32_t* __restrict__ req_blocks,
+                                                  int mbpr, int qrow, int hq, int h, int G,
+                                                  int begin, int tbl_end, int lane,
+                                                  SplitInputs<D>& in) {
+    constexpr int S = DecodeShape<D>::kSteps;
+    const int j = lane & 15;
+    const int g = lane >> 4;
+    const int lb0 = begin / kBlock;
+    const int nblk = (tbl_end - begin + kBlock - 1) / kBlock;
+    in.bt_lo = (lane < nblk && lb0 + lane < mbpr) ? req_blocks[lb0 + lane] : -1;
+    in.bt_hi = (lane + 64 < nblk && lb0 + lane + 64 < mbpr) ? req_blocks[lb0 + lane + 64] : -1;
+    const bool live = j < G;
+    const __bf16* qv = q + (static_cast<int64_t>(qrow) * hq + h * G + (live ? j : 0)) * D;
+#pragma unroll
+    for (int kk = 0; kk < S; ++kk) {
+        const int dim0 = F8 ? 64 * (kk >> 1) + 16 * g + 8 * (kk & 1) : (kk * 4 + g) * 8;
+        u32x4 w = load16(qv + dim0);
+        if (!live) w = u32x4{0, 0, 0, 0};
+        in.qop[kk] = __builtin_bit_cast(bf16x8, w);
+    }
+}
+
+// Attention of the G query heads of kv_head h over context positions [begin, end) (at most
+// 2048) with the split's inputs: the online-softmax state of one wavefront.
+template <int D, bool F8>
+__device__ __forceinline__ void run_split(
+    const std::conditional_t<F8, uint8_t, __bf16>* __restrict__ k_cache,
+    const std::conditional_t<F8, uint8_t, __bf16>* __restrict__ v_cache,
+    const float* __restrict__ k_scale, const float* __restrict__ v_scale,
+    const SplitInputs<D>& in, int hkv, int h, int begin, int end, float scale_log2, int lane,
+    SoftmaxState<D>& st) {
+    constexpr int NV = DecodeShape<D>::kNV;
+    using Regs = std::conditional_t<F8, ChunkRegsF8<D>, ChunkRegs<D>>;
+    const int g = lane >> 4;
+    const int nblk = (end - begin + kBlock - 1) / kBlock;
+    auto block_id = [&](int jb) -> int {  // jb: wave-uniform block index within the split
+        return __builtin_amdgcn_readlane(jb < 64 ? in.bt_lo : in.bt_hi, jb & 63);
+    };
+#pragma unroll
+    for (int n = 0; n < NV; ++n) st.acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    st.m = kNegInf;
+    st.l = 0.f;
+
+    const int nchunks = (end - begin + kChunk - 1) / kChunk;
+    // Block ids of chunk c (clamped to the last chunk so prefetches are unconditional).
+    auto chunk_blocks = [&](int c, int* p0, int* p1) {
+        c = c < nchunks ? c : nchunks - 1;
+        *p0 = block_id(2 * c);
+        *p1 = (2 * c + 1 < nblk) ? block_id(2 * c + 1) : -1;
+    };
+    Regs ra, rb;
+    auto load = [&](Regs& r, int p0, int p1) {
+        if constexpr (F8)
+            load_chunk<D>(r, k_cache, v_cache, k_scale, v_scale, p0, p1, h, hkv, lane);
+        else
+            load_chunk<D>(r, k_cache, v_cache, p0, p1, h, hkv, lane);
+    };
+    int a0, a1, b0, b1;
+    chunk_blocks(0, &a0, &a1);
+    load(ra, a0, a1);
+    for (int c = 0; c < nchunks; c += 2) {
+        chunk_blocks(c + 1, &b0, &b1);
+        load(rb, b0, b1);
+        consume_chunk<D>(st, ra, in.qop, begin + c * kChunk, end, a0, a1, scale_log2, g);
+        if (c + 1 >= nchunks) break;
+        chunk_blocks(c + 2, &a0, &a1);
+        load(ra, a0, a1);
+        consume_chunk<D>(st, rb, in.qop, begin + (c + 1) * kChunk, end, b0, b1, scale_log2, g);
+    }
+}
+
 // F8: the cache holds E4M3 bytes with row scales (k_scale / v_scale); else bf16.
 template <int D, bool F8>
 __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
@@ -497,10 +585,8 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     const int32_t* __restrict__ context_lens, __bf16* __restrict__ out, float* __restrict__ ws_o,
     float* __restrict__ ws_ml, MergeDesc* __restrict__ desc, ItemArgs items, int mbpr, int hq,
     int hkv, int splits, int split_tokens, int balanced_w, int slots, float scale_log2) {
-    constexpr int S = DecodeShape<D>::kSteps;
     constexpr int NV = DecodeShape<D>::kNV;
     using Cache = std::conditional_t<F8, uint8_t, __bf16>;
-    using Regs = std::conditional_t<F8, ChunkRegsF8<D>, ChunkRegs<D>>;
     const Cache* __restrict__ k_cache = static_cast<const Cache*>(k_cache_v);
     const Cache* __restrict__ v_cache = static_cast<const Cache*>(v_cache_v);
     const int lane = threadIdx.x & 63;
@@ -557,65 +643,12 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     const int begin = s * split_tokens;
     if (begin >= ctx) return;
     const int end = min(ctx, begin + split_tokens);
-    const int32_t* req_blocks = block_table + static_cast<int64_t>(req) * mbpr;
-
-    // Block ids of this split, one per lane (two registers cover 128 blocks).
-    const int lb0 = begin / kBlock;
-    const int nblk = (end - begin + kBlock - 1) / kBlock;
-    const int bt_lo = (lane < nblk && lb0 + lane < mbpr) ? req_blocks[lb0 + lane] : -1;
-    const int bt_hi = (lane + 64 < nblk && lb0 + lane + 64 < mbpr) ? req_blocks[lb0 + lane + 64] : -1;
-    auto block_id = [&](int jb) -> int {  // jb: wave-uniform block index within the split
-        return __builtin_amdgcn_readlane(jb < 64 ? bt_lo : bt_hi, jb & 63);
-    };
-
-    // Q^T operand: lane (head j, grp g) holds dims (kk*4+g)*8 .. +8 of head j (fp8: the
-    // permuted order of the fp8 K loads).
-    bf16x8 qop[S];
-    {
-        const bool live = j < G;
-        const __bf16* qv = q + (static_cast<int64_t>(qrow) * hq + h * G + (live ? j : 0)) * D;
-#pragma unroll
-        for (int kk = 0; kk < S; ++kk) {
-            const int dim0 = F8 ? 64 * (kk >> 1) + 16 * g + 8 * (kk & 1) : (kk * 4 + g) * 8;
-            u32x4 w = load16(qv + dim0);
-            if (!live) w = u32x4{0, 0, 0, 0};
-            qop[kk] = __builtin_bit_cast(bf16x8, w);
-        }
-    }
-
+    SplitInputs<D> in;
+    load_split_inputs<D, F8>(q, block_table + static_cast<int64_t>(req) * mbpr, mbpr, qrow, hq,
+                             h, G, begin, end, lane, in);
     SoftmaxState<D> st;
-#pragma unroll
-    for (int n = 0; n < NV; ++n) st.acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-    st.m = kNegInf;
-    st.l = 0.f;
-
-    const int nchunks = (end - begin + kChunk - 1) / kChunk;
-    // Block ids of chunk c (clamped to the last chunk so prefetches are unconditional).
-    auto chunk_blocks = [&](int c, int* p0, int* p1) {
-        c = c < nchunks ? c : nchunks - 1;
-        *p0 = block_id(2 * c);
-        *p1 = (2 * c + 1 < nblk) ? block_id(2 * c + 1) : -1;
-    };
-    Regs ra, rb;
-    auto load = [&](Regs& r, int p0, int p1) {
-        if constexpr (F8)
-            load_chunk<D>(r, k_cache, v_cache, k_scale, v_scale, p0, p1, h, hkv, lane);
-        else
-            load_chunk<D>(r, k_cache, v_cache, p0, p1, h, hkv, lane);
-    };
-    int a0, a1, b0, b1;
-    chunk_blocks(0, &a0, &a1);
-    load(ra, a0, a1);
-    for (int c = 0; c < nchunks; c += 2) {
-        chunk_blocks(c + 1, &b0, &b1);
-        load(rb, b0, b1);
-        consume_chunk<D>(st, ra, qop, begin + c * kChunk, end, a0, a1, scale_log2, g);
-        if (c + 1 >= nchunks) break;
-        chunk_blocks(c + 2, &a0, &a1);
-        load(ra, a0, a1);
-        consume_chunk<D>(st, rb, qop, begin + (c + 1) * kChunk, end, b0, b1, scale_log2, g);
-    }
-
+    run_split<D, F8>(k_cache, v_cache, k_scale, v_scale, in, hkv, h, begin, end, scale_log2, lane,
+                     st);
     const float l_tot = wave_sum_xor16_32(st.l);
     const bool live = j < G;
     const int head = h * G + j;
@@ -661,6 +694,110 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     if (g == 0) {
         ws_ml[slot * 2 + 0] = st.m;
         ws_ml[slot * 2 + 1] = l_tot;
+    }
+}
+
+// Single-launch decode for batches with few (item, kv_head) groups: one workgroup of W
+// wavefronts per group, wavefront w attending over the w-th of W equal parts of the
+// context; the parts are merged through LDS with the same log-sum-exp weighting as
+// merge_row, so no second kernel and no workspace. (For many groups the balanced split plan
+// spreads ragged contexts better.)
+template <int D>
+struct GroupShape {
+    static constexpr int kWaves = D <= 128 ? 8 : 4;  // two wavefronts per SIMD at <= 256 VGPRs
+    static constexpr int kMaxG = 16;                 // LDS: kWaves * 16 * D floats = 64 KiB
+};
+
+template <int D, bool F8>
+__global__ __launch_bounds__(64 * GroupShape<D>::kWaves) void decode_group_kernel(
+    const __bf16* __restrict__ q, const void* __restrict__ k_cache_v,
+    const void* __restrict__ v_cache_v, const float* __restrict__ k_scale,
+    const float* __restrict__ v_scale, const int32_t* __restrict__ block_table,
+    const int32_t* __restrict__ context_lens, __bf16* __restrict__ out, ItemArgs items,
+    int mbpr, int hq, int hkv, float scale_log2) {
+    constexpr int W = GroupShape<D>::kWaves;
+    constexpr int NV = DecodeShape<D>::kNV;
+    constexpr int kMaxG = GroupShape<D>::kMaxG;
+    using Cache = std::conditional_t<F8, uint8_t, __bf16>;
+    __shared__ float lds_o[W * kMaxG * D];
+    __shared__ float lds_m[W * kMaxG];
+    __shared__ float lds_l[W * kMaxG];
+    const Cache* __restrict__ k_cache = static_cast<const Cache*>(k_cache_v);
+    const Cache* __restrict__ v_cache = static_cast<const Cache*>(v_cache_v);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int h = blockIdx.x % hkv;
+    const int item = blockIdx.x / hkv;
+    int req, qrow;
+    if (!resolve_item(items, item, &req, &qrow)) return;  // workgroup-uniform
+    const int G = hq / hkv;
+    // Parts are cut from the table row (mbpr blocks) in whole 32-token chunks, so every
+    // wavefront's block ids and Q are loaded together with the context length.
+    const int ctx_raw = context_lens[req];
+    const int per = ((mbpr + 1) / 2 + W - 1) / W;  // chunks per part
+    const int begin = wave * per * kChunk;
+    const int tbl_end = min(mbpr * kBlock, begin + per * kChunk);
+    SplitInputs<D> in;
+    load_split_inputs<D, F8>(q, block_table + static_cast<int64_t>(req) * mbpr, mbpr, qrow, hq,
+                             h, G, begin, max(begin, tbl_end), lane, in);
+    const int ctx = effective_ctx(ctx_raw, mbpr, items.zero_invalid);
+    if (ctx < 0) {
+        // Decode semantics: invalid context -> zeros; prefill semantics: row untouched.
+        if (items.zero_invalid) {
+            for (int x = threadIdx.x; x < G * D; x += 64 * W)
+                out[(static_cast<int64_t>(qrow) * hq + h * G) * D + x] = static_cast<__bf16>(0.0f);
+        }
+        return;
+    }
+    const int end = min(ctx, tbl_end);
+    SoftmaxState<D> st;
+    if (begin < end) {
+        run_split<D, F8>(k_cache, v_cache, k_scale, v_scale, in, hkv, h, begin, end, scale_log2,
+                         lane, st);
+    } else {
+#pragma unroll
+        for (int n = 0; n < NV; ++n) st.acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+        st.m = kNegInf;
+        st.l = 0.f;
+    }
+    const float l_tot = wave_sum_xor16_32(st.l);
+    const int j = lane & 15;
+    const int g = lane >> 4;
+    if (j < G) {
+        float* po = lds_o + (wave * kMaxG + j) * D;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int n = 0; n < NV; ++n) po[NV * (4 * g + r) + n] = st.acc[n][r];
+        if (g == 0) {
+            lds_m[wave * kMaxG + j] = st.m;
+            lds_l[wave * kMaxG + j] = l_tot;
+        }
+    }
+    __syncthreads();
+    constexpr int kPer = D / 64;
+    for (int jj = wave; jj < G; jj += W) {
+        float mmax = kNegInf;
+#pragma unroll
+        for (int w = 0; w < W; ++w) mmax = fmaxf(mmax, lds_m[w * kMaxG + jj]);
+        float acc[kPer];
+#pragma unroll
+        for (int x = 0; x < kPer; ++x) acc[x] = 0.f;
+        float lsum = 0.f;
+        if (mmax != kNegInf) {
+#pragma unroll
+            for (int w = 0; w < W; ++w) {
+                const float wt = __builtin_amdgcn_exp2f(lds_m[w * kMaxG + jj] - mmax);
+                lsum += lds_l[w * kMaxG + jj] * wt;
+#pragma unroll
+                for (int x = 0; x < kPer; ++x)
+                    acc[x] += lds_o[(w * kMaxG + jj) * D + lane * kPer + x] * wt;
+            }
+        }
+        const float inv = lsum > 0.f ? 1.f / (lsum + items.eps) : 0.f;
+        __bf16* o = out + (static_cast<int64_t>(qrow) * hq + h * G + jj) * D;
+#pragma unroll
+        for (int x = 0; x < kPer; ++x) o[lane * kPer + x] = static_cast<__bf16>(acc[x] * inv);
     }
 }
 
@@ -716,6 +853,14 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
                          const ItemArgs& it, int mbpr, int hq, int hkv, const DecodePlan& plan,
                          void* workspace, hipStream_t stream) {
     const float scale_log2 = kLog2e / sqrtf(static_cast<float>(D));
+    if (plan.group) {
+        const int64_t groups = static_cast<int64_t>(it.num_items) * hkv;
+        decode_group_kernel<D, F8><<<static_cast<unsigned>(groups),
+                                     64 * GroupShape<D>::kWaves, 0, stream>>>(
+            static_cast<const __bf16*>(q), k_cache, v_cache, k_scale, v_scale, block_table,
+            context_lens, static_cast<__bf16*>(output), it, mbpr, hq, hkv, scale_log2);
+        return hipGetLastError();
+    }
     const int64_t waves = plan.balanced
                               ? static_cast<int64_t>(plan.slots) * hkv
                               : static_cast<int64_t>(it.num_items) * hkv * plan.splits;
@@ -742,6 +887,12 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
 
 DecodePlan plan_decode(int num_items, int num_kv_heads, int max_ctx, bool allow_balanced) {
     DecodePlan p;
+    // Batches of 1-3 requests: one workgroup per (request, kv_head) merges its parts in LDS
+    // (a single launch; these batches are latency-bound).
+    if (num_items < kBalancedMinItems && max_ctx <= kGroupMaxCtx) {
+        p.group = true;
+        return p;
+    }
     const int chunks = max_ctx > 0 ? (max_ctx + kChunk - 1) / kChunk : 1;
     constexpr int kMaxChunksPerSplit = kMaxSplitTokens / kChunk;
     // Small batches keep the fixed plan: their splits are already even and the on-device
@@ -773,7 +924,7 @@ DecodePlan plan_decode(int num_items, int num_kv_heads, int max_ctx, bool allow_
 
 size_t decode_workspace_bytes(int num_items, int num_q_heads, int head_dim,
                               const DecodePlan& plan) {
-    if (!plan.balanced && plan.splits <= 1) return 0;
+    if (plan.group || (!plan.balanced && plan.splits <= 1)) return 0;
     // partial O + (m, l) per partial row, then the merge descriptors
     return desc_offset(partial_rows(num_items, num_q_heads, plan), head_dim) +
            static_cast<size_t>(num_items) * num_q_heads * sizeof(MergeDesc);

@@ -28,6 +28,7 @@ struct DecodePlan {
     bool balanced = false;
     int slots = 0;
     int wave_target = 0;
+    bool group = false;  // one workgroup per (item, kv_head), parts merged in LDS
 };
 
 constexpr int kBalancedMaxItems = 256;
