@@ -36,7 +36,7 @@ import torch
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
-from ccinfer_amd import _lib  # noqa: E402
+from ccinfer_amd import SideStream, _lib  # noqa: E402
 from ccinfer_amd import workloads as W  # noqa: E402
 
 HBM_PEAK = 8.0e12          # B/s, MI355X HBM3E
@@ -60,6 +60,8 @@ class Ops:
                                                         w.hkv, w.d, 16)
         self.ws_bytes = int(n)
         self.ws = torch.zeros(max(1, self.ws_bytes), dtype=torch.uint8, device=dev)
+        # a mixed batch's decode items run on this side stream beside the prompt tiles
+        self.side = SideStream(dev)
 
     def write(self):
         w = self.w
@@ -80,11 +82,12 @@ class Ops:
 
     def prefill(self):
         w = self.w
-        rc = self.lib.ccinfer_prefill_attention(
+        rc = self.lib.ccinfer_prefill_attention_overlap(
             w.q.data_ptr(), w.k_cache.data_ptr(), w.v_cache.data_ptr(),
             self.meta["block_table"].data_ptr(), self.meta["query_start_loc"].data_ptr(),
             self.meta["context_lens"].data_ptr(), self.out.data_ptr(), w.batch, w.q.shape[0],
-            w.mbpr, w.hq, w.hkv, w.d, 16, self.ws.data_ptr(), self.ws_bytes, self.s)
+            w.mbpr, w.hq, w.hkv, w.d, 16, self.ws.data_ptr(), self.ws_bytes, self.s,
+            *self.side.handles())
         assert rc == 0, rc
 
 

@@ -8,6 +8,7 @@ from .ops import (  # noqa: F401
     ITEM_DECODE,
     ITEM_SAMPLE,
     CcinferError,
+    SideStream,
     build_batch_metadata,
     decode_attention,
     decode_attention_fp8,
@@ -25,6 +26,7 @@ __all__ = [
     "ITEM_DECODE",
     "ITEM_SAMPLE",
     "CcinferError",
+    "SideStream",
     "build_batch_metadata",
     "decode_attention",
     "decode_attention_fp8",

@@ -36,6 +36,13 @@ SIGNATURES = {
         [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
          _vp, _c_size, _vp],
     ),
+    "ccinfer_prefill_attention_overlap": (
+        _c_int,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+         _vp, _c_size, _vp, _vp, _vp, _vp],
+    ),
+    "ccinfer_prefill_attention_fp8_overlap": (
+        _c_int, [_vp] * 9 + [_c_int] * 7 + [_vp, _c_size, _vp, _vp, _vp, _vp]),
     "ccinfer_error_message": (ctypes.c_char_p, [_c_int]),
     "ccinfer_version": (ctypes.c_char_p, []),
 }

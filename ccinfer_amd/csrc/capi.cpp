@@ -55,6 +55,15 @@ bool fits_int(int64_t v) { return v >= 0 && v <= INT_MAX; }
 
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
+// The MFMA paths move q, output and cache rows in 16-byte pieces; the reference launchers
+// take any bf16 (2-byte aligned) view, so bf16 calls with a less aligned pointer run the
+// generic kernels, and fp8 calls (MFMA only) are rejected.
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+bool fast_aligned(const void* q, const void* k_cache, const void* v_cache, const void* output) {
+    return aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && aligned16(output);
+}
+
 bool decode_shape_ok(int batch_size, int max_blocks_per_req, int num_q_heads, int num_kv_heads,
                      int head_dim, int cache_block_size) {
     if (batch_size <= 0 || max_blocks_per_req <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 ||
@@ -78,9 +87,78 @@ bool prefill_shape_ok(int batch_size, int total_query_tokens, int max_blocks_per
 
 bool prefill_uses_fast(int batch_size, int max_blocks_per_req, int num_q_heads,
                        int num_kv_heads, int head_dim, int cache_block_size) {
-    return cache_block_size == 16 && batch_size <= 4096 &&
+    (void)batch_size;
+    return cache_block_size == 16 &&
            prefill_fast_supported(num_q_heads, num_kv_heads, head_dim, max_blocks_per_req) &&
            decode_fast_supported(num_q_heads, num_kv_heads, head_dim, cache_block_size);
+}
+
+// A side stream needs both events; the events may not be NULL with a side stream.
+bool overlap_ok(void* side_stream, void* fork_event, void* join_event) {
+    return side_stream == nullptr || (fork_event != nullptr && join_event != nullptr);
+}
+
+int prefill_entry(const void* q, const void* k_cache, const void* v_cache,
+                              const int32_t* block_table, const int32_t* query_start_loc,
+                              const int32_t* context_lens, void* output, int batch_size,
+                              int total_query_tokens, int max_blocks_per_req, int num_q_heads,
+                              int num_kv_heads, int head_dim, int cache_block_size,
+                              void* workspace, size_t workspace_bytes, void* stream,
+                              const PrefillOverlap* overlap) {
+    if (!q || !k_cache || !v_cache || !block_table || !query_start_loc || !context_lens ||
+        !output)
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    if (!prefill_shape_ok(batch_size, total_query_tokens, max_blocks_per_req, num_q_heads,
+                          num_kv_heads, head_dim, cache_block_size))
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    if (!prefill_uses_fast(batch_size, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
+                           cache_block_size) ||
+        !fast_aligned(q, k_cache, v_cache, output)) {
+        return map_hip_error(generic_prefill_attention(
+            q, k_cache, v_cache, block_table, query_start_loc, context_lens, output, batch_size,
+            total_query_tokens, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
+            cache_block_size, as_stream(stream)));
+    }
+    const size_t need =
+        prefill_workspace_bytes(batch_size, total_query_tokens, max_blocks_per_req,
+                                num_q_heads, num_kv_heads, head_dim, cache_block_size);
+    if (workspace == nullptr || workspace_bytes < need) return CCINFER_ERR_INVALID_ARGUMENT;
+    return map_hip_error(prefill_attention(q, k_cache, v_cache, block_table, query_start_loc,
+                                           context_lens, output, batch_size, total_query_tokens,
+                                           max_blocks_per_req, num_q_heads, num_kv_heads,
+                                           head_dim, cache_block_size, workspace,
+                                           as_stream(stream), overlap));
+}
+
+int prefill_fp8_entry(const void* q, const void* k_cache, const void* v_cache,
+                                  const float* k_scale, const float* v_scale,
+                                  const int32_t* block_table, const int32_t* query_start_loc,
+                                  const int32_t* context_lens, void* output, int batch_size,
+                                  int total_query_tokens, int max_blocks_per_req,
+                                  int num_q_heads, int num_kv_heads, int head_dim,
+                                  int cache_block_size, void* workspace, size_t workspace_bytes,
+                                  void* stream, const PrefillOverlap* overlap) {
+    if (!q || !k_cache || !v_cache || !k_scale || !v_scale || !block_table ||
+        !query_start_loc || !context_lens || !output)
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    if (!prefill_shape_ok(batch_size, total_query_tokens, max_blocks_per_req, num_q_heads,
+                          num_kv_heads, head_dim, cache_block_size))
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    // fp8 has the pipelined MFMA path only (head_dim 64 / 128)
+    if (!prefill_uses_fast(batch_size, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
+                           cache_block_size) ||
+        !prefill_fp8_supported(head_dim, max_blocks_per_req))
+        return CCINFER_ERR_UNSUPPORTED;
+    if (!fast_aligned(q, k_cache, v_cache, output) || !aligned16(k_scale) || !aligned16(v_scale))
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    const size_t need =
+        prefill_workspace_bytes(batch_size, total_query_tokens, max_blocks_per_req,
+                                num_q_heads, num_kv_heads, head_dim, cache_block_size);
+    if (workspace == nullptr || workspace_bytes < need) return CCINFER_ERR_INVALID_ARGUMENT;
+    return map_hip_error(prefill_attention_fp8(
+        q, k_cache, v_cache, k_scale, v_scale, block_table, query_start_loc, context_lens,
+        output, batch_size, total_query_tokens, max_blocks_per_req, num_q_heads, num_kv_heads,
+        head_dim, workspace, as_stream(stream), overlap));
 }
 
 }  // namespace
@@ -178,7 +256,8 @@ int ccinfer_decode_attention(const void* q, const void* k_cache, const void* v_c
     if (!decode_shape_ok(batch_size, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
                          cache_block_size))
         return CCINFER_ERR_INVALID_ARGUMENT;
-    if (!decode_fast_supported(num_q_heads, num_kv_heads, head_dim, cache_block_size)) {
+    if (!decode_fast_supported(num_q_heads, num_kv_heads, head_dim, cache_block_size) ||
+        !fast_aligned(q, k_cache, v_cache, output)) {
         return map_hip_error(generic_decode_attention(
             q, k_cache, v_cache, block_table, context_lens, output, batch_size,
             max_blocks_per_req, num_q_heads, num_kv_heads, head_dim, cache_block_size,
@@ -227,6 +306,8 @@ int ccinfer_decode_attention_fp8(const void* q, const void* k_cache, const void*
         return CCINFER_ERR_INVALID_ARGUMENT;
     if (!decode_fast_supported(num_q_heads, num_kv_heads, head_dim, cache_block_size))
         return CCINFER_ERR_UNSUPPORTED;  // fp8 has the MFMA path only
+    if (!fast_aligned(q, k_cache, v_cache, output) || !aligned16(k_scale) || !aligned16(v_scale))
+        return CCINFER_ERR_INVALID_ARGUMENT;
     const DecodePlan plan =
         plan_decode(batch_size, num_kv_heads, max_blocks_per_req * cache_block_size, true);
     const size_t need = decode_workspace_bytes(batch_size, num_q_heads, head_dim, plan);
@@ -259,28 +340,28 @@ int ccinfer_prefill_attention(const void* q, const void* k_cache, const void* v_
                               int total_query_tokens, int max_blocks_per_req, int num_q_heads,
                               int num_kv_heads, int head_dim, int cache_block_size,
                               void* workspace, size_t workspace_bytes, void* stream) {
-    if (!q || !k_cache || !v_cache || !block_table || !query_start_loc || !context_lens ||
-        !output)
-        return CCINFER_ERR_INVALID_ARGUMENT;
-    if (!prefill_shape_ok(batch_size, total_query_tokens, max_blocks_per_req, num_q_heads,
-                          num_kv_heads, head_dim, cache_block_size))
-        return CCINFER_ERR_INVALID_ARGUMENT;
-    if (!prefill_uses_fast(batch_size, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
-                           cache_block_size)) {
-        return map_hip_error(generic_prefill_attention(
-            q, k_cache, v_cache, block_table, query_start_loc, context_lens, output, batch_size,
-            total_query_tokens, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
-            cache_block_size, as_stream(stream)));
-    }
-    const size_t need =
-        prefill_workspace_bytes(batch_size, total_query_tokens, max_blocks_per_req,
-                                num_q_heads, num_kv_heads, head_dim, cache_block_size);
-    if (workspace == nullptr || workspace_bytes < need) return CCINFER_ERR_INVALID_ARGUMENT;
-    return map_hip_error(prefill_attention(q, k_cache, v_cache, block_table, query_start_loc,
-                                           context_lens, output, batch_size, total_query_tokens,
-                                           max_blocks_per_req, num_q_heads, num_kv_heads,
-                                           head_dim, cache_block_size, workspace,
-                                           as_stream(stream)));
+    return prefill_entry(q, k_cache, v_cache, block_table, query_start_loc, context_lens, output,
+                         batch_size, total_query_tokens, max_blocks_per_req, num_q_heads,
+                         num_kv_heads, head_dim, cache_block_size, workspace, workspace_bytes,
+                         stream, nullptr);
+}
+
+int ccinfer_prefill_attention_overlap(const void* q, const void* k_cache, const void* v_cache,
+                                      const int32_t* block_table,
+                                      const int32_t* query_start_loc,
+                                      const int32_t* context_lens, void* output, int batch_size,
+                                      int total_query_tokens, int max_blocks_per_req,
+                                      int num_q_heads, int num_kv_heads, int head_dim,
+                                      int cache_block_size, void* workspace,
+                                      size_t workspace_bytes, void* stream, void* side_stream,
+                                      void* fork_event, void* join_event) {
+    if (!overlap_ok(side_stream, fork_event, join_event)) return CCINFER_ERR_INVALID_ARGUMENT;
+    const PrefillOverlap ov{as_stream(side_stream), static_cast<hipEvent_t>(fork_event),
+                            static_cast<hipEvent_t>(join_event)};
+    return prefill_entry(q, k_cache, v_cache, block_table, query_start_loc, context_lens, output,
+                         batch_size, total_query_tokens, max_blocks_per_req, num_q_heads,
+                         num_kv_heads, head_dim, cache_block_size, workspace, workspace_bytes,
+                         stream, &ov);
 }
 
 int ccinfer_prefill_attention_fp8(const void* q, const void* k_cache, const void* v_cache,
@@ -291,25 +372,26 @@ int ccinfer_prefill_attention_fp8(const void* q, const void* k_cache, const void
                                   int num_q_heads, int num_kv_heads, int head_dim,
                                   int cache_block_size, void* workspace, size_t workspace_bytes,
                                   void* stream) {
-    if (!q || !k_cache || !v_cache || !k_scale || !v_scale || !block_table ||
-        !query_start_loc || !context_lens || !output)
-        return CCINFER_ERR_INVALID_ARGUMENT;
-    if (!prefill_shape_ok(batch_size, total_query_tokens, max_blocks_per_req, num_q_heads,
-                          num_kv_heads, head_dim, cache_block_size))
-        return CCINFER_ERR_INVALID_ARGUMENT;
-    // fp8 has the pipelined MFMA path only (head_dim 64 / 128)
-    if (!prefill_uses_fast(batch_size, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
-                           cache_block_size) ||
-        (head_dim != 64 && head_dim != 128))
-        return CCINFER_ERR_UNSUPPORTED;
-    const size_t need =
-        prefill_workspace_bytes(batch_size, total_query_tokens, max_blocks_per_req,
-                                num_q_heads, num_kv_heads, head_dim, cache_block_size);
-    if (workspace == nullptr || workspace_bytes < need) return CCINFER_ERR_INVALID_ARGUMENT;
-    return map_hip_error(prefill_attention_fp8(
-        q, k_cache, v_cache, k_scale, v_scale, block_table, query_start_loc, context_lens,
-        output, batch_size, total_query_tokens, max_blocks_per_req, num_q_heads, num_kv_heads,
-        head_dim, workspace, as_stream(stream)));
+    return prefill_fp8_entry(q, k_cache, v_cache, k_scale, v_scale, block_table, query_start_loc,
+                             context_lens, output, batch_size, total_query_tokens,
+                             max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
+                             cache_block_size, workspace, workspace_bytes, stream, nullptr);
+}
+
+int ccinfer_prefill_attention_fp8_overlap(
+    const void* q, const void* k_cache, const void* v_cache, const float* k_scale,
+    const float* v_scale, const int32_t* block_table, const int32_t* query_start_loc,
+    const int32_t* context_lens, void* output, int batch_size, int total_query_tokens,
+    int max_blocks_per_req, int num_q_heads, int num_kv_heads, int head_dim,
+    int cache_block_size, void* workspace, size_t workspace_bytes, void* stream,
+    void* side_stream, void* fork_event, void* join_event) {
+    if (!overlap_ok(side_stream, fork_event, join_event)) return CCINFER_ERR_INVALID_ARGUMENT;
+    const PrefillOverlap ov{as_stream(side_stream), static_cast<hipEvent_t>(fork_event),
+                            static_cast<hipEvent_t>(join_event)};
+    return prefill_fp8_entry(q, k_cache, v_cache, k_scale, v_scale, block_table, query_start_loc,
+                             context_lens, output, batch_size, total_query_tokens,
+                             max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
+                             cache_block_size, workspace, workspace_bytes, stream, &ov);
 }
 
 const char* ccinfer_error_message(int code) {

@@ -1,8 +1,9 @@
 // HipBackend: the MI355X implementation of the hot-path backend ops (the reference's
 // CudaBackend::{prefill,decode}_attention_impl / write_kv_cache_impl,
-// src/backend/cuda/cuda_backend.cpp:162-187). It owns one HIP stream (default priority)
-// and one device workspace for the split-KV partials and the prefill work list; the
-// workspace grows on demand and is reused across calls.
+// src/backend/cuda/cuda_backend.cpp:162-187). It owns one HIP stream (default priority),
+// a side stream plus fork/join events on which a mixed prefill batch's decode items run
+// beside its prompt tiles, and one device workspace for the split-KV partials and the
+// prefill work list; the workspace grows on demand and is reused across calls.
 #pragma once
 
 #include <hip/hip_bf16.h>
@@ -40,6 +41,9 @@ private:
 
     int device_id_ = 0;
     hipStream_t stream_ = nullptr;
+    hipStream_t side_stream_ = nullptr;
+    hipEvent_t fork_event_ = nullptr;
+    hipEvent_t join_event_ = nullptr;
     void* workspace_ = nullptr;
     size_t workspace_bytes_ = 0;
 };

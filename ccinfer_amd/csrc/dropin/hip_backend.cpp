@@ -33,12 +33,24 @@ Result<std::unique_ptr<HipBackend>> HipBackend::create(int device_id) {
     if (auto r = check_hip(hipSetDevice(device_id)); !r) return unexpected(r.error());
     if (auto r = check_hip(hipStreamCreateWithFlags(&b->stream_, hipStreamNonBlocking)); !r)
         return unexpected(r.error());
+    // The side stream a mixed prefill batch's decode items run on, and its fork / join events
+    // (both streams at the default priority).
+    if (auto r = check_hip(hipStreamCreateWithFlags(&b->side_stream_, hipStreamNonBlocking)); !r)
+        return unexpected(r.error());
+    if (auto r = check_hip(hipEventCreateWithFlags(&b->fork_event_, hipEventDisableTiming)); !r)
+        return unexpected(r.error());
+    if (auto r = check_hip(hipEventCreateWithFlags(&b->join_event_, hipEventDisableTiming)); !r)
+        return unexpected(r.error());
     return b;
 }
 
 HipBackend::~HipBackend() {
     if (stream_ != nullptr) (void)hipStreamSynchronize(stream_);
+    if (side_stream_ != nullptr) (void)hipStreamSynchronize(side_stream_);
     if (workspace_ != nullptr) (void)hipFree(workspace_);
+    if (fork_event_ != nullptr) (void)hipEventDestroy(fork_event_);
+    if (join_event_ != nullptr) (void)hipEventDestroy(join_event_);
+    if (side_stream_ != nullptr) (void)hipStreamDestroy(side_stream_);
     if (stream_ != nullptr) (void)hipStreamDestroy(stream_);
 }
 
@@ -48,8 +60,10 @@ Result<void*> HipBackend::workspace(size_t bytes) {
     if (bytes == 0) return static_cast<void*>(nullptr);
     if (bytes > workspace_bytes_) {
         if (workspace_ != nullptr) {
-            // The old buffer may still be read by work queued on our stream.
+            // The old buffer may still be read by work queued on our streams.
             if (auto r = check_hip(hipStreamSynchronize(stream_)); !r) return unexpected(r.error());
+            if (auto r = check_hip(hipStreamSynchronize(side_stream_)); !r)
+                return unexpected(r.error());
             (void)hipFree(workspace_);
             workspace_ = nullptr;
             workspace_bytes_ = 0;
@@ -68,10 +82,11 @@ Result<void> HipBackend::prefill_attention_impl<__hip_bfloat16>(const PrefillAtt
                                                        p.cache_block_size_);
     auto ws = workspace(need);
     if (!ws) return unexpected(ws.error());
-    return check(ccinfer_prefill_attention(
+    return check(ccinfer_prefill_attention_overlap(
         p.q_, p.k_cache_, p.v_cache_, p.block_table_, p.query_start_loc_, p.context_lens_,
         p.output_, p.batch_size_, p.num_tokens_, p.max_blocks_per_req_, p.num_q_heads_,
-        p.num_kv_heads_, p.head_dim_, p.cache_block_size_, *ws, need, stream_));
+        p.num_kv_heads_, p.head_dim_, p.cache_block_size_, *ws, need, stream_, side_stream_,
+        fork_event_, join_event_));
 }
 
 template <>

@@ -65,16 +65,27 @@ hipError_t decode_attention(const void* q, const void* k_cache, const void* v_ca
 bool prefill_fast_supported(int num_q_heads, int num_kv_heads, int head_dim,
                             int max_blocks_per_req);
 
+// The fp8 prefill (pipelined path, head_dim 64 / 128, table row staged in LDS).
+bool prefill_fp8_supported(int head_dim, int max_blocks_per_req);
+
 size_t prefill_workspace_bytes(int batch_size, int total_query_tokens, int max_blocks_per_req,
                                int num_q_heads, int num_kv_heads, int head_dim,
                                int block_size);
+
+// Caller-owned side stream and events a mixed batch's decode items may run on (see
+// ccinfer_prefill_attention_overlap).
+struct PrefillOverlap {
+    hipStream_t side = nullptr;
+    hipEvent_t fork = nullptr;
+    hipEvent_t join = nullptr;
+};
 
 hipError_t prefill_attention(const void* q, const void* k_cache, const void* v_cache,
                              const int32_t* block_table, const int32_t* query_start_loc,
                              const int32_t* context_lens, void* output, int batch_size,
                              int total_query_tokens, int max_blocks_per_req, int num_q_heads,
                              int num_kv_heads, int head_dim, int block_size, void* workspace,
-                             hipStream_t stream);
+                             hipStream_t stream, const PrefillOverlap* overlap = nullptr);
 
 // ---- fp8 (OCP E4M3) KV cache, one fp32 scale per cache row -------------------------
 // Scale of (slot, kv_head) at ((slot / kFp8Block) * Hkv + kv_head) * kFp8Block + slot % 16.
@@ -102,7 +113,8 @@ hipError_t prefill_attention_fp8(const void* q, const void* k_cache, const void*
                                  const int32_t* context_lens, void* output, int batch_size,
                                  int total_query_tokens, int max_blocks_per_req,
                                  int num_q_heads, int num_kv_heads, int head_dim,
-                                 void* workspace, hipStream_t stream);
+                                 void* workspace, hipStream_t stream,
+                                 const PrefillOverlap* overlap = nullptr);
 
 // ---- per-step batch metadata built on the device ------------------------------
 constexpr int kItemDecode = 1;  // item flag: decode item (exactly one new token)

@@ -24,10 +24,9 @@
 //      diagonal / ragged tiles.
 //   3. single-token requests go through the split-KV decode kernel (decode_attn.hip) with
 //      prefill semantics (no 1e-6 in the denominator, bad rows left untouched); for batches
-//      of 32+ requests on a library-owned side stream forked after the planner and joined
-//      back at the end, so the memory-bound decode items run beside the MFMA-bound tiles.
-#include <mutex>
-#include <optional>
+//      of 32+ requests on the caller's side stream (when given) forked after the planner and
+//      joined back at the end, so the memory-bound decode items run beside the MFMA-bound
+//      tiles.
 #include <type_traits>
 
 #include "attn_common.hpp"
@@ -109,14 +108,19 @@ __device__ void block_inclusive_scan(int* a, int n, int* part) {
 // ---------------------------------------------------------------------------
 // Planner: one workgroup of 1024 threads.
 // ws layout: counts[0] = #tiles, counts[1] = #decode items; tiles[max_tiles]; dec[B].
+// kBig: more than kMaxPlanRequests requests; the per-request arrays then live in the
+// workspace (big_ntiles / big_scan, B ints each) instead of LDS.
 // ---------------------------------------------------------------------------
+template <bool kBig>
 __global__ __launch_bounds__(1024) void prefill_plan_kernel(
     const int32_t* __restrict__ qsl, const int32_t* __restrict__ context_lens, int batch_size,
     int total_tokens, int tile_tokens, int32_t* __restrict__ counts,
     TileEntry* __restrict__ tiles, int32_t* __restrict__ dec_req, uint32_t* __restrict__ zero_row,
-    int zero_words) {
-    __shared__ int s_ntiles[kMaxPlanRequests];
-    __shared__ int s_scan[kMaxPlanRequests];
+    int zero_words, int* __restrict__ big_ntiles, int* __restrict__ big_scan) {
+    __shared__ int lds_ntiles[kBig ? 1 : kMaxPlanRequests];
+    __shared__ int lds_scan[kBig ? 1 : kMaxPlanRequests];
+    int* s_ntiles = kBig ? big_ntiles : lds_ntiles;
+    int* s_scan = kBig ? big_scan : lds_scan;
     __shared__ int s_hist[kBuckets];
     __shared__ int s_hscan[kBuckets];
     __shared__ int s_part[16];
@@ -641,7 +645,9 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
     __shared__ uint8_t lds_valid0[kKeysPerTile];
     __shared__ uint8_t lds_valid1[kKeysPerTile];
     __shared__ uint8_t lds_valid2[kKeysPerTile];
-    __shared__ int32_t lds_bt[kMaxTableLds];
+    // The block table in LDS (fp8 staging only; the bf16 staging reads its block ids from
+    // global memory into a register window).
+    __shared__ int32_t lds_bt[F8 ? kMaxTableLds : 1];
     __shared__ int s_holes;
 
     const int G = hq / hkv;
@@ -688,9 +694,10 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
     const int max_fast_pb = static_cast<int>(
         min(static_cast<int64_t>(0x7fffffff),
             static_cast<int64_t>(0xffffffffll / (static_cast<int64_t>(kBlock) * hkv * D * 2)) - 1));
-    for (int lb = threadIdx.x; lb < ntiles * (kKeysPerTile / kBlock); lb += kPipeThreads) {
+    for (int lb = threadIdx.x; lb < (F8 ? ntiles * (kKeysPerTile / kBlock) : nblk);
+         lb += kPipeThreads) {
         const int pb = lb < nblk ? req_blocks[lb] : -1;
-        lds_bt[lb] = pb;
+        if constexpr (F8) lds_bt[lb] = pb;
         if (lb < nblk && (pb < 0 || pb > max_fast_pb)) s_holes = 1;
     }
 
@@ -737,9 +744,9 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
     // Rows past kv_end or in unmapped blocks are not loaded: their LDS slots are written with
     // zeros instead, and the mask gives them probability 0.
     // Block ids this wavefront stages, held in one register: lane i has the id of load
-    // i % NL's cache block in tile kWin * bt_win + i / NL. A stage reads its ids with
-    // readlane (no LDS round trip); the window is reloaded from the LDS table every kWin
-    // tiles.
+    // i % NL's cache block in tile kWin * bt_win + i / NL (-1 past the visible table). A
+    // stage reads its ids with readlane; the window is reloaded from the table row every
+    // kWin tiles, so the table length is not bounded by LDS.
     constexpr int kWin = 64 / NL;
 #if defined(__HIP_DEVICE_COMPILE__)
     // (device pass only: the host pass cannot type the buffer builtins, and a kernel
@@ -754,8 +761,8 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
     auto bt_window = [&](int win) __attribute__((always_inline)) {
         const int x = lane % NL;
         const int blk = ((x * kPipeWaves + wave) * 64 / CPR) >> 4;
-        btw = lds_bt[min((win * kWin + lane / NL) * (kKeysPerTile / kBlock) + blk,
-                         kMaxTableLds - 1)];
+        const int lb = (win * kWin + lane / NL) * (kKeysPerTile / kBlock) + blk;
+        btw = lb < nblk ? req_blocks[lb] : -1;
         bt_win = win;
     };
     // kHoles: the table has holes in the visible range; then every tile goes through the
@@ -1281,7 +1288,7 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
 }
 
 struct PrefillLayout {
-    size_t counts_off, zero_off, tiles_off, dec_off, decode_ws_off, total;
+    size_t counts_off, zero_off, tiles_off, dec_off, big_off, decode_ws_off, total;
     int max_tiles;
     int tile_tokens;
     DecodePlan plan;
@@ -1311,6 +1318,9 @@ PrefillLayout prefill_layout(int batch_size, int total_query_tokens, int max_blo
     off = align256(off + static_cast<size_t>(L.max_tiles) * sizeof(TileEntry));
     L.dec_off = off;
     off = align256(off + static_cast<size_t>(batch_size) * sizeof(int32_t));
+    L.big_off = off;  // the planner's per-request arrays for batches it cannot keep in LDS
+    if (batch_size > kMaxPlanRequests)
+        off = align256(off + 2 * static_cast<size_t>(batch_size) * sizeof(int32_t));
     L.decode_ws_off = off;
     off = align256(off + decode_workspace_bytes(batch_size, num_q_heads, head_dim, L.plan));
     L.total = off;
@@ -1354,9 +1364,16 @@ hipError_t launch_tiles(const void* q, const void* k_cache, const void* v_cache,
 bool prefill_fast_supported(int num_q_heads, int num_kv_heads, int head_dim,
                             int max_blocks_per_req) {
     if (num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0) return false;
-    if (max_blocks_per_req > kMaxTableLds) return false;
     const int G = num_q_heads / num_kv_heads;
-    return G <= 16 && (head_dim == 64 || head_dim == 128 || head_dim == 256);
+    if (G > 16) return false;
+    // head_dim 64 / 128 (bf16) stage any table length; the head_dim-256 kernel and the fp8
+    // staging keep the table row in LDS.
+    if (head_dim == 64 || head_dim == 128) return true;
+    return head_dim == 256 && max_blocks_per_req <= kMaxTableLds;
+}
+
+bool prefill_fp8_supported(int head_dim, int max_blocks_per_req) {
+    return pipe_head_dim(head_dim) && max_blocks_per_req <= kMaxTableLds;
 }
 
 size_t prefill_workspace_bytes(int batch_size, int total_query_tokens, int max_blocks_per_req,
@@ -1369,74 +1386,11 @@ size_t prefill_workspace_bytes(int batch_size, int total_query_tokens, int max_b
 
 namespace {
 
-// Fork/join onto one library-owned side stream per device (default priority, non-blocking),
-// created on first use. Construction records an event on the caller's stream and makes the
-// side stream wait for it; join() records an event on the side stream and makes the caller's
-// stream wait for it. Nothing is synchronised on the host, and the pattern is a legal
-// fork/join under stream capture. A mutex held from fork to join keeps concurrent callers
-// from interleaving their records and waits on the shared events; their side-stream work
-// serialises on the one side stream.
+// Mixed batches of at least this many requests run their decode items on the caller's side
+// stream (when one is given) beside the tile kernel; smaller batches -- typically pure
+// prompt batches with no decode items -- keep them after the tiles, where their near-empty
+// launches take no CUs from the tiles.
 constexpr int kOverlapMinRequests = 32;
-
-class SideStream {
-  public:
-    explicit SideStream(hipStream_t stream) : stream_(stream), lock_(mutex()) {
-        int dev = 0;
-        err_ = hipGetDevice(&dev);
-        if (err_ != hipSuccess) return;
-        if (dev < 0 || dev >= kMaxDevices) {
-            err_ = hipErrorInvalidDevice;
-            return;
-        }
-        State& st = state()[dev];
-        if (st.side == nullptr) {
-            err_ = hipStreamCreateWithFlags(&st.side, hipStreamNonBlocking);
-            if (err_ == hipSuccess)
-                err_ = hipEventCreateWithFlags(&st.fork, hipEventDisableTiming);
-            if (err_ == hipSuccess)
-                err_ = hipEventCreateWithFlags(&st.join, hipEventDisableTiming);
-            if (err_ != hipSuccess) {
-                st = State{};
-                return;
-            }
-        }
-        st_ = &st;
-        err_ = hipEventRecord(st.fork, stream_);
-        if (err_ == hipSuccess) err_ = hipStreamWaitEvent(st.side, st.fork, 0);
-    }
-    hipError_t error() const { return err_; }
-    hipStream_t stream() const { return st_->side; }
-    hipError_t join() {
-        hipError_t e = hipEventRecord(st_->join, st_->side);
-        if (e == hipSuccess) e = hipStreamWaitEvent(stream_, st_->join, 0);
-        joined_ = true;
-        return e;
-    }
-    ~SideStream() {
-        if (st_ != nullptr && !joined_) (void)join();  // error paths still rejoin
-    }
-
-  private:
-    static constexpr int kMaxDevices = 64;
-    struct State {
-        hipStream_t side = nullptr;
-        hipEvent_t fork = nullptr;
-        hipEvent_t join = nullptr;
-    };
-    static std::mutex& mutex() {
-        static std::mutex m;
-        return m;
-    }
-    static State* state() {
-        static State s[kMaxDevices];
-        return s;
-    }
-    hipStream_t stream_;
-    std::lock_guard<std::mutex> lock_;
-    State* st_ = nullptr;
-    hipError_t err_ = hipSuccess;
-    bool joined_ = false;
-};
 
 }  // namespace
 
@@ -1448,8 +1402,8 @@ hipError_t prefill_impl(const void* q, const void* k_cache, const void* v_cache,
                         const int32_t* query_start_loc, const int32_t* context_lens,
                         void* output, int batch_size, int total_query_tokens,
                         int max_blocks_per_req, int num_q_heads, int num_kv_heads, int head_dim,
-                        int block_size, void* workspace, hipStream_t stream) {
-    if (batch_size > kMaxPlanRequests) return hipErrorInvalidValue;
+                        int block_size, void* workspace, hipStream_t stream,
+                        const PrefillOverlap* overlap) {
     const PrefillLayout L = prefill_layout(batch_size, total_query_tokens, max_blocks_per_req,
                                            num_q_heads, num_kv_heads, head_dim, block_size);
     char* ws = static_cast<char*>(workspace);
@@ -1457,18 +1411,24 @@ hipError_t prefill_impl(const void* q, const void* k_cache, const void* v_cache,
     TileEntry* tiles = reinterpret_cast<TileEntry*>(ws + L.tiles_off);
     int32_t* dec = reinterpret_cast<int32_t*>(ws + L.dec_off);
     uint32_t* zero_row = reinterpret_cast<uint32_t*>(ws + L.zero_off);
-    prefill_plan_kernel<<<1, 1024, 0, stream>>>(query_start_loc, context_lens, batch_size,
-                                                total_query_tokens, L.tile_tokens, counts, tiles,
-                                                dec, zero_row, head_dim / 2);
+    if (batch_size > kMaxPlanRequests) {
+        int* big = reinterpret_cast<int*>(ws + L.big_off);
+        prefill_plan_kernel<true><<<1, 1024, 0, stream>>>(
+            query_start_loc, context_lens, batch_size, total_query_tokens, L.tile_tokens, counts,
+            tiles, dec, zero_row, head_dim / 2, big, big + batch_size);
+    } else {
+        prefill_plan_kernel<false><<<1, 1024, 0, stream>>>(
+            query_start_loc, context_lens, batch_size, total_query_tokens, L.tile_tokens, counts,
+            tiles, dec, zero_row, head_dim / 2, nullptr, nullptr);
+    }
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     // Single-token requests of a mixed batch go through the split-KV decode (prefill
-    // semantics). Batches of kOverlapMinRequests or more run them on a side stream,
-    // concurrently with the tile kernel: they write other output rows and other workspace,
-    // and the memory-bound decode work fills CUs the MFMA-bound tiles leave idle (configs[3]
-    // of the benchmark: 0.98 -> 0.94 ms). Small batches -- typically pure prompt batches with
-    // no decode items at all -- keep them on the caller's stream after the tiles: there the
-    // near-empty decode launches would only take CUs from the tiles.
+    // semantics). Given the caller's side stream and events, batches of kOverlapMinRequests
+    // or more run them there, concurrently with the tile kernel: they write other output rows
+    // and other workspace, and the memory-bound decode work fills CUs the MFMA-bound tiles
+    // leave idle. The fork and join are event records and waits only (no host sync), which
+    // is also legal under stream capture.
     DecodeItems items;
     items.num_items = batch_size;
     items.item_count = counts + 1;
@@ -1487,11 +1447,12 @@ hipError_t prefill_impl(const void* q, const void* k_cache, const void* v_cache,
                                     items, max_blocks_per_req, num_q_heads, num_kv_heads,
                                     head_dim, block_size, L.plan, ws + L.decode_ws_off, s);
     };
-    std::optional<SideStream> side;
-    if (batch_size >= kOverlapMinRequests) {
-        side.emplace(stream);
-        if (side->error() != hipSuccess) return side->error();
-        err = launch_decode_items(side->stream());
+    const bool fork = overlap != nullptr && overlap->side != nullptr &&
+                      batch_size >= kOverlapMinRequests;
+    if (fork) {
+        err = hipEventRecord(overlap->fork, stream);
+        if (err == hipSuccess) err = hipStreamWaitEvent(overlap->side, overlap->fork, 0);
+        if (err == hipSuccess) err = launch_decode_items(overlap->side);
         if (err != hipSuccess) return err;
     }
     switch (head_dim) {
@@ -1519,8 +1480,14 @@ hipError_t prefill_impl(const void* q, const void* k_cache, const void* v_cache,
         default:
             return hipErrorInvalidValue;
     }
+    if (fork) {
+        // join even when the tile launch failed, so the side stream's work is ordered
+        const hipError_t je = hipEventRecord(overlap->join, overlap->side);
+        const hipError_t jw = je == hipSuccess ? hipStreamWaitEvent(stream, overlap->join, 0) : je;
+        return err != hipSuccess ? err : jw;
+    }
     if (err != hipSuccess) return err;
-    return side ? side->join() : launch_decode_items(stream);
+    return launch_decode_items(stream);
 }
 
 }  // namespace
@@ -1530,11 +1497,11 @@ hipError_t prefill_attention(const void* q, const void* k_cache, const void* v_c
                              const int32_t* context_lens, void* output, int batch_size,
                              int total_query_tokens, int max_blocks_per_req, int num_q_heads,
                              int num_kv_heads, int head_dim, int block_size, void* workspace,
-                             hipStream_t stream) {
+                             hipStream_t stream, const PrefillOverlap* overlap) {
     return prefill_impl<false>(q, k_cache, v_cache, nullptr, nullptr, block_table,
                                query_start_loc, context_lens, output, batch_size,
                                total_query_tokens, max_blocks_per_req, num_q_heads, num_kv_heads,
-                               head_dim, block_size, workspace, stream);
+                               head_dim, block_size, workspace, stream, overlap);
 }
 
 hipError_t prefill_attention_fp8(const void* q, const void* k_cache, const void* v_cache,
@@ -1543,12 +1510,13 @@ hipError_t prefill_attention_fp8(const void* q, const void* k_cache, const void*
                                  const int32_t* context_lens, void* output, int batch_size,
                                  int total_query_tokens, int max_blocks_per_req,
                                  int num_q_heads, int num_kv_heads, int head_dim,
-                                 void* workspace, hipStream_t stream) {
+                                 void* workspace, hipStream_t stream,
+                                 const PrefillOverlap* overlap) {
     if (!pipe_head_dim(head_dim)) return hipErrorInvalidValue;
     return prefill_impl<true>(q, k_cache, v_cache, k_scale, v_scale, block_table,
                               query_start_loc, context_lens, output, batch_size,
                               total_query_tokens, max_blocks_per_req, num_q_heads, num_kv_heads,
-                              head_dim, kBlock, workspace, stream);
+                              head_dim, kBlock, workspace, stream, overlap);
 }
 
 }  // namespace ccinfer::hipk

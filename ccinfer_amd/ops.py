@@ -61,6 +61,23 @@ def _stream() -> int:
     return torch.cuda.current_stream().cuda_stream
 
 
+class SideStream:
+    """A side stream with its fork/join events, for prefill_attention(..., overlap=...): a
+    mixed batch's decode items then run there beside the prompt tiles. Owned by the caller
+    (the library keeps no streams); one per concurrent caller."""
+
+    def __init__(self, device=None):
+        self.stream = torch.cuda.Stream(device=device)
+        self.fork = torch.cuda.Event()
+        self.join = torch.cuda.Event()
+        # torch creates an event on its first record
+        self.fork.record(self.stream)
+        self.join.record(self.stream)
+
+    def handles(self):
+        return self.stream.cuda_stream, self.fork.cuda_event, self.join.cuda_event
+
+
 def _kv_shape(k_cache: torch.Tensor):
     """(num_slots, num_kv_heads, head_dim) of a 3-D or 4-D cache tensor."""
     if k_cache.dim() == 4:
@@ -297,7 +314,8 @@ def prefill_attention_fp8(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch
                           block_table: torch.Tensor, query_start_loc: torch.Tensor,
                           context_lens: torch.Tensor, output: Optional[torch.Tensor] = None,
                           cache_block_size: int = 16,
-                          workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                          workspace: Optional[torch.Tensor] = None,
+                          overlap: Optional[SideStream] = None) -> torch.Tensor:
     """prefill_attention over an fp8 cache written by write_kv_cache_fp8."""
     op = "prefill_attention_fp8"
     _dev_tensor(q, torch.bfloat16, op)
@@ -320,10 +338,13 @@ def prefill_attention_fp8(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch
     mbpr = block_table.shape[1]
     need = prefill_workspace_size(b, total, mbpr, hq, hkv, d, cache_block_size)
     ws, ws_bytes = _workspace(need, q.device, workspace)
-    _check(_lib.load().ccinfer_prefill_attention_fp8(
-        _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale), _ptr(block_table),
-        _ptr(query_start_loc), _ptr(context_lens), _ptr(output), b, total, mbpr, hq, hkv, d,
-        cache_block_size, _ptr(ws), ws_bytes, _stream()), op)
+    args = (_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale),
+            _ptr(block_table), _ptr(query_start_loc), _ptr(context_lens), _ptr(output), b, total,
+            mbpr, hq, hkv, d, cache_block_size, _ptr(ws), ws_bytes, _stream())
+    if overlap is None:
+        _check(_lib.load().ccinfer_prefill_attention_fp8(*args), op)
+    else:
+        _check(_lib.load().ccinfer_prefill_attention_fp8_overlap(*args, *overlap.handles()), op)
     return output
 
 
@@ -331,11 +352,13 @@ def prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
                       block_table: torch.Tensor, query_start_loc: torch.Tensor,
                       context_lens: torch.Tensor, output: Optional[torch.Tensor] = None,
                       cache_block_size: int = 16,
-                      workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                      workspace: Optional[torch.Tensor] = None,
+                      overlap: Optional[SideStream] = None) -> torch.Tensor:
     """Paged causal prefill attention (prefill_attn.cu:43-242 semantics); returns output.
 
     Rows the reference leaves unwritten (requests with context_len < query_len) keep the
-    contents of `output` (uninitialised when `output` is None).
+    contents of `output` (uninitialised when `output` is None). With `overlap`, a mixed
+    batch's decode items run on its side stream beside the prompt tiles.
     """
     op = "prefill_attention"
     for t in (q, k_cache, v_cache):
@@ -354,8 +377,11 @@ def prefill_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
     mbpr = block_table.shape[1]
     need = prefill_workspace_size(b, total, mbpr, hq, hkv, d, cache_block_size)
     ws, ws_bytes = _workspace(need, q.device, workspace)
-    _check(_lib.load().ccinfer_prefill_attention(
-        _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(block_table), _ptr(query_start_loc),
-        _ptr(context_lens), _ptr(output), b, total, mbpr, hq, hkv, d, cache_block_size, _ptr(ws),
-        ws_bytes, _stream()), op)
+    args = (_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(block_table), _ptr(query_start_loc),
+            _ptr(context_lens), _ptr(output), b, total, mbpr, hq, hkv, d, cache_block_size,
+            _ptr(ws), ws_bytes, _stream())
+    if overlap is None:
+        _check(_lib.load().ccinfer_prefill_attention(*args), op)
+    else:
+        _check(_lib.load().ccinfer_prefill_attention_overlap(*args, *overlap.handles()), op)
     return output

@@ -19,8 +19,15 @@
  * ccinfer::ErrorCode (src/base/error_code.h:8-45) -- the same codes the reference returns
  * through Result<void>.
  *
- * Thread safety: stateless and re-entrant; concurrent calls on different streams must use
- * different workspaces.
+ * Thread safety: stateless and re-entrant (the library keeps no global state); concurrent
+ * calls on different streams must use different workspaces.
+ *
+ * Alignment: the reference launchers accept any bf16 (2-byte aligned) view. The MFMA paths
+ * move q, output and K/V cache rows in 16-byte pieces, so bf16 decode / prefill calls with
+ * a q, output, k_cache or v_cache pointer that is not 16-byte aligned run on the generic
+ * kernels instead (same results, slower); the fp8 calls, which have the MFMA paths only,
+ * return CCINFER_ERR_INVALID_ARGUMENT for such pointers (and for k_scale / v_scale not
+ * 16-byte aligned).
  */
 #ifndef CCINFER_ATTN_H
 #define CCINFER_ATTN_H
@@ -108,7 +115,8 @@ size_t ccinfer_decode_workspace_size(int batch_size, int max_blocks_per_req, int
  * [max_blocks_per_req] int32; context_lens: [batch_size] int32, including the current
  * token (whose K/V must already be written). cache_block_size must be 16 and head_dim one
  * of {32,64,80,96,112,120,128,192,256} (as in the reference). Unlike the reference, there
- * is no context-length ceiling (split-KV). */
+ * is no context-length ceiling (split-KV). Batches of 1-3 requests with table rows of at
+ * most 4096 positions run in a single launch and need no workspace. */
 int ccinfer_decode_attention(const void* q, const void* k_cache, const void* v_cache,
                              const int32_t* block_table, const int32_t* context_lens,
                              void* output, int batch_size, int max_blocks_per_req,
@@ -154,7 +162,10 @@ size_t ccinfer_prefill_workspace_size(int batch_size, int total_query_tokens,
  * q, output: [total_query_tokens][num_q_heads][head_dim] bf16; query_start_loc:
  * [batch_size + 1]; context_lens[r] = prefix_r + query_len_r; query i of request r sees
  * cache positions [0, prefix_r + i]. Mixed batches (single-token decode items next to
- * prompt chunks) are accepted, as in the reference. head_dim <= 256. */
+ * prompt chunks) are accepted, as in the reference. head_dim <= 256. As in the reference,
+ * neither the batch size nor the table length is bounded (the MFMA path covers head_dim 64
+ * and 128 at any size, head_dim 256 up to 4096 blocks per table row). A mixed batch's
+ * decode items run after the prompt tiles on `stream`. */
 int ccinfer_prefill_attention(const void* q, const void* k_cache, const void* v_cache,
                               const int32_t* block_table, const int32_t* query_start_loc,
                               const int32_t* context_lens, void* output, int batch_size,
@@ -162,11 +173,31 @@ int ccinfer_prefill_attention(const void* q, const void* k_cache, const void* v_
                               int num_kv_heads, int head_dim, int cache_block_size,
                               void* workspace, size_t workspace_bytes, void* stream);
 
+/* ccinfer_prefill_attention with the decode items of a mixed batch (of at least 32
+ * requests) run on the caller's side_stream (a hipStream_t) concurrently with the prompt
+ * tiles on `stream`: the call records fork_event on `stream`, makes side_stream wait for
+ * it, and joins back by recording join_event on side_stream and making `stream` wait for it
+ * -- event records and waits only, so it can be captured into a graph. fork_event and
+ * join_event are caller-owned hipEvent_t (hipEventDisableTiming is enough); side_stream
+ * NULL runs as ccinfer_prefill_attention. No counterpart in the reference (one stream);
+ * HipBackend owns such a side stream. Concurrent calls must not share the side stream's
+ * events. */
+int ccinfer_prefill_attention_overlap(const void* q, const void* k_cache, const void* v_cache,
+                                      const int32_t* block_table,
+                                      const int32_t* query_start_loc,
+                                      const int32_t* context_lens, void* output, int batch_size,
+                                      int total_query_tokens, int max_blocks_per_req,
+                                      int num_q_heads, int num_kv_heads, int head_dim,
+                                      int cache_block_size, void* workspace,
+                                      size_t workspace_bytes, void* stream, void* side_stream,
+                                      void* fork_event, void* join_event);
+
 /* Replaces launch_prefill_attention (src/kernel/cuda_kernels.h:61-66) for an fp8 cache
  * (layout and scales as for ccinfer_write_kv_cache_fp8): the same semantics, planner and
  * workspace (ccinfer_prefill_workspace_size) as ccinfer_prefill_attention, with K/V read as
  * byte * row scale; single-token requests of a mixed batch go through the fp8 decode.
- * head_dim 64 or 128 on the MFMA path (CCINFER_ERR_UNSUPPORTED otherwise). */
+ * head_dim 64 or 128 and at most 4096 blocks per table row on the MFMA path
+ * (CCINFER_ERR_UNSUPPORTED otherwise). */
 int ccinfer_prefill_attention_fp8(const void* q, const void* k_cache, const void* v_cache,
                                   const float* k_scale, const float* v_scale,
                                   const int32_t* block_table, const int32_t* query_start_loc,
@@ -175,6 +206,16 @@ int ccinfer_prefill_attention_fp8(const void* q, const void* k_cache, const void
                                   int num_q_heads, int num_kv_heads, int head_dim,
                                   int cache_block_size, void* workspace, size_t workspace_bytes,
                                   void* stream);
+
+/* ccinfer_prefill_attention_fp8 with the decode items of a mixed batch on side_stream, as
+ * for ccinfer_prefill_attention_overlap. */
+int ccinfer_prefill_attention_fp8_overlap(
+    const void* q, const void* k_cache, const void* v_cache, const float* k_scale,
+    const float* v_scale, const int32_t* block_table, const int32_t* query_start_loc,
+    const int32_t* context_lens, void* output, int batch_size, int total_query_tokens,
+    int max_blocks_per_req, int num_q_heads, int num_kv_heads, int head_dim,
+    int cache_block_size, void* workspace, size_t workspace_bytes, void* stream,
+    void* side_stream, void* fork_event, void* join_event);
 
 /* Human-readable text for a status code (the reference's error_message()). */
 const char* ccinfer_error_message(int code);

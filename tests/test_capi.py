@@ -114,6 +114,38 @@ def test_prefill_validation(lib):
     assert _prefill(lib, ws=FAKE, wsb=need - 1) == INVALID
 
 
+def test_alignment_limits_and_overlap_validation(lib):
+    """fp8 calls (MFMA path only) reject q / output / cache / scale pointers that are not
+    16-byte aligned; bf16 calls route them to the generic kernels (GPU tests). Large batches
+    and long tables stay on the MFMA prefill (nonzero workspace); the fp8 prefill keeps its
+    4096-block table limit; a side stream without its events is rejected."""
+    UNSUPPORTED = 26
+    d8 = lib.ccinfer_decode_attention_fp8
+    args = [FAKE] * 8 + [2, 4, 8, 2, 128, 16, None, 0, None]
+    for i in (0, 1, 2, 3, 4, 7):          # q, k, v, k_scale, v_scale, output
+        a = list(args)
+        a[i] = FAKE + (2 if i < 3 or i == 7 else 4)
+        assert d8(*a) == INVALID, i
+    p8 = lib.ccinfer_prefill_attention_fp8
+    pargs = [FAKE] * 9 + [2, 64, 8, 16, 8, 128, 16, FAKE, 1 << 30, None]
+    for i in (0, 1, 8):                   # q, k_cache, output
+        a = list(pargs)
+        a[i] = FAKE + 8
+        assert p8(*a) == INVALID, i
+    a = list(pargs)
+    a[11] = 5000                          # more than 4096 blocks per row
+    assert p8(*a) == UNSUPPORTED
+    assert lib.ccinfer_prefill_workspace_size(6000, 6000, 8, 16, 8, 128, 16) > 0
+    assert lib.ccinfer_prefill_workspace_size(2, 64, 8192, 16, 8, 128, 16) > 0
+    assert lib.ccinfer_prefill_workspace_size(2, 64, 8192, 16, 8, 256, 16) == 0  # generic
+    ov = lib.ccinfer_prefill_attention_overlap
+    base = [FAKE] * 7 + [2, 64, 8, 16, 8, 128, 16, FAKE, 1 << 30, None]
+    assert ov(*base, FAKE, None, FAKE) == INVALID
+    assert ov(*base, FAKE, FAKE, None) == INVALID
+    ov8 = lib.ccinfer_prefill_attention_fp8_overlap
+    assert ov8(*pargs, FAKE, None, None) == INVALID
+
+
 def test_error_code_values_match_reference_enum():
     """The C ABI returns the reference's ErrorCode numbering (src/base/error_code.h:8-45)."""
     text = (ROOT / "ccinfer_amd" / "csrc" / "dropin" / "base" / "error_code.h").read_text()

@@ -184,3 +184,31 @@ def test_workspace_reuse_across_shapes(gpu):
                                meta["context_lens"], workspace=ws)
         torch.cuda.synchronize()
         assert_attn_close(f32(out), oracle_decode(w), f"reuse {it}")
+
+
+def _offset_view(t: torch.Tensor, elems: int = 1) -> torch.Tensor:
+    """A copy of `t` whose data pointer is `elems` bf16 elements past a 256-byte boundary."""
+    flat = torch.empty(t.numel() + elems, dtype=t.dtype, device=t.device)
+    v = flat[elems:].view(t.shape)
+    v.copy_(t)
+    return v
+
+
+@pytest.mark.parametrize("which", ["q", "k_cache", "v_cache", "output"])
+def test_two_byte_aligned_views(gpu, which):
+    """The reference launchers take any bf16 view: a q, cache or output pointer that is only
+    2-byte aligned runs on the generic kernels (the MFMA path moves 16-byte pieces)."""
+    say(f"decode with a 2-byte aligned {which}")
+    w = W.decode_batched(device=gpu, seed=17, batch=6, ctx_lo=20, ctx_hi=600, with_write=False)
+    meta = w.device_meta(gpu)
+    args = {"q": w.q, "k_cache": w.k_cache, "v_cache": w.v_cache}
+    out = None
+    if which == "output":
+        out = _offset_view(torch.zeros_like(w.q))
+    else:
+        args[which] = _offset_view(args[which])
+    assert (args["q"].data_ptr() % 16 != 0) == (which == "q")
+    got = decode_attention(args["q"], args["k_cache"], args["v_cache"], meta["block_table"],
+                           meta["context_lens"], output=out)
+    torch.cuda.synchronize()
+    assert_attn_close(f32(got), oracle_decode(w), f"misaligned {which}")

@@ -145,12 +145,18 @@ def test_prefill_fp8_mixed_batch_with_side_stream_decode_items(gpu):
     w = W.mixed_step(device=gpu, n_chunks=2, chunk=128, n_decode=40, dec_hi=4096)
     meta = w.device_meta(gpu)
     kc, vc, ks, vs = quantised_cache(gpu, w, w.hkv, w.d)
+    from ccinfer_amd import SideStream
     out = prefill_attention_fp8(w.q, kc, vc, ks, vs, meta["block_table"],
-                                meta["query_start_loc"], meta["context_lens"])
+                                meta["query_start_loc"], meta["context_lens"],
+                                overlap=SideStream(gpu))
     torch.cuda.synchronize()
     want = oracle.prefill_fp8(u16(w.q), kc.cpu().numpy(), vc.cpu().numpy(), ks.cpu().numpy(),
                               vs.cpu().numpy(), w.block_table, w.query_start_loc, w.context_lens)
     assert_attn_close(f32(out), want, "fp8 mixed")
+    serial = prefill_attention_fp8(w.q, kc, vc, ks, vs, meta["block_table"],
+                                   meta["query_start_loc"], meta["context_lens"])
+    torch.cuda.synchronize()
+    assert torch.equal(out, serial)  # the side stream changes the schedule, not the bits
     # the decode items equal the fp8 decode operator on the same rows
     nc = 2
     rows = torch.from_numpy(w.query_start_loc[nc:-1].astype(np.int64)).to(gpu)

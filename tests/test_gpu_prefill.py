@@ -219,8 +219,9 @@ def test_deterministic(gpu):
 
 
 def test_mixed_batch_under_graph_capture(gpu):
-    """The decode items run on a side stream forked from the caller's stream and joined
-    back; that fork/join must capture into a graph and replay to the eager result."""
+    """The decode items run on the caller's side stream, forked from the caller's stream and
+    joined back; that fork/join must capture into a graph and replay to the eager result."""
+    from ccinfer_amd import SideStream
     say("prefill mixed batch captured in a graph")
     # 42 requests: at least 32, so the decode items take the side stream
     w = W.mixed_step(device=gpu, n_chunks=2, chunk=128, n_decode=40, dec_hi=4096)
@@ -230,21 +231,105 @@ def test_mixed_batch_under_graph_capture(gpu):
     out = torch.zeros_like(w.q)
     n = prefill_workspace_size(w.batch, w.q.shape[0], w.mbpr, w.hq, w.hkv, w.d)
     ws = torch.zeros(max(1, n), dtype=torch.uint8, device=gpu)
+    side = SideStream(gpu)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):  # warm-up outside capture: creates the side stream
-        prefill_attention(w.q, w.k_cache, w.v_cache, meta["block_table"],
-                          meta["query_start_loc"], meta["context_lens"], output=out,
-                          workspace=ws)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=s):
         prefill_attention(w.q, w.k_cache, w.v_cache, meta["block_table"],
                           meta["query_start_loc"], meta["context_lens"], output=out,
-                          workspace=ws)
+                          workspace=ws, overlap=side)
     for _ in range(3):
         out.zero_()
         torch.cuda.synchronize()
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
+
+
+def test_concurrent_mixed_prefills_on_two_streams(gpu):
+    """Two mixed batches launched concurrently on two streams, each with its own workspace
+    and side stream, give the same bits as the same calls run one after the other: the
+    library holds no state shared between calls."""
+    from ccinfer_amd import SideStream
+    say("prefill concurrent mixed batches on two streams")
+    ws_a = W.mixed_step(device=gpu, seed=41, n_chunks=2, chunk=256, n_decode=48, dec_hi=8192)
+    ws_b = W.mixed_step(device=gpu, seed=42, n_chunks=3, chunk=128, n_decode=36, dec_hi=6000)
+    for w in (ws_a, ws_b):
+        write_new(w, gpu)
+    serial = [run_prefill(w, gpu).clone() for w in (ws_a, ws_b)]
+    outs = [torch.zeros_like(w.q) for w in (ws_a, ws_b)]
+    metas = [w.device_meta(gpu) for w in (ws_a, ws_b)]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    sides = [SideStream(gpu), SideStream(gpu)]
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for o in outs:
+            o.zero_()
+        torch.cuda.synchronize()
+        for w, m, o, st, sd in zip((ws_a, ws_b), metas, outs, streams, sides):
+            with torch.cuda.stream(st):
+                prefill_attention(w.q, w.k_cache, w.v_cache, m["block_table"],
+                                  m["query_start_loc"], m["context_lens"], output=o, overlap=sd)
+        torch.cuda.synchronize()
+        for o, want in zip(outs, serial):
+            assert torch.equal(o, want)
+
+
+@pytest.mark.parametrize("which", ["q", "k_cache", "output"])
+def test_two_byte_aligned_views(gpu, which):
+    """A q, cache or output view that is only 2-byte aligned runs on the generic kernels."""
+    say(f"prefill with a 2-byte aligned {which}")
+    w = W.prefill_prefix(device=gpu, seed=19, n_seqs=3, prefix=32, new=90, share_pairs=(),
+                         hq=8, hkv=4, d=128)
+    write_new(w, gpu)
+
+    def shifted(t):
+        flat = torch.empty(t.numel() + 1, dtype=t.dtype, device=t.device)
+        v = flat[1:].view(t.shape)
+        v.copy_(t)
+        return v
+
+    meta = w.device_meta(gpu)
+    q, kc, out = w.q, w.k_cache, None
+    if which == "q":
+        q = shifted(w.q)
+    elif which == "k_cache":
+        kc = shifted(w.k_cache)
+    else:
+        out = shifted(torch.zeros_like(w.q))
+    got = prefill_attention(q, kc, w.v_cache, meta["block_table"], meta["query_start_loc"],
+                            meta["context_lens"], output=out)
+    torch.cuda.synchronize()
+    assert_attn_close(f32(got), oracle_prefill(w), f"misaligned {which}")
+
+
+def test_more_than_4096_requests(gpu):
+    """The planner keeps per-request arrays in LDS up to 4096 requests and in the workspace
+    beyond; the reference launcher has no batch limit."""
+    say("prefill 5200 requests: 4700 prompt chunks + 500 decodes (sampled rows)")
+    w = W.mixed_step(device=gpu, seed=23, n_chunks=4700, chunk=4, prefix_hi=64, n_decode=500,
+                     dec_lo=8, dec_hi=200)
+    write_new(w, gpu)
+    assert w.batch > 4096
+    got = f32(run_prefill(w, gpu))
+    pairs = sample_pairs(w, 512, 23)
+    want = oracle_prefill(w, pairs=pairs)
+    r, h = pairs[:, 0], pairs[:, 1]
+    assert_attn_close(got[r, h], want[r, h], "5200 requests")
+
+
+def test_table_row_longer_than_4096_blocks(gpu):
+    """A 70K-token context (4400 blocks per table row) stays on the MFMA path: block ids are
+    read from the table row in global memory, not staged in LDS."""
+    say("prefill 1 x (70144 cached + 300 new) (sampled rows)")
+    w = W.prefill_prefix(device=gpu, seed=24, n_seqs=1, prefix=70144, new=300, share_pairs=(),
+                         hq=16, hkv=8, d=128)
+    write_new(w, gpu)
+    assert w.mbpr > 4096
+    got = f32(run_prefill(w, gpu))
+    pairs = sample_pairs(w, 48, 24)
+    want = oracle_prefill(w, pairs=pairs)
+    r, h = pairs[:, 0], pairs[:, 1]
+    assert_attn_close(got[r, h], want[r, h], "long table")
