@@ -46,6 +46,7 @@ SOURCES = [
     CSRC / "qkv_prologue.hip",
     CSRC / "batch_meta.hip",
     CSRC / "kv_fp8.hip",
+    CSRC / "noalloc.hip",
     CSRC / "capi.cpp",
     CSRC / "dropin" / "launchers.cpp",
     CSRC / "dropin" / "hip_backend.cpp",

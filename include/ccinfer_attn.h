@@ -124,6 +124,20 @@ int ccinfer_decode_attention(const void* q, const void* k_cache, const void* v_c
                              int cache_block_size, void* workspace, size_t workspace_bytes,
                              void* stream);
 
+/* ccinfer_decode_attention without a workspace and without any allocation. No counterpart
+ * in the reference: for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). The split-KV scratch is
+ * one static 32 MiB device array per GPU, resolved on the first call on each device and
+ * held until the process ends; shapes whose ccinfer_decode_workspace_size exceeds 32 MiB
+ * return CCINFER_ERR_INVALID_ARGUMENT (configs of batch 64 x 4096 or 32 x 32768 tokens need
+ * under 9 MiB). Calls that overlap on one GPU (concurrent streams) share the array and
+ * race; otherwise identical results to ccinfer_decode_attention. */
+int ccinfer_decode_attention_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                                     const int32_t* block_table, const int32_t* context_lens,
+                                     void* output, int batch_size, int max_blocks_per_req,
+                                     int num_q_heads, int num_kv_heads, int head_dim,
+                                     int cache_block_size, void* stream);
+
 /* fp8 KV cache (no counterpart in the reference, whose cache is bf16 only; its KV profile
  * list, src/base/traits.h:117-124, anticipates other element types). Same [slot][n_kv_heads]
  * [head_dim] layout and block-table contract, one OCP E4M3 byte per element, plus one fp32
