@@ -499,6 +499,13 @@ def profile(op: str, iters: int) -> None:
         w = W.prefill_prefix(device=dev, seed=11, n_seqs=16, prefix=4096, new=256,
                              share_pairs=share)
         fn = Ops(w, dev, stream).prefill
+    elif op in ("shared_prefix_ragged", "private_prefix_ragged"):
+        # 16 sequences x (4096 cached + 64..1024 new): unequal new lengths, one shared prefix
+        # (or 16 private copies) -- the sharers' tiles differ in length
+        share = tuple((i, 0) for i in range(1, 16)) if op == "shared_prefix_ragged" else ()
+        w = W.prefill_prefix(device=dev, seed=12, n_seqs=16, prefix=4096,
+                             new=[64 + 64 * i for i in range(16)], share_pairs=share)
+        fn = Ops(w, dev, stream).prefill
     else:
         w = {"decode": W.decode_batched, "write": W.decode_batched, "prefill": W.prefill_prefix,
              "mixed": W.mixed_step, "long": W.decode_long}[op](device=dev)
@@ -561,6 +568,7 @@ def main():
                     help="print a table of the op across shapes and exit")
     ap.add_argument("--profile-op", choices=["decode", "write", "prefill", "mixed", "long",
                                              "prologue", "shared_prefix", "private_prefix",
+                                             "shared_prefix_ragged", "private_prefix_ragged",
                                              "copy"], default=None)
     ap.add_argument("--profile-iters", type=int, default=5)
     args = ap.parse_args()

@@ -167,35 +167,38 @@ def decode_long(device="cpu", seed: int = 5, batch: int = 32, ctx: int = 32768,
 
 
 def prefill_prefix(device="cpu", seed: int = 3, n_seqs: int = 8, prefix: int = 512,
-                   new: int = 1536, share_pairs=((1, 0),), hq: int = 16, hkv: int = 8,
+                   new=1536, share_pairs=((1, 0),), hq: int = 16, hkv: int = 8,
                    d: int = 128) -> PagedWorkload:
     """Config 3: n_seqs x (cached prefix + new prompt tokens), causal; seq 1 shares seq 0's
-    prefix blocks. The new tokens' K/V are returned in k_new/v_new + slot_mapping (to be
-    written before attention)."""
+    prefix blocks. `new` is one length for every sequence or one per sequence. The new
+    tokens' K/V are returned in k_new/v_new + slot_mapping (to be written before attention)."""
     assert prefix % BLOCK == 0
     rng = np.random.default_rng(seed)
-    ctx_len = prefix + new
-    nblk = -(-ctx_len // BLOCK)
+    news = np.full(n_seqs, new, np.int64) if np.isscalar(new) else np.asarray(new, np.int64)
+    assert news.shape == (n_seqs,) and np.all(news > 0)
+    ctx = prefix + news
+    nblk = -(-ctx // BLOCK)
     pblk = prefix // BLOCK
     shared = {dst: (src, pblk) for dst, src in share_pairs}
-    distinct = n_seqs * nblk - len(shared) * pblk
+    distinct = int(nblk.sum()) - len(shared) * pblk
     pool = _pool_size(distinct)
-    bt = _tables(rng, [nblk] * n_seqs, pool, shared)
+    bt = _tables(rng, nblk.tolist(), pool, shared)
     g = _gen(seed, device)
-    total = n_seqs * new
+    qsl = np.concatenate([[0], np.cumsum(news)]).astype(np.int32)
+    total = int(qsl[-1])
     q = randn_bf16((total, hq, d), g, device)
     k, v = _cache(pool, hkv, d, g, device)
-    pos = np.tile(np.arange(prefix, ctx_len), n_seqs)
-    seq = np.repeat(np.arange(n_seqs), new)
+    seq = np.repeat(np.arange(n_seqs), news)
+    pos = prefix + np.arange(total) - qsl[seq]
     slot = (bt[seq, pos // BLOCK] * BLOCK + pos % BLOCK).astype(np.int32)
-    w = PagedWorkload(f"prefill_{n_seqs}x({prefix}+{new})", hq, hkv, d,
-                      np.full(n_seqs, ctx_len, np.int32), bt, pool, q, k, v,
-                      query_start_loc=(np.arange(n_seqs + 1) * new).astype(np.int32))
+    label = f"{int(news[0])}" if np.all(news == news[0]) else f"{int(news.min())}..{int(news.max())}"
+    w = PagedWorkload(f"prefill_{n_seqs}x({prefix}+{label})", hq, hkv, d, ctx.astype(np.int32),
+                      bt, pool, q, k, v, query_start_loc=qsl)
     w.slot_mapping = slot
     w.k_new = randn_bf16((total, hkv, d), g, device)
     w.v_new = randn_bf16((total, hkv, d), g, device)
     w.info["prefix"] = prefix
-    w.info["new"] = new
+    w.info["new"] = int(news[0]) if np.all(news == news[0]) else news.tolist()
     return w
 
 

@@ -82,26 +82,33 @@ def test_config3_prefix_cached(gpu):
     assert np.all(np.isfinite(got))
 
 
-def test_shared_prefix_equals_private_copy(gpu):
-    """Two sequences listing the same prefix blocks == one of them on a private copy."""
-    say("prefill shared prefix == private copy")
-    w = W.prefill_prefix(device=gpu, seed=8, n_seqs=3, prefix=64, new=100, hq=16, hkv=8)
+@pytest.mark.parametrize("prefix,new,sharers", [
+    (64, 100, (1,)), (1024, [300, 77, 513, 129], (1, 2, 3))])
+def test_shared_prefix_equals_private_copy(gpu, prefix, new, sharers):
+    """Sequences listing the same prefix blocks (with equal or unequal new-token lengths) ==
+    the same batch with private copies of those blocks."""
+    say(f"prefill shared prefix == private copy (prefix {prefix}, new {new})")
+    n = 3 if np.isscalar(new) else len(new)
+    w = W.prefill_prefix(device=gpu, seed=8, n_seqs=n, prefix=prefix, new=new, hq=16, hkv=8,
+                         share_pairs=tuple((s, 0) for s in sharers))
     write_new(w, gpu)
     shared = u16(run_prefill(w, gpu))
-    # Give seq 1 private copies of its (shared) prefix blocks in fresh pool blocks.
-    pblk = 64 // 16
+    # Give the sharers private copies of their (shared) prefix blocks in fresh pool blocks.
+    pblk = prefix // 16
     extra = w.num_blocks
-    kc = torch.cat([w.k_cache, torch.empty((pblk * 16,) + w.k_cache.shape[1:],
+    kc = torch.cat([w.k_cache, torch.empty((len(sharers) * pblk * 16,) + w.k_cache.shape[1:],
                                            dtype=w.k_cache.dtype, device=gpu)])
-    vc = torch.cat([w.v_cache, torch.empty_like(kc[:pblk * 16])])
+    vc = torch.cat([w.v_cache, torch.empty_like(kc[:len(sharers) * pblk * 16])])
     bt = w.block_table.copy()
-    for i in range(pblk):
-        src = int(bt[1, i])
-        kc[(extra + i) * 16:(extra + i + 1) * 16] = w.k_cache[src * 16:(src + 1) * 16]
-        vc[(extra + i) * 16:(extra + i + 1) * 16] = w.v_cache[src * 16:(src + 1) * 16]
-        bt[1, i] = extra + i
-    assert np.array_equal(w.block_table[0, :pblk], w.block_table[1, :pblk])
-    w2 = W.PagedWorkload("copy", w.hq, w.hkv, w.d, w.context_lens, bt, extra + pblk, w.q, kc, vc,
+    for si, seq in enumerate(sharers):
+        assert np.array_equal(w.block_table[0, :pblk], w.block_table[seq, :pblk])
+        for i in range(pblk):
+            src, dst = int(bt[seq, i]), extra + si * pblk + i
+            kc[dst * 16:(dst + 1) * 16] = w.k_cache[src * 16:(src + 1) * 16]
+            vc[dst * 16:(dst + 1) * 16] = w.v_cache[src * 16:(src + 1) * 16]
+            bt[seq, i] = dst
+    extra += len(sharers) * pblk
+    w2 = W.PagedWorkload("copy", w.hq, w.hkv, w.d, w.context_lens, bt, extra, w.q, kc, vc,
                          query_start_loc=w.query_start_loc)
     private = u16(run_prefill(w2, gpu))
     assert np.array_equal(shared, private)
