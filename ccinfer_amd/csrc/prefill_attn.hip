@@ -648,7 +648,7 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
     // The block table in LDS (fp8 staging only; the bf16 staging reads its block ids from
     // global memory into a register window).
     __shared__ int32_t lds_bt[F8 ? kMaxTableLds : 1];
-    __shared__ int s_holes;
+    __shared__ int s_holes[kPipeWaves];
 
     const int G = hq / hkv;
     const int HPW = heads_per_wg(G);
@@ -682,23 +682,44 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
     const int q_head = kvh * G + hg * HPW + head_local;
     const int32_t* req_blocks = block_table + static_cast<int64_t>(req) * mbpr;
 
-    // Block-table slice in LDS: entries for every block the tiles touch, -1 past the
-    // visible range or the table row. Holes (negative ids inside the visible range, or a
-    // visible range longer than the row) force the masked path on every tile.
-    if (threadIdx.x == 0) s_holes = 0;
-    __syncthreads();
     const int nblk_vis = (kv_end + kBlock - 1) / kBlock;
     const int nblk = min(nblk_vis, mbpr);
+    // Block ids this wavefront stages, held in one register: lane i has the id of load
+    // i % NL's cache block in tile kWin * bt_win + i / NL (-1 past the visible table). A
+    // stage reads its ids with readlane; the window is reloaded from the table row every
+    // kWin tiles, so the table length is not bounded by LDS.
+    constexpr int kWin = 64 / NL;
+    int btw;
+    int bt_win = -1;
+    auto bt_window = [&](int win) __attribute__((always_inline)) {
+        const int x = lane % NL;
+        const int blk = ((x * kPipeWaves + wave) * 64 / CPR) >> 4;
+        const int lb = (win * kWin + lane / NL) * (kKeysPerTile / kBlock) + blk;
+        btw = lb < nblk ? req_blocks[lb] : -1;
+        bt_win = win;
+    };
+    // The first window's load goes out before the table scan below, so the two overlap.
+    if constexpr (!F8) bt_window(0);
+
+    // Block-table slice in LDS (fp8): entries for every block the tiles touch, -1 past the
+    // visible range or the table row. Holes (negative ids inside the visible range, or a
+    // visible range longer than the row) force the masked path on every tile; each
+    // wavefront records whether its share of the scan found one.
     // Block ids whose byte offset does not fit the 32-bit buffer offset of the fast staging
     // path are treated like holes (the checked path addresses with 64 bits).
     const int max_fast_pb = static_cast<int>(
         min(static_cast<int64_t>(0x7fffffff),
             static_cast<int64_t>(0xffffffffll / (static_cast<int64_t>(kBlock) * hkv * D * 2)) - 1));
+    bool bad = false;
     for (int lb = threadIdx.x; lb < (F8 ? ntiles * (kKeysPerTile / kBlock) : nblk);
          lb += kPipeThreads) {
         const int pb = lb < nblk ? req_blocks[lb] : -1;
         if constexpr (F8) lds_bt[lb] = pb;
-        if (lb < nblk && (pb < 0 || pb > max_fast_pb)) s_holes = 1;
+        bad = bad || (lb < nblk && (pb < 0 || pb > max_fast_pb));
+    }
+    {
+        const bool any = __builtin_amdgcn_ballot_w64(bad) != 0;
+        if (lane == 0) s_holes[wave] = any ? 1 : 0;
     }
 
     // Staging constants. Load x of a wavefront fills the 64 16-byte LDS slots starting at
@@ -743,11 +764,6 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
 
     // Rows past kv_end or in unmapped blocks are not loaded: their LDS slots are written with
     // zeros instead, and the mask gives them probability 0.
-    // Block ids this wavefront stages, held in one register: lane i has the id of load
-    // i % NL's cache block in tile kWin * bt_win + i / NL (-1 past the visible table). A
-    // stage reads its ids with readlane; the window is reloaded from the table row every
-    // kWin tiles, so the table length is not bounded by LDS.
-    constexpr int kWin = 64 / NL;
 #if defined(__HIP_DEVICE_COMPILE__)
     // (device pass only: the host pass cannot type the buffer builtins, and a kernel
     // template that fails there loses its launch stub silently)
@@ -756,15 +772,6 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
     const __amdgpu_buffer_rsrc_t v_rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void*)v_cache, 0, -1, 0x00020000);
 #endif
-    int btw;
-    int bt_win = -1;
-    auto bt_window = [&](int win) __attribute__((always_inline)) {
-        const int x = lane % NL;
-        const int blk = ((x * kPipeWaves + wave) * 64 / CPR) >> 4;
-        const int lb = (win * kWin + lane / NL) * (kKeysPerTile / kBlock) + blk;
-        btw = lb < nblk ? req_blocks[lb] : -1;
-        bt_win = win;
-    };
     // kHoles: the table has holes in the visible range; then every tile goes through the
     // checked path, which also records per-row validity for the mask. Otherwise only a tile
     // that reaches past kv_end does (its rows past kv_end are zero-filled).
@@ -915,8 +922,11 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
             qop[kk] = __builtin_bit_cast(bf16x8, load16(qv + kk * 16 + h32 * 8));
         }
     }
-    __syncthreads();  // block table staged
-    const bool holes = s_holes != 0 || nblk_vis > mbpr;
+    __syncthreads();  // block table scanned (and, for fp8, staged)
+    bool any_hole = false;
+#pragma unroll
+    for (int w = 0; w < kPipeWaves; ++w) any_hole = any_hole || s_holes[w] != 0;
+    const bool holes = any_hole || nblk_vis > mbpr;
 
     // O^T: lane (c, h), element v of dim tile n holds dim 32 n + 8 (v/4) + 4 h + v%4 of
     // query row tw + c. lsum: this lane's share of the row sum of query row tw + c (the
