@@ -304,7 +304,7 @@ int ccinfer_decode_attention_fp8(const void* q, const void* k_cache, const void*
     if (!decode_shape_ok(batch_size, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
                          cache_block_size))
         return CCINFER_ERR_INVALID_ARGUMENT;
-    if (!decode_fast_supported(num_q_heads, num_kv_heads, head_dim, cache_block_size))
+    if (!decode_fp8_supported(num_q_heads, num_kv_heads, head_dim, cache_block_size))
         return CCINFER_ERR_UNSUPPORTED;  // fp8 has the MFMA path only
     if (!fast_aligned(q, k_cache, v_cache, output) || !aligned16(k_scale) || !aligned16(v_scale))
         return CCINFER_ERR_INVALID_ARGUMENT;

@@ -214,45 +214,54 @@ struct ChunkRegs {
     uint32_t v[8][DecodeShape<D>::kVWords];
 };
 
-template <int D>
+// kPad: the cache rows hold dr < D dims (dr a multiple of D/16); the kernel runs at the
+// MFMA size D with dims [dr, D) zero. Loads of missing dims read a valid piece of the row
+// instead (so every lane still issues the same loads) and are replaced by zeros.
+template <int D, bool kPad = false>
 __device__ __forceinline__ void load_chunk(ChunkRegs<D>& c, const __bf16* __restrict__ k_cache,
                                            const __bf16* __restrict__ v_cache, int pb0, int pb1,
-                                           int kv_head, int hkv, int lane) {
+                                           int kv_head, int hkv, int lane, int dr = D) {
     constexpr int S = DecodeShape<D>::kSteps;
     constexpr int NV = DecodeShape<D>::kNV;
+    const int rs = kPad ? dr : D;  // row stride (elements)
     const int i = lane & 15;
     const int g = lane >> 4;
     const int pbs[2] = {pb0 < 0 ? 0 : pb0, pb1 < 0 ? 0 : pb1};
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
         const __bf16* row =
-            k_cache + ((static_cast<int64_t>(pbs[kb]) * kBlock + i) * hkv + kv_head) * D;
+            k_cache + ((static_cast<int64_t>(pbs[kb]) * kBlock + i) * hkv + kv_head) * rs;
 #pragma unroll
-        for (int kk = 0; kk < S; ++kk)
-            c.k[kb][kk] = nt_load(reinterpret_cast<const u32x4*>(row + (kk * 4 + g) * 8));
+        for (int kk = 0; kk < S; ++kk) {
+            const int dim0 = (kk * 4 + g) * 8;
+            const bool ok = !kPad || dim0 < dr;
+            c.k[kb][kk] = nt_load(reinterpret_cast<const u32x4*>(row + (ok ? dim0 : 0)));
+            if (!ok) c.k[kb][kk] = u32x4{0, 0, 0, 0};
+        }
     }
+    const bool vok = !kPad || i * NV < dr;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         const int kb = e >> 2;
         const int off = g * 4 + (e & 3);
         const __bf16* row =
-            v_cache + ((static_cast<int64_t>(pbs[kb]) * kBlock + off) * hkv + kv_head) * D +
-            i * NV;
+            v_cache + ((static_cast<int64_t>(pbs[kb]) * kBlock + off) * hkv + kv_head) * rs +
+            (vok ? i * NV : 0);
         if constexpr (NV == 8) {
             const u32x4 w = nt_load(reinterpret_cast<const u32x4*>(row));
 #pragma unroll
-            for (int x = 0; x < 4; ++x) c.v[e][x] = w[x];
+            for (int x = 0; x < 4; ++x) c.v[e][x] = vok ? w[x] : 0u;
         } else if constexpr (NV == 4) {
             const u32x2 w = nt_load(reinterpret_cast<const u32x2*>(row));
-            c.v[e][0] = w[0];
-            c.v[e][1] = w[1];
+            c.v[e][0] = vok ? w[0] : 0u;
+            c.v[e][1] = vok ? w[1] : 0u;
         } else {
             const u32x4 w0 = nt_load(reinterpret_cast<const u32x4*>(row));
             const u32x4 w1 = nt_load(reinterpret_cast<const u32x4*>(row + 8));
 #pragma unroll
             for (int x = 0; x < 4; ++x) {
-                c.v[e][x] = w0[x];
-                c.v[e][4 + x] = w1[x];
+                c.v[e][x] = vok ? w0[x] : 0u;
+                c.v[e][4 + x] = vok ? w1[x] : 0u;
             }
         }
     }
@@ -443,7 +452,8 @@ __device__ __forceinline__ void consume_chunk(SoftmaxState<D>& st, ChunkRegsF8<D
 // used so a row costs a couple of memory latencies, not one per split.
 template <int D>
 __device__ void merge_row(const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
-                          int64_t base, int ns, float eps, __bf16* __restrict__ o, int lane) {
+                          int64_t base, int ns, float eps, __bf16* __restrict__ o, int lane,
+                          int dr = D) {
     constexpr int kPer = D / 64;
     constexpr int kBatch = 8;
     float mmax = kNegInf;
@@ -488,7 +498,8 @@ __device__ void merge_row(const float* __restrict__ ws_o, const float* __restric
     for (int off = 32; off >= 1; off >>= 1) lsum += __shfl_xor(lsum, off);
     const float inv = lsum > 0.f ? 1.f / (lsum + eps) : 0.f;
 #pragma unroll
-    for (int x = 0; x < kPer; ++x) o[lane * kPer + x] = static_cast<__bf16>(acc[x] * inv);
+    for (int x = 0; x < kPer; ++x)
+        if (lane * kPer + x < dr) o[lane * kPer + x] = static_cast<__bf16>(acc[x] * inv);
 }
 
 // Per-split inputs: the split's block ids, one per lane (two registers cover 128 blocks),
@@ -503,12 +514,12 @@ struct SplitInputs {
 
 // Loads the inputs of a split starting at position `begin` whose table entries end at
 // position tbl_end (no more than 2048 positions).
-template <int D, bool F8>
+template <int D, bool F8, bool kPad = false>
 __device__ __forceinline__ void load_split_inputs(const __bf16* __restrict__ q,
                                                   const int32_t* __restrict__ req_blocks,
                                                   int mbpr, int qrow, int hq, int h, int G,
                                                   int begin, int tbl_end, int lane,
-                                                  SplitInputs<D>& in) {
+                                                  SplitInputs<D>& in, int dr = D) {
     constexpr int S = DecodeShape<D>::kSteps;
     const int j = lane & 15;
     const int g = lane >> 4;
@@ -517,25 +528,27 @@ __device__ __forceinline__ void load_split_inputs(const __bf16* __restrict__ q,
     in.bt_lo = (lane < nblk && lb0 + lane < mbpr) ? req_blocks[lb0 + lane] : -1;
     in.bt_hi = (lane + 64 < nblk && lb0 + lane + 64 < mbpr) ? req_blocks[lb0 + lane + 64] : -1;
     const bool live = j < G;
-    const __bf16* qv = q + (static_cast<int64_t>(qrow) * hq + h * G + (live ? j : 0)) * D;
+    const __bf16* qv =
+        q + (static_cast<int64_t>(qrow) * hq + h * G + (live ? j : 0)) * (kPad ? dr : D);
 #pragma unroll
     for (int kk = 0; kk < S; ++kk) {
         const int dim0 = F8 ? 64 * (kk >> 1) + 16 * g + 8 * (kk & 1) : (kk * 4 + g) * 8;
-        u32x4 w = load16(qv + dim0);
-        if (!live) w = u32x4{0, 0, 0, 0};
+        const bool ok = !kPad || dim0 < dr;
+        u32x4 w = load16(qv + (ok ? dim0 : 0));
+        if (!live || !ok) w = u32x4{0, 0, 0, 0};
         in.qop[kk] = __builtin_bit_cast(bf16x8, w);
     }
 }
 
 // Attention of the G query heads of kv_head h over context positions [begin, end) (at most
 // 2048) with the split's inputs: the online-softmax state of one wavefront.
-template <int D, bool F8>
+template <int D, bool F8, bool kPad = false>
 __device__ __forceinline__ void run_split(
     const std::conditional_t<F8, uint8_t, __bf16>* __restrict__ k_cache,
     const std::conditional_t<F8, uint8_t, __bf16>* __restrict__ v_cache,
     const float* __restrict__ k_scale, const float* __restrict__ v_scale,
     const SplitInputs<D>& in, int hkv, int h, int begin, int end, float scale_log2, int lane,
-    SoftmaxState<D>& st) {
+    SoftmaxState<D>& st, int dr = D) {
     constexpr int NV = DecodeShape<D>::kNV;
     using Regs = std::conditional_t<F8, ChunkRegsF8<D>, ChunkRegs<D>>;
     const int g = lane >> 4;
@@ -560,7 +573,7 @@ __device__ __forceinline__ void run_split(
         if constexpr (F8)
             load_chunk<D>(r, k_cache, v_cache, k_scale, v_scale, p0, p1, h, hkv, lane);
         else
-            load_chunk<D>(r, k_cache, v_cache, p0, p1, h, hkv, lane);
+            load_chunk<D, kPad>(r, k_cache, v_cache, p0, p1, h, hkv, lane, dr);
     };
     int a0, a1, b0, b1;
     chunk_blocks(0, &a0, &a1);
@@ -577,14 +590,16 @@ __device__ __forceinline__ void run_split(
 }
 
 // F8: the cache holds E4M3 bytes with row scales (k_scale / v_scale); else bf16.
-template <int D, bool F8>
+// kPad: head_dim dr < D (see load_chunk); q and output rows hold dr elements.
+template <int D, bool F8, bool kPad>
 __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     const __bf16* __restrict__ q, const void* __restrict__ k_cache_v,
     const void* __restrict__ v_cache_v, const float* __restrict__ k_scale,
     const float* __restrict__ v_scale, const int32_t* __restrict__ block_table,
     const int32_t* __restrict__ context_lens, __bf16* __restrict__ out, float* __restrict__ ws_o,
     float* __restrict__ ws_ml, MergeDesc* __restrict__ desc, ItemArgs items, int mbpr, int hq,
-    int hkv, int splits, int split_tokens, int balanced_w, int slots, float scale_log2) {
+    int hkv, int splits, int split_tokens, int balanced_w, int slots, float scale_log2, int dr) {
+    const int ds = kPad ? dr : D;  // q / output row stride
     constexpr int NV = DecodeShape<D>::kNV;
     using Cache = std::conditional_t<F8, uint8_t, __bf16>;
     const Cache* __restrict__ k_cache = static_cast<const Cache*>(k_cache_v);
@@ -634,8 +649,8 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     if (ctx < 0) {
         // Decode semantics: invalid context -> zeros (written once, by split 0).
         if (items.zero_invalid && s == 0) {
-            for (int x = lane; x < G * D; x += 64) {
-                out[(static_cast<int64_t>(qrow) * hq + h * G) * D + x] = static_cast<__bf16>(0.0f);
+            for (int x = lane; x < G * ds; x += 64) {
+                out[(static_cast<int64_t>(qrow) * hq + h * G) * ds + x] = static_cast<__bf16>(0.0f);
             }
         }
         return;
@@ -644,24 +659,25 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     if (begin >= ctx) return;
     const int end = min(ctx, begin + split_tokens);
     SplitInputs<D> in;
-    load_split_inputs<D, F8>(q, block_table + static_cast<int64_t>(req) * mbpr, mbpr, qrow, hq,
-                             h, G, begin, end, lane, in);
+    load_split_inputs<D, F8, kPad>(q, block_table + static_cast<int64_t>(req) * mbpr, mbpr, qrow,
+                                   hq, h, G, begin, end, lane, in, dr);
     SoftmaxState<D> st;
-    run_split<D, F8>(k_cache, v_cache, k_scale, v_scale, in, hkv, h, begin, end, scale_log2, lane,
-                     st);
+    run_split<D, F8, kPad>(k_cache, v_cache, k_scale, v_scale, in, hkv, h, begin, end, scale_log2,
+                           lane, st, dr);
     const float l_tot = wave_sum_xor16_32(st.l);
     const bool live = j < G;
     const int head = h * G + j;
     if (ns == 1) {
         if (!live) return;
         const float inv = l_tot > 0.f ? 1.f / (l_tot + items.eps) : 0.f;
-        __bf16* o = out + (static_cast<int64_t>(qrow) * hq + head) * D;
+        __bf16* o = out + (static_cast<int64_t>(qrow) * hq + head) * ds;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             uint32_t w[NV / 2];
 #pragma unroll
             for (int x = 0; x < NV / 2; ++x)
                 w[x] = pack_bf16x2(st.acc[2 * x][r] * inv, st.acc[2 * x + 1][r] * inv);
+            if (kPad && NV * (4 * g + r) >= dr) continue;  // padded dims
             uint32_t* dst = reinterpret_cast<uint32_t*>(o + NV * (4 * g + r));
 #pragma unroll
             for (int x = 0; x < NV / 2; ++x) dst[x] = w[x];
@@ -708,13 +724,14 @@ struct GroupShape {
     static constexpr int kMaxG = 16;                 // LDS: kWaves * 16 * D floats = 64 KiB
 };
 
-template <int D, bool F8>
+template <int D, bool F8, bool kPad>
 __global__ __launch_bounds__(64 * GroupShape<D>::kWaves) void decode_group_kernel(
     const __bf16* __restrict__ q, const void* __restrict__ k_cache_v,
     const void* __restrict__ v_cache_v, const float* __restrict__ k_scale,
     const float* __restrict__ v_scale, const int32_t* __restrict__ block_table,
     const int32_t* __restrict__ context_lens, __bf16* __restrict__ out, ItemArgs items,
-    int mbpr, int hq, int hkv, float scale_log2) {
+    int mbpr, int hq, int hkv, float scale_log2, int dr) {
+    const int ds = kPad ? dr : D;  // q / output row stride
     constexpr int W = GroupShape<D>::kWaves;
     constexpr int NV = DecodeShape<D>::kNV;
     constexpr int kMaxG = GroupShape<D>::kMaxG;
@@ -738,22 +755,22 @@ __global__ __launch_bounds__(64 * GroupShape<D>::kWaves) void decode_group_kerne
     const int begin = wave * per * kChunk;
     const int tbl_end = min(mbpr * kBlock, begin + per * kChunk);
     SplitInputs<D> in;
-    load_split_inputs<D, F8>(q, block_table + static_cast<int64_t>(req) * mbpr, mbpr, qrow, hq,
-                             h, G, begin, max(begin, tbl_end), lane, in);
+    load_split_inputs<D, F8, kPad>(q, block_table + static_cast<int64_t>(req) * mbpr, mbpr, qrow,
+                                   hq, h, G, begin, max(begin, tbl_end), lane, in, dr);
     const int ctx = effective_ctx(ctx_raw, mbpr, items.zero_invalid);
     if (ctx < 0) {
         // Decode semantics: invalid context -> zeros; prefill semantics: row untouched.
         if (items.zero_invalid) {
-            for (int x = threadIdx.x; x < G * D; x += 64 * W)
-                out[(static_cast<int64_t>(qrow) * hq + h * G) * D + x] = static_cast<__bf16>(0.0f);
+            for (int x = threadIdx.x; x < G * ds; x += 64 * W)
+                out[(static_cast<int64_t>(qrow) * hq + h * G) * ds + x] = static_cast<__bf16>(0.0f);
         }
         return;
     }
     const int end = min(ctx, tbl_end);
     SoftmaxState<D> st;
     if (begin < end) {
-        run_split<D, F8>(k_cache, v_cache, k_scale, v_scale, in, hkv, h, begin, end, scale_log2,
-                         lane, st);
+        run_split<D, F8, kPad>(k_cache, v_cache, k_scale, v_scale, in, hkv, h, begin, end,
+                               scale_log2, lane, st, dr);
     } else {
 #pragma unroll
         for (int n = 0; n < NV; ++n) st.acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -795,9 +812,11 @@ __global__ __launch_bounds__(64 * GroupShape<D>::kWaves) void decode_group_kerne
             }
         }
         const float inv = lsum > 0.f ? 1.f / (lsum + items.eps) : 0.f;
-        __bf16* o = out + (static_cast<int64_t>(qrow) * hq + h * G + jj) * D;
+        __bf16* o = out + (static_cast<int64_t>(qrow) * hq + h * G + jj) * ds;
 #pragma unroll
-        for (int x = 0; x < kPer; ++x) o[lane * kPer + x] = static_cast<__bf16>(acc[x] * inv);
+        for (int x = 0; x < kPer; ++x)
+            if (!kPad || lane * kPer + x < dr)
+                o[lane * kPer + x] = static_cast<__bf16>(acc[x] * inv);
     }
 }
 
@@ -805,7 +824,7 @@ __global__ __launch_bounds__(64 * GroupShape<D>::kWaves) void decode_group_kerne
 template <int D>
 __global__ __launch_bounds__(256) void decode_merge_kernel(
     __bf16* __restrict__ out, const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
-    const MergeDesc* __restrict__ desc, ItemArgs items, int hq) {
+    const MergeDesc* __restrict__ desc, ItemArgs items, int hq, int dr) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wi = blockIdx.x * kWavesPerGroup + wave;
@@ -817,7 +836,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(
     if (!resolve_item(items, item, &req, &qrow)) return;
     if (d.ns <= 1) return;  // invalid row, or written directly by the split kernel
     merge_row<D>(ws_o, ws_ml, d.base, static_cast<int>(d.ns), items.eps,
-                 out + (static_cast<int64_t>(qrow) * hq + head) * D, lane);
+                 out + (static_cast<int64_t>(qrow) * hq + head) * dr, lane, dr);
 }
 
 struct DecodeWs {
@@ -846,19 +865,20 @@ DecodeWs carve(void* workspace, size_t rows, int d) {
     return w;
 }
 
-template <int D, bool F8>
+// dr: the head dim of q / cache / output rows (dr == D unless kPad).
+template <int D, bool F8, bool kPad>
 hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache,
                          const float* k_scale, const float* v_scale,
                          const int32_t* block_table, const int32_t* context_lens, void* output,
                          const ItemArgs& it, int mbpr, int hq, int hkv, const DecodePlan& plan,
-                         void* workspace, hipStream_t stream) {
-    const float scale_log2 = kLog2e / sqrtf(static_cast<float>(D));
+                         void* workspace, hipStream_t stream, int dr) {
+    const float scale_log2 = kLog2e / sqrtf(static_cast<float>(dr));
     if (plan.group) {
         const int64_t groups = static_cast<int64_t>(it.num_items) * hkv;
-        decode_group_kernel<D, F8><<<static_cast<unsigned>(groups),
-                                     64 * GroupShape<D>::kWaves, 0, stream>>>(
+        decode_group_kernel<D, F8, kPad><<<static_cast<unsigned>(groups),
+                                           64 * GroupShape<D>::kWaves, 0, stream>>>(
             static_cast<const __bf16*>(q), k_cache, v_cache, k_scale, v_scale, block_table,
-            context_lens, static_cast<__bf16*>(output), it, mbpr, hq, hkv, scale_log2);
+            context_lens, static_cast<__bf16*>(output), it, mbpr, hq, hkv, scale_log2, dr);
         return hipGetLastError();
     }
     const int64_t waves = plan.balanced
@@ -869,17 +889,17 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
     DecodeWs w{};
     if (merge) w = carve(workspace, partial_rows(it.num_items, hq, plan), D);
     const int bw = plan.balanced ? plan.wave_target : 0;
-    decode_split_kernel<D, F8><<<grid, 256, 0, stream>>>(
+    decode_split_kernel<D, F8, kPad><<<grid, 256, 0, stream>>>(
         static_cast<const __bf16*>(q), k_cache, v_cache, k_scale, v_scale, block_table,
         context_lens,
         static_cast<__bf16*>(output), w.o, w.ml, w.desc, it, mbpr, hq, hkv, plan.splits,
-        plan.split_tokens, bw, plan.slots, scale_log2);
+        plan.split_tokens, bw, plan.slots, scale_log2, dr);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess || !merge) return err;
     const int64_t rows = static_cast<int64_t>(it.num_items) * hq;
     const int mgrid = static_cast<int>((rows + kWavesPerGroup - 1) / kWavesPerGroup);
     decode_merge_kernel<D><<<mgrid, 256, 0, stream>>>(static_cast<__bf16*>(output), w.o, w.ml,
-                                                      w.desc, it, hq);
+                                                      w.desc, it, hq, dr);
     return hipGetLastError();
 }
 
@@ -922,11 +942,23 @@ DecodePlan plan_decode(int num_items, int num_kv_heads, int max_ctx, bool allow_
     return p;
 }
 
+int decode_mfma_dim(int head_dim) {
+    // The MFMA tile's head dim for a cache of head_dim: native at 64 / 128 / 256; smaller
+    // dims run padded with zeros when every per-lane piece (8 dims of K, D/16 of V) is
+    // either wholly valid or wholly padding.
+    if (head_dim <= 0 || head_dim % 8 != 0) return 0;
+    if (head_dim <= 64) return 64;
+    if (head_dim <= 128) return 128;
+    return head_dim <= 256 && head_dim % 16 == 0 ? 256 : 0;
+}
+
 size_t decode_workspace_bytes(int num_items, int num_q_heads, int head_dim,
                               const DecodePlan& plan) {
     if (plan.group || (!plan.balanced && plan.splits <= 1)) return 0;
-    // partial O + (m, l) per partial row, then the merge descriptors
-    return desc_offset(partial_rows(num_items, num_q_heads, plan), head_dim) +
+    // partial O (rows of the MFMA head dim) + (m, l) per partial row, then the merge
+    // descriptors
+    const int d = decode_mfma_dim(head_dim);
+    return desc_offset(partial_rows(num_items, num_q_heads, plan), d) +
            static_cast<size_t>(num_items) * num_q_heads * sizeof(MergeDesc);
 }
 
@@ -934,7 +966,12 @@ bool decode_fast_supported(int num_q_heads, int num_kv_heads, int head_dim, int 
     if (block_size != kBlock || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0)
         return false;
     const int G = num_q_heads / num_kv_heads;
-    return G >= 1 && G <= 16 && (head_dim == 64 || head_dim == 128 || head_dim == 256);
+    return G >= 1 && G <= 16 && decode_mfma_dim(head_dim) != 0;
+}
+
+bool decode_fp8_supported(int num_q_heads, int num_kv_heads, int head_dim, int block_size) {
+    return decode_fast_supported(num_q_heads, num_kv_heads, head_dim, block_size) &&
+           decode_mfma_dim(head_dim) == head_dim;
 }
 
 hipError_t decode_attention(const void* q, const void* k_cache, const void* v_cache,
@@ -945,25 +982,27 @@ hipError_t decode_attention(const void* q, const void* k_cache, const void* v_ca
     (void)block_size;
     ItemArgs it{items.num_items, items.item_count, items.item_req, items.query_start_loc,
                 items.denom_eps, items.zero_invalid ? 1 : 0};
-    switch (head_dim) {
+    const int D = decode_mfma_dim(head_dim);
+    const bool pad = D != head_dim;
+#define CCI_DECODE(DD, PP)                                                                   \
+    return launch_decode<DD, false, PP>(q, k_cache, v_cache, nullptr, nullptr, block_table, \
+                                        context_lens, output, it, max_blocks_per_req,        \
+                                        num_q_heads, num_kv_heads, plan, workspace, stream,  \
+                                        head_dim)
+    switch (D) {
         case 64:
-            return launch_decode<64, false>(q, k_cache, v_cache, nullptr, nullptr, block_table,
-                                             context_lens, output, it,
-                                     max_blocks_per_req, num_q_heads, num_kv_heads, plan,
-                                     workspace, stream);
+            if (pad) CCI_DECODE(64, true);
+            CCI_DECODE(64, false);
         case 128:
-            return launch_decode<128, false>(q, k_cache, v_cache, nullptr, nullptr, block_table,
-                                             context_lens, output, it,
-                                      max_blocks_per_req, num_q_heads, num_kv_heads, plan,
-                                      workspace, stream);
+            if (pad) CCI_DECODE(128, true);
+            CCI_DECODE(128, false);
         case 256:
-            return launch_decode<256, false>(q, k_cache, v_cache, nullptr, nullptr, block_table,
-                                             context_lens, output, it,
-                                      max_blocks_per_req, num_q_heads, num_kv_heads, plan,
-                                      workspace, stream);
+            if (pad) CCI_DECODE(256, true);
+            CCI_DECODE(256, false);
         default:
             return hipErrorInvalidValue;
     }
+#undef CCI_DECODE
 }
 
 hipError_t decode_attention_fp8(const void* q, const void* k_cache, const void* v_cache,
@@ -976,17 +1015,17 @@ hipError_t decode_attention_fp8(const void* q, const void* k_cache, const void* 
                 items.denom_eps, items.zero_invalid ? 1 : 0};
     switch (head_dim) {
         case 64:
-            return launch_decode<64, true>(q, k_cache, v_cache, k_scale, v_scale, block_table,
+            return launch_decode<64, true, false>(q, k_cache, v_cache, k_scale, v_scale, block_table,
                                            context_lens, output, it, max_blocks_per_req,
-                                           num_q_heads, num_kv_heads, plan, workspace, stream);
+                                           num_q_heads, num_kv_heads, plan, workspace, stream, 64);
         case 128:
-            return launch_decode<128, true>(q, k_cache, v_cache, k_scale, v_scale, block_table,
+            return launch_decode<128, true, false>(q, k_cache, v_cache, k_scale, v_scale, block_table,
                                             context_lens, output, it, max_blocks_per_req,
-                                            num_q_heads, num_kv_heads, plan, workspace, stream);
+                                            num_q_heads, num_kv_heads, plan, workspace, stream, 128);
         case 256:
-            return launch_decode<256, true>(q, k_cache, v_cache, k_scale, v_scale, block_table,
+            return launch_decode<256, true, false>(q, k_cache, v_cache, k_scale, v_scale, block_table,
                                             context_lens, output, it, max_blocks_per_req,
-                                            num_q_heads, num_kv_heads, plan, workspace, stream);
+                                            num_q_heads, num_kv_heads, plan, workspace, stream, 256);
         default:
             return hipErrorInvalidValue;
     }

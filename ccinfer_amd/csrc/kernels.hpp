@@ -41,8 +41,13 @@ DecodePlan plan_decode(int num_items, int num_kv_heads, int max_ctx, bool allow_
 size_t decode_workspace_bytes(int num_items, int num_q_heads, int head_dim,
                               const DecodePlan& plan);
 
-// Whether the MFMA split-KV decode kernel supports this shape.
+// Whether the MFMA split-KV decode kernel supports this shape (bf16 cache). Head dims that
+// are multiples of 8 up to 128 (of 16 up to 256) run at the next MFMA size of 64 / 128 / 256
+// with the missing dims zero.
 bool decode_fast_supported(int num_q_heads, int num_kv_heads, int head_dim, int block_size);
+
+// The same for an fp8 cache: head dims 64, 128 and 256 only.
+bool decode_fp8_supported(int num_q_heads, int num_kv_heads, int head_dim, int block_size);
 
 // Query rows to attend, described either densely (item i is request i, query row i)
 // or through a device list written by the prefill planner.

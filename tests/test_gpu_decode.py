@@ -114,6 +114,24 @@ def test_head_shapes(gpu, hq, hkv, d):
     assert_attn_close(f32(run_decode(w, gpu)), oracle_decode(w), f"hq{hq}/hkv{hkv}/d{d}")
 
 
+@pytest.mark.parametrize("hq,hkv,d,batch,ctx_hi", [
+    (16, 8, 80, 2, 3000),     # one workgroup per (request, kv_head), parts merged in LDS
+    (8, 2, 32, 3, 900),
+    (8, 4, 192, 2, 2500),
+    (16, 8, 96, 40, 5000),    # balanced split plan + merge kernel
+    (8, 8, 120, 12, 4000),
+    (8, 4, 192, 24, 3000),
+    (16, 4, 112, 64, 2000),
+    (8, 8, 32, 48, 6000)])
+def test_padded_head_dims_every_plan(gpu, hq, hkv, d, batch, ctx_hi):
+    """Head dims below 64 / 128 / 256 run the MFMA kernels padded with zeros; every decode
+    plan (LDS-merged groups, balanced splits with the merge kernel) against the oracle."""
+    say(f"decode padded d={d} hq={hq} hkv={hkv} batch={batch} ctx<={ctx_hi}")
+    w = W.decode_batched(device=gpu, seed=d * 7 + batch, batch=batch, ctx_lo=1, ctx_hi=ctx_hi,
+                         hq=hq, hkv=hkv, d=d, with_write=False)
+    assert_attn_close(f32(run_decode(w, gpu)), oracle_decode(w), f"padded d{d} b{batch}")
+
+
 def test_edge_cases_zero_ctx_overflow_and_holes(gpu):
     say("decode edge cases")
     w = W.decode_batched(device=gpu, seed=21, batch=6, ctx_lo=40, ctx_hi=300, with_write=False)
