@@ -46,6 +46,9 @@ size_t decode_workspace_bytes(int num_items, int num_q_heads, int head_dim,
 // with the missing dims zero.
 bool decode_fast_supported(int num_q_heads, int num_kv_heads, int head_dim, int block_size);
 
+// The MFMA head dim (64 / 128 / 256) that a head_dim runs at, or 0 if none does.
+int decode_mfma_dim(int head_dim);
+
 // The same for an fp8 cache: head dims 64, 128 and 256 only.
 bool decode_fp8_supported(int num_q_heads, int num_kv_heads, int head_dim, int block_size);
 

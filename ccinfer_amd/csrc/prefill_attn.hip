@@ -228,13 +228,14 @@ __device__ __forceinline__ int lds_off(int row, int chunk) {
 // (p%CPR) ^ swizzle(row). Rows outside the visible range (past the context, negative block
 // ids, past the table row) are fetched from `zero_row` so the tile never holds garbage that
 // a masked probability of 0 could turn into NaN. Validity flags go to lvalid[row].
-template <int D>
+// kPad: cache rows hold dr < D dims (a multiple of 8); chunks past dr come from zero_row.
+template <int D, bool kPad = false>
 __device__ __forceinline__ void stage_issue(__bf16* lk, __bf16* lv, uint8_t* lvalid,
                                             const __bf16* __restrict__ k_cache,
                                             const __bf16* __restrict__ v_cache,
                                             const __bf16* __restrict__ zero_row,
                                             const int32_t* lbt, int key_base, int ctx, int nblk,
-                                            int kv_head, int hkv) {
+                                            int kv_head, int hkv, int dr = D) {
     constexpr int CPR = PrefillShape<D>::kCPR;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -250,9 +251,10 @@ __device__ __forceinline__ void stage_issue(__bf16* lk, __bf16* lv, uint8_t* lva
         if (key < ctx && lb < nblk) pb = lbt[lb];
         const __bf16* ks = zero_row;
         const __bf16* vs = zero_row;
-        if (pb >= 0) {
+        if (pb >= 0 && (!kPad || lchunk * 8 < dr)) {
             const int64_t base =
-                ((static_cast<int64_t>(pb) * kBlock + (key & (kBlock - 1))) * hkv + kv_head) * D;
+                ((static_cast<int64_t>(pb) * kBlock + (key & (kBlock - 1))) * hkv + kv_head) *
+                (kPad ? dr : D);
             ks = k_cache + base;
             vs = v_cache + base;
         }
@@ -297,15 +299,18 @@ __device__ __forceinline__ bf16x8 load_vt(const __bf16* lv, int h2, int n, int l
 constexpr float kRescaleSlack = 8.0f;
 constexpr float kMaxInit = -1.0e30f;
 
-template <int D>
+// kPad: q / cache / output rows hold dr < D dims; the kernel runs at D with the missing dims
+// zero.
+template <int D, bool kPad = false>
 __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k_cache,
     const __bf16* __restrict__ v_cache, const int32_t* __restrict__ block_table,
     const int32_t* __restrict__ qsl, const int32_t* __restrict__ context_lens,
     __bf16* __restrict__ out, const int32_t* __restrict__ counts,
     const TileEntry* __restrict__ tiles, const __bf16* __restrict__ zero_row, int total_tokens,
-    int mbpr, int hq, int hkv, int block_size, float scale_log2) {
+    int mbpr, int hq, int hkv, int block_size, float scale_log2, int dr) {
     (void)block_size;  // the fast path is specialised for 16-token blocks
+    const int ds = kPad ? dr : D;  // row stride of q / cache / output (elements)
     using Sh = PrefillShape<D>;
     constexpr int QT = Sh::kQT;
     constexpr int QW = Sh::kQW;
@@ -363,11 +368,12 @@ __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
     for (int qt = 0; qt < QT; ++qt) {
         const int tq = tw + qt * 16 + j;
         const bool live = tq < rows;
-        const __bf16* qv = q + (static_cast<int64_t>(qb + (live ? tq : 0)) * hq + q_head) * D;
+        const __bf16* qv = q + (static_cast<int64_t>(qb + (live ? tq : 0)) * hq + q_head) * ds;
 #pragma unroll
         for (int kk = 0; kk < S; ++kk) {
-            u32x4 w = load16(qv + (kk * 4 + g) * 8);
-            if (!live) w = u32x4{0, 0, 0, 0};
+            const bool ok = !kPad || (kk * 4 + g) * 8 < dr;
+            u32x4 w = load16(qv + (ok ? (kk * 4 + g) * 8 : 0));
+            if (!live || !ok) w = u32x4{0, 0, 0, 0};
             qop[qt][kk] = __builtin_bit_cast(bf16x8, w);
         }
     }
@@ -406,8 +412,8 @@ __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
     __syncthreads();
     const bool holes = s_holes != 0 || nblk_vis > mbpr;
 
-    stage_issue<D>(lds_k0, lds_v0, lds_valid0, k_cache, v_cache, zero_row, lds_bt, 0, ctx, nblk,
-                   kvh, hkv);
+    stage_issue<D, kPad>(lds_k0, lds_v0, lds_valid0, k_cache, v_cache, zero_row, lds_bt, 0, ctx,
+                         nblk, kvh, hkv, dr);
     __builtin_amdgcn_s_waitcnt(0);  // this wavefront's direct-to-LDS loads have landed
     __syncthreads();
 
@@ -520,8 +526,8 @@ __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
         uint8_t* nvalid = B == 0 ? lds_valid1 : lds_valid0;
         const bool more = t + 1 < ntiles;
         if (more) {
-            stage_issue<D>(nk, nv, nvalid, k_cache, v_cache, zero_row, lds_bt,
-                           (t + 1) * kKeysPerTile, ctx, nblk, kvh, hkv);
+            stage_issue<D, kPad>(nk, nv, nvalid, k_cache, v_cache, zero_row, lds_bt,
+                                 (t + 1) * kKeysPerTile, ctx, nblk, kvh, hkv, dr);
         }
         const int key0 = t * kKeysPerTile;
         if (key0 <= wave_max_key) {
@@ -559,9 +565,10 @@ __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
         const int tq = tw + qt * 16 + j;
         if (tq >= rows) continue;
         const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-        __bf16* o = out + (static_cast<int64_t>(qb + tq) * hq + q_head) * D;
+        __bf16* o = out + (static_cast<int64_t>(qb + tq) * hq + q_head) * ds;
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
+            if (kPad && 16 * n + 4 * g >= dr) continue;  // padded dims
             u32x2 w;
             w[0] = pack_bf16x2(acc[qt][n][0] * inv, acc[qt][n][1] * inv);
             w[1] = pack_bf16x2(acc[qt][n][2] * inv, acc[qt][n][3] * inv);
@@ -606,7 +613,11 @@ __host__ __device__ constexpr bool pipe_head_dim(int d) { return d == 64 || d ==
 // staged as bytes into a two-tile ring and dequantised (byte * row scale, rounded to bf16)
 // into a two-tile ring of bf16 tiles in the same swizzled layout, so everything after the
 // staging is the bf16 kernel.
-template <int D, bool F8 = false>
+// kPad (bf16 only): q / cache / output rows hold dr < D dims (a multiple of 8). Staging
+// fetches chunk 0 of the row again in place of the missing chunks (finite values: the Q
+// operand is zero in those dims, so they add exactly 0 to the scores), and the missing
+// output dims are not stored.
+template <int D, bool F8 = false, bool kPad = false>
 __global__ __launch_bounds__((PipeShape<D>::kThreads))
 void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ k_cache_v,
                          const void* __restrict__ v_cache_v, const float* __restrict__ k_scale,
@@ -615,7 +626,10 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
                          const int32_t* __restrict__ qsl,
                          const int32_t* __restrict__ context_lens, __bf16* __restrict__ out,
                          const int32_t* __restrict__ counts, const TileEntry* __restrict__ tiles,
-                         int total_tokens, int mbpr, int hq, int hkv, float scale_log2) {
+                         int total_tokens, int mbpr, int hq, int hkv, float scale_log2,
+                         int dr) {
+    static_assert(!(F8 && kPad), "fp8 runs the native head dims only");
+    const int ds = kPad ? dr : D;  // row stride of q / cache / output (elements)
     using Sh = PipeShape<D>;
     constexpr int S2 = D / 16;   // QK k-steps (32x32x16 MFMA)
     constexpr int NT2 = D / 32;  // PV dim tiles
@@ -709,7 +723,7 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
     // path are treated like holes (the checked path addresses with 64 bits).
     const int max_fast_pb = static_cast<int>(
         min(static_cast<int64_t>(0x7fffffff),
-            static_cast<int64_t>(0xffffffffll / (static_cast<int64_t>(kBlock) * hkv * D * 2)) - 1));
+            static_cast<int64_t>(0xffffffffll / (static_cast<int64_t>(kBlock) * hkv * ds * 2)) - 1));
     bool bad = false;
     for (int lb = threadIdx.x; lb < (F8 ? ntiles * (kKeysPerTile / kBlock) : nblk);
          lb += kPipeThreads) {
@@ -735,9 +749,10 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
         const int row = p / CPR;
         const int lch = (p % CPR) ^ (chunk_swizzle<D>(row) & (CPR - 1));
         st_row[x] = row;
-        st_off[x] = static_cast<uint32_t>((((row & (kBlock - 1)) * hkv + kvh) * D + lch * 8) * 2);
+        const int src = kPad && lch * 8 >= dr ? 0 : lch * 8;
+        st_off[x] = static_cast<uint32_t>((((row & (kBlock - 1)) * hkv + kvh) * ds + src) * 2);
     }
-    const int64_t blk_bytes = static_cast<int64_t>(kBlock) * hkv * D * 2;
+    const int64_t blk_bytes = static_cast<int64_t>(kBlock) * hkv * ds * 2;
 
     // Per-lane LDS read offsets (elements); lane l = 32 h + c (c = l % 32, h = l / 32).
     // K operand of k-step kk: key row c, logical chunk 2 kk + h. Rows 16 apart share a
@@ -915,11 +930,14 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
     {
         const int tq = tw + c32;
         const bool live = tq < rows;
-        const __bf16* qv = q + (static_cast<int64_t>(qb + (live ? tq : 0)) * hq + q_head) * D;
+        const __bf16* qv = q + (static_cast<int64_t>(qb + (live ? tq : 0)) * hq + q_head) * ds;
 #pragma unroll
         for (int kk = 0; kk < S2; ++kk) {
             // rows past the tile's end read row 0 (finite) and are never stored
-            qop[kk] = __builtin_bit_cast(bf16x8, load16(qv + kk * 16 + h32 * 8));
+            const bool ok = !kPad || kk * 16 + h32 * 8 < dr;
+            u32x4 w = load16(qv + (ok ? kk * 16 + h32 * 8 : 0));
+            if (!ok) w = u32x4{0, 0, 0, 0};
+            qop[kk] = __builtin_bit_cast(bf16x8, w);
         }
     }
     __syncthreads();  // block table scanned (and, for fp8, staged)
@@ -1282,11 +1300,12 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
         const int tq = tw + c32;
         if (tq < rows) {
             const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-            __bf16* o = out + (static_cast<int64_t>(qb + tq) * hq + q_head) * D;
+            __bf16* o = out + (static_cast<int64_t>(qb + tq) * hq + q_head) * ds;
 #pragma unroll
             for (int n = 0; n < NT2; ++n) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
+                    if (kPad && 32 * n + 8 * i + 4 * h32 >= dr) continue;  // padded dims
                     u32x2 w;
                     w[0] = pack_bf16x2(acc[n][4 * i] * inv, acc[n][4 * i + 1] * inv);
                     w[1] = pack_bf16x2(acc[n][4 * i + 2] * inv, acc[n][4 * i + 3] * inv);
@@ -1316,14 +1335,15 @@ PrefillLayout prefill_layout(int batch_size, int total_query_tokens, int max_blo
                              int num_q_heads, int num_kv_heads, int head_dim, int block_size) {
     PrefillLayout L{};
     const int G = num_q_heads / num_kv_heads;
-    L.tile_tokens = tile_tokens_for(head_dim, G);
+    const int D = decode_mfma_dim(head_dim);  // the kernels' (padded) head dim
+    L.tile_tokens = tile_tokens_for(D, G);
     L.max_tiles = total_query_tokens / L.tile_tokens + batch_size;
     L.plan = plan_decode(batch_size, num_kv_heads, max_blocks_per_req * block_size, true);
     size_t off = 0;
     L.counts_off = off;
     off = align256(off + 2 * sizeof(int32_t));
-    L.zero_off = off;  // one all-zero K/V row (head_dim bf16), rewritten by the planner
-    off = align256(off + static_cast<size_t>(head_dim) * 2);
+    L.zero_off = off;  // one all-zero K/V row (D bf16), rewritten by the planner
+    off = align256(off + static_cast<size_t>(D) * 2);
     L.tiles_off = off;
     off = align256(off + static_cast<size_t>(L.max_tiles) * sizeof(TileEntry));
     L.dec_off = off;
@@ -1337,34 +1357,35 @@ PrefillLayout prefill_layout(int batch_size, int total_query_tokens, int max_blo
     return L;
 }
 
-template <int D, bool F8>
+// dr: the head dim of q / cache / output rows (dr == D unless kPad).
+template <int D, bool F8, bool kPad>
 hipError_t launch_tiles(const void* q, const void* k_cache, const void* v_cache,
                         const float* k_scale, const float* v_scale,
                         const int32_t* block_table, const int32_t* qsl,
                         const int32_t* context_lens, void* output, int total_query_tokens,
                         int mbpr, int hq, int hkv, int block_size, const int32_t* counts,
                         const TileEntry* tiles, const void* zero_row, int max_tiles,
-                        hipStream_t stream) {
+                        hipStream_t stream, int dr) {
     const int G = hq / hkv;
     const int U = hkv * (G / heads_per_wg(G));
     const int64_t grid = static_cast<int64_t>(max_tiles) * U;
-    const float scale_log2 = kLog2e / sqrtf(static_cast<float>(D));
+    const float scale_log2 = kLog2e / sqrtf(static_cast<float>(dr));
     if constexpr (pipe_head_dim(D)) {
-        prefill_pipe_kernel<D, F8>
+        prefill_pipe_kernel<D, F8, kPad>
             <<<static_cast<unsigned>(grid), PipeShape<D>::kThreads, 0, stream>>>(
             static_cast<const __bf16*>(q), k_cache, v_cache, k_scale, v_scale, block_table, qsl,
             context_lens,
             static_cast<__bf16*>(output), counts, tiles, total_query_tokens, mbpr, hq, hkv,
-            scale_log2);
+            scale_log2, dr);
         return hipGetLastError();
     } else if constexpr (F8) {
         return hipErrorInvalidValue;  // fp8 has the pipelined path only
     } else {
-        prefill_tile_kernel<D><<<static_cast<unsigned>(grid), kThreads, 0, stream>>>(
+        prefill_tile_kernel<D, kPad><<<static_cast<unsigned>(grid), kThreads, 0, stream>>>(
             static_cast<const __bf16*>(q), static_cast<const __bf16*>(k_cache),
             static_cast<const __bf16*>(v_cache), block_table, qsl, context_lens,
             static_cast<__bf16*>(output), counts, tiles, static_cast<const __bf16*>(zero_row),
-            total_query_tokens, mbpr, hq, hkv, block_size, scale_log2);
+            total_query_tokens, mbpr, hq, hkv, block_size, scale_log2, dr);
         return hipGetLastError();
     }
 }
@@ -1376,10 +1397,12 @@ bool prefill_fast_supported(int num_q_heads, int num_kv_heads, int head_dim,
     if (num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0) return false;
     const int G = num_q_heads / num_kv_heads;
     if (G > 16) return false;
-    // head_dim 64 / 128 (bf16) stage any table length; the head_dim-256 kernel and the fp8
-    // staging keep the table row in LDS.
-    if (head_dim == 64 || head_dim == 128) return true;
-    return head_dim == 256 && max_blocks_per_req <= kMaxTableLds;
+    // Head dims run at the MFMA size 64 / 128 / 256 (smaller ones padded with zeros). The
+    // 64 / 128 kernels (bf16) stage any table length; the 256 kernel keeps the table row in
+    // LDS.
+    const int D = decode_mfma_dim(head_dim);
+    if (D == 64 || D == 128) return true;
+    return D == 256 && max_blocks_per_req <= kMaxTableLds;
 }
 
 bool prefill_fp8_supported(int head_dim, int max_blocks_per_req) {
@@ -1425,11 +1448,11 @@ hipError_t prefill_impl(const void* q, const void* k_cache, const void* v_cache,
         int* big = reinterpret_cast<int*>(ws + L.big_off);
         prefill_plan_kernel<true><<<1, 1024, 0, stream>>>(
             query_start_loc, context_lens, batch_size, total_query_tokens, L.tile_tokens, counts,
-            tiles, dec, zero_row, head_dim / 2, big, big + batch_size);
+            tiles, dec, zero_row, decode_mfma_dim(head_dim) / 2, big, big + batch_size);
     } else {
         prefill_plan_kernel<false><<<1, 1024, 0, stream>>>(
             query_start_loc, context_lens, batch_size, total_query_tokens, L.tile_tokens, counts,
-            tiles, dec, zero_row, head_dim / 2, nullptr, nullptr);
+            tiles, dec, zero_row, decode_mfma_dim(head_dim) / 2, nullptr, nullptr);
     }
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
@@ -1465,31 +1488,31 @@ hipError_t prefill_impl(const void* q, const void* k_cache, const void* v_cache,
         if (err == hipSuccess) err = launch_decode_items(overlap->side);
         if (err != hipSuccess) return err;
     }
-    switch (head_dim) {
-        case 64:
-            err = launch_tiles<64, F8>(q, k_cache, v_cache, k_scale, v_scale, block_table,
-                                        query_start_loc,
-                                   context_lens, output, total_query_tokens, max_blocks_per_req,
-                                   num_q_heads, num_kv_heads, block_size, counts, tiles,
-                                   zero_row, L.max_tiles, stream);
-            break;
-        case 128:
-            err = launch_tiles<128, F8>(q, k_cache, v_cache, k_scale, v_scale, block_table,
-                                        query_start_loc,
-                                    context_lens, output, total_query_tokens, max_blocks_per_req,
-                                    num_q_heads, num_kv_heads, block_size, counts, tiles,
-                                    zero_row, L.max_tiles, stream);
-            break;
-        case 256:
-            err = launch_tiles<256, F8>(q, k_cache, v_cache, k_scale, v_scale, block_table,
-                                        query_start_loc,
-                                    context_lens, output, total_query_tokens, max_blocks_per_req,
-                                    num_q_heads, num_kv_heads, block_size, counts, tiles,
-                                    zero_row, L.max_tiles, stream);
-            break;
-        default:
-            return hipErrorInvalidValue;
+    const int D = decode_mfma_dim(head_dim);
+    const bool pad = D != head_dim;
+#define CCI_TILES(DD, PP)                                                                    \
+    launch_tiles<DD, F8, PP>(q, k_cache, v_cache, k_scale, v_scale, block_table,             \
+                             query_start_loc, context_lens, output, total_query_tokens,      \
+                             max_blocks_per_req, num_q_heads, num_kv_heads, block_size,      \
+                             counts, tiles, zero_row, L.max_tiles, stream, head_dim)
+    if (F8 && pad) {
+        err = hipErrorInvalidValue;  // fp8 runs the native head dims only
+    } else {
+        switch (D) {
+            case 64:
+                err = pad ? CCI_TILES(64, !F8) : CCI_TILES(64, false);
+                break;
+            case 128:
+                err = pad ? CCI_TILES(128, !F8) : CCI_TILES(128, false);
+                break;
+            case 256:
+                err = pad ? CCI_TILES(256, !F8) : CCI_TILES(256, false);
+                break;
+            default:
+                err = hipErrorInvalidValue;
+        }
     }
+#undef CCI_TILES
     if (fork) {
         // join even when the tile launch failed, so the side stream's work is ordered
         const hipError_t je = hipEventRecord(overlap->join, overlap->side);

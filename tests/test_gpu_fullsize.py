@@ -94,7 +94,10 @@ def test_config5_decode_all_rows_poisoned(gpu):
 
 @pytest.mark.parametrize("hq,hkv,d,prefix,new,holes", [
     (16, 8, 128, 512, 300, False), (16, 8, 128, 96, 700, True), (32, 8, 128, 64, 257, False),
-    (8, 8, 64, 128, 400, True), (16, 8, 256, 48, 200, True)])
+    (8, 8, 64, 128, 400, True), (16, 8, 256, 48, 200, True),
+    # head dims below 64 / 128 / 256 run those kernels padded with zeros
+    (16, 8, 80, 208, 300, True), (8, 2, 32, 128, 400, False), (8, 4, 192, 64, 250, True),
+    (16, 4, 112, 96, 333, False), (4, 4, 120, 512, 129, True), (8, 8, 72, 64, 200, False)])
 def test_prefill_poisoned_shapes(gpu, hq, hkv, d, prefix, new, holes):
     """Ragged tiles, a shared prefix and (optionally) table holes, on every head shape's
     fast path, with all unreadable slots poisoned."""
@@ -109,6 +112,17 @@ def test_prefill_poisoned_shapes(gpu, hq, hkv, d, prefix, new, holes):
         w.block_table = bt
     poison_unused(w, gpu)
     assert_attn_close(f32(run_prefill(w, gpu)), oracle_prefill(w), "poisoned prefill")
+
+
+@pytest.mark.parametrize("d", [96, 192])
+def test_mixed_padded_head_dim_poisoned(gpu, d):
+    """A mixed batch (chunked prefills + decode items) at a padded head dim."""
+    say(f"mixed batch d={d}, unused slots poisoned")
+    w = W.mixed_step(device=gpu, seed=d, n_chunks=3, chunk=200, prefix_hi=512, n_decode=40,
+                     dec_lo=16, dec_hi=3000, hq=8, hkv=4, d=d)
+    write_new(w, gpu)
+    poison_unused(w, gpu)
+    assert_attn_close(f32(run_prefill(w, gpu)), oracle_prefill(w), f"mixed d{d}")
 
 
 def test_prefill_fp8_poisoned(gpu):
