@@ -598,7 +598,8 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     const float* __restrict__ v_scale, const int32_t* __restrict__ block_table,
     const int32_t* __restrict__ context_lens, __bf16* __restrict__ out, float* __restrict__ ws_o,
     float* __restrict__ ws_ml, MergeDesc* __restrict__ desc, ItemArgs items, int mbpr, int hq,
-    int hkv, int splits, int split_tokens, int balanced_w, int slots, float scale_log2, int dr) {
+    int hkv, int splits, int split_tokens, int balanced_w, int slots, float scale_log2, int dr,
+    int rep) {
     const int ds = kPad ? dr : D;  // q / output row stride
     constexpr int NV = DecodeShape<D>::kNV;
     using Cache = std::conditional_t<F8, uint8_t, __bf16>;
@@ -662,8 +663,8 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     load_split_inputs<D, F8, kPad>(q, block_table + static_cast<int64_t>(req) * mbpr, mbpr, qrow,
                                    hq, h, G, begin, end, lane, in, dr);
     SoftmaxState<D> st;
-    run_split<D, F8, kPad>(k_cache, v_cache, k_scale, v_scale, in, hkv, h, begin, end, scale_log2,
-                           lane, st, dr);
+    run_split<D, F8, kPad>(k_cache, v_cache, k_scale, v_scale, in, hkv / rep, h / rep, begin, end,
+                           scale_log2, lane, st, dr);
     const float l_tot = wave_sum_xor16_32(st.l);
     const bool live = j < G;
     const int head = h * G + j;
@@ -730,7 +731,7 @@ __global__ __launch_bounds__(64 * GroupShape<D>::kWaves) void decode_group_kerne
     const void* __restrict__ v_cache_v, const float* __restrict__ k_scale,
     const float* __restrict__ v_scale, const int32_t* __restrict__ block_table,
     const int32_t* __restrict__ context_lens, __bf16* __restrict__ out, ItemArgs items,
-    int mbpr, int hq, int hkv, float scale_log2, int dr) {
+    int mbpr, int hq, int hkv, float scale_log2, int dr, int rep) {
     const int ds = kPad ? dr : D;  // q / output row stride
     constexpr int W = GroupShape<D>::kWaves;
     constexpr int NV = DecodeShape<D>::kNV;
@@ -769,8 +770,8 @@ __global__ __launch_bounds__(64 * GroupShape<D>::kWaves) void decode_group_kerne
     const int end = min(ctx, tbl_end);
     SoftmaxState<D> st;
     if (begin < end) {
-        run_split<D, F8, kPad>(k_cache, v_cache, k_scale, v_scale, in, hkv, h, begin, end,
-                               scale_log2, lane, st, dr);
+        run_split<D, F8, kPad>(k_cache, v_cache, k_scale, v_scale, in, hkv / rep, h / rep, begin,
+                               end, scale_log2, lane, st, dr);
     } else {
 #pragma unroll
         for (int n = 0; n < NV; ++n) st.acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -865,6 +866,13 @@ DecodeWs carve(void* workspace, size_t rows, int d) {
     return w;
 }
 
+// Smallest r with G % r == 0 and G / r <= 16 (one MFMA N-tile of query heads).
+int decode_head_rep(int G) {
+    int r = (G + 15) / 16;
+    while (G % r != 0) ++r;
+    return r;
+}
+
 // dr: the head dim of q / cache / output rows (dr == D unless kPad).
 template <int D, bool F8, bool kPad>
 hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache,
@@ -873,12 +881,16 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
                          const ItemArgs& it, int mbpr, int hq, int hkv, const DecodePlan& plan,
                          void* workspace, hipStream_t stream, int dr) {
     const float scale_log2 = kLog2e / sqrtf(static_cast<float>(dr));
+    // Query groups larger than one MFMA N-tile run as `rep` virtual kv heads of hq / hkv /
+    // rep query heads each; virtual head v reads cache head v / rep.
+    const int rep = decode_head_rep(hq / hkv);
+    hkv *= rep;
     if (plan.group) {
         const int64_t groups = static_cast<int64_t>(it.num_items) * hkv;
         decode_group_kernel<D, F8, kPad><<<static_cast<unsigned>(groups),
                                            64 * GroupShape<D>::kWaves, 0, stream>>>(
             static_cast<const __bf16*>(q), k_cache, v_cache, k_scale, v_scale, block_table,
-            context_lens, static_cast<__bf16*>(output), it, mbpr, hq, hkv, scale_log2, dr);
+            context_lens, static_cast<__bf16*>(output), it, mbpr, hq, hkv, scale_log2, dr, rep);
         return hipGetLastError();
     }
     const int64_t waves = plan.balanced
@@ -893,7 +905,7 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
         static_cast<const __bf16*>(q), k_cache, v_cache, k_scale, v_scale, block_table,
         context_lens,
         static_cast<__bf16*>(output), w.o, w.ml, w.desc, it, mbpr, hq, hkv, plan.splits,
-        plan.split_tokens, bw, plan.slots, scale_log2, dr);
+        plan.split_tokens, bw, plan.slots, scale_log2, dr, rep);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess || !merge) return err;
     const int64_t rows = static_cast<int64_t>(it.num_items) * hq;
@@ -966,7 +978,7 @@ bool decode_fast_supported(int num_q_heads, int num_kv_heads, int head_dim, int 
     if (block_size != kBlock || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0)
         return false;
     const int G = num_q_heads / num_kv_heads;
-    return G >= 1 && G <= 16 && decode_mfma_dim(head_dim) != 0;
+    return G >= 1 && decode_mfma_dim(head_dim) != 0;
 }
 
 bool decode_fp8_supported(int num_q_heads, int num_kv_heads, int head_dim, int block_size) {

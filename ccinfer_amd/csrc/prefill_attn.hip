@@ -1395,8 +1395,6 @@ hipError_t launch_tiles(const void* q, const void* k_cache, const void* v_cache,
 bool prefill_fast_supported(int num_q_heads, int num_kv_heads, int head_dim,
                             int max_blocks_per_req) {
     if (num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0) return false;
-    const int G = num_q_heads / num_kv_heads;
-    if (G > 16) return false;
     // Head dims run at the MFMA size 64 / 128 / 256 (smaller ones padded with zeros). The
     // 64 / 128 kernels (bf16) stage any table length; the 256 kernel keeps the table row in
     // LDS.

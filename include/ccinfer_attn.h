@@ -115,8 +115,9 @@ size_t ccinfer_decode_workspace_size(int batch_size, int max_blocks_per_req, int
  * [max_blocks_per_req] int32; context_lens: [batch_size] int32, including the current
  * token (whose K/V must already be written). cache_block_size must be 16 and head_dim one
  * of {32,64,80,96,112,120,128,192,256} (as in the reference); all of them run the MFMA
- * kernels (32 padded to 64, 80-120 to 128, 192 to 256, with zeros) for query groups
- * num_q_heads / num_kv_heads of at most 16. Unlike the reference, there is no
+ * kernels (32 padded to 64, 80-120 to 128, 192 to 256, with zeros), for any query group
+ * size (groups above 16 heads run as several groups of at most 16 over the same KV head).
+ * Unlike the reference, there is no
  * context-length ceiling (split-KV). Batches of 1-3 requests with table rows of at most
  * 4096 positions run in a single launch and need no workspace. */
 int ccinfer_decode_attention(const void* q, const void* k_cache, const void* v_cache,
@@ -158,8 +159,8 @@ int ccinfer_write_kv_cache_fp8(const void* k_new, const void* v_new, void* k_cac
 
 /* Replaces launch_decode_attention (src/kernel/cuda_kernels.h:72-77) for an fp8 cache: the
  * same semantics, plan and workspace (ccinfer_decode_workspace_size) as
- * ccinfer_decode_attention, with K/V read as byte * row scale. head_dim 64, 128 or 256 and
- * at most 16 query heads per KV head (CCINFER_ERR_UNSUPPORTED otherwise). */
+ * ccinfer_decode_attention, with K/V read as byte * row scale. head_dim 64, 128 or 256
+ * (CCINFER_ERR_UNSUPPORTED otherwise). */
 int ccinfer_decode_attention_fp8(const void* q, const void* k_cache, const void* v_cache,
                                  const float* k_scale, const float* v_scale,
                                  const int32_t* block_table, const int32_t* context_lens,
@@ -179,8 +180,8 @@ size_t ccinfer_prefill_workspace_size(int batch_size, int total_query_tokens,
  * [batch_size + 1]; context_lens[r] = prefix_r + query_len_r; query i of request r sees
  * cache positions [0, prefix_r + i]. Mixed batches (single-token decode items next to
  * prompt chunks) are accepted, as in the reference. head_dim <= 256. As in the reference,
- * neither the batch size nor the table length is bounded. The MFMA path covers query
- * groups of at most 16 and head dims that are multiples of 8 up to 128 (at any size; those
+ * neither the batch size nor the table length is bounded. The MFMA path covers every
+ * query group size and head dims that are multiples of 8 up to 128 (at any size; those
  * below 64 / 128 run padded with zeros) or multiples of 16 up to 256 (up to 4096 blocks per
  * table row); other shapes run the generic kernel. A mixed batch's
  * decode items run after the prompt tiles on `stream`. */

@@ -104,7 +104,8 @@ def test_config5_long_context_sampled(gpu):
 
 
 @pytest.mark.parametrize("hq,hkv,d", [(16, 8, 64), (16, 8, 256), (8, 8, 128), (32, 8, 128),
-                                      (64, 4, 128), (32, 1, 128),  # G=16 fast, G=32 generic
+                                      (64, 4, 128), (32, 1, 128),  # G=16, G=32 (2 x 16)
+                                      (48, 2, 128), (17, 1, 64), (64, 1, 96),  # G=24, 17, 64
                                       (16, 8, 80), (12, 4, 96), (8, 2, 32), (8, 4, 192),
                                       (4, 2, 112), (4, 4, 120)])
 def test_head_shapes(gpu, hq, hkv, d):

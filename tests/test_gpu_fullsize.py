@@ -114,12 +114,13 @@ def test_prefill_poisoned_shapes(gpu, hq, hkv, d, prefix, new, holes):
     assert_attn_close(f32(run_prefill(w, gpu)), oracle_prefill(w), "poisoned prefill")
 
 
-@pytest.mark.parametrize("d", [96, 192])
-def test_mixed_padded_head_dim_poisoned(gpu, d):
-    """A mixed batch (chunked prefills + decode items) at a padded head dim."""
-    say(f"mixed batch d={d}, unused slots poisoned")
-    w = W.mixed_step(device=gpu, seed=d, n_chunks=3, chunk=200, prefix_hi=512, n_decode=40,
-                     dec_lo=16, dec_hi=3000, hq=8, hkv=4, d=d)
+@pytest.mark.parametrize("d,hq,hkv", [(96, 8, 4), (192, 8, 4), (128, 32, 1)])
+def test_mixed_padded_head_dim_or_wide_group_poisoned(gpu, d, hq, hkv):
+    """A mixed batch (chunked prefills + decode items) at a padded head dim, or with 32
+    query heads per KV head."""
+    say(f"mixed batch d={d} hq={hq} hkv={hkv}, unused slots poisoned")
+    w = W.mixed_step(device=gpu, seed=d + hq, n_chunks=3, chunk=200, prefix_hi=512,
+                     n_decode=40, dec_lo=16, dec_hi=3000, hq=hq, hkv=hkv, d=d)
     write_new(w, gpu)
     poison_unused(w, gpu)
     assert_attn_close(f32(run_prefill(w, gpu)), oracle_prefill(w), f"mixed d{d}")

@@ -150,7 +150,7 @@ def test_plan_with_thousands_of_requests(gpu):
 @pytest.mark.parametrize("hq,hkv,d,new,prefix", [
     (16, 8, 128, 200, 48), (4, 4, 128, 70, 0), (16, 4, 128, 130, 32), (8, 8, 64, 90, 16),
     (16, 8, 256, 75, 32), (6, 2, 128, 40, 16), (16, 8, 96, 37, 16), (4, 2, 80, 33, 0),
-    (32, 2, 128, 20, 16)])
+    (32, 2, 128, 20, 16), (32, 1, 128, 100, 16), (17, 1, 64, 70, 0), (48, 2, 96, 60, 32)])
 def test_head_shapes_and_ragged_lengths(gpu, hq, hkv, d, new, prefix):
     say(f"prefill shape hq={hq} hkv={hkv} d={d} new={new} prefix={prefix}")
     w = W.prefill_prefix(device=gpu, seed=hq + d + new, n_seqs=3, prefix=prefix, new=new,
