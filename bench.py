@@ -118,6 +118,20 @@ def time_loop(fn, steps: int, warmup: int, stream: torch.cuda.Stream):
     return start.elapsed_time(end) / steps, (t1 - t0) * 1e3 / steps
 
 
+def side_span_ms(ops: "Ops", stream: torch.cuda.Stream, n: int) -> float:
+    """Median time from the start of a mixed prefill step (on `stream`) to the end of its
+    side-stream work (the decode items), over n steps."""
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    with torch.cuda.stream(stream):
+        for a, b in zip(starts, ends):
+            a.record(stream)
+            ops.prefill()
+            b.record(ops.side.stream)
+            torch.cuda.synchronize()
+    return float(np.median([a.elapsed_time(b) for a, b in zip(starts, ends)]))
+
+
 def traffic_from_profiles(kernel_tag: str):
     """HBM bytes per dispatch recorded by the rocprofv3 --pmc runs (profiles/*.md)."""
     f = PROFILES / f"{kernel_tag}.pmc.md"
@@ -339,6 +353,12 @@ def run(args):
         r = {"ms_per_step": ms, "host_ms_per_step": host_ms, "decode_kv_bytes": dbytes,
              "prefill_flops": flops, "roofline_ms": roof_s * 1e3,
              "roofline_frac": roof_s / (ms * 1e-3)}
+        # The decode items run on the side stream beside the prompt tiles: their span is
+        # from the step's start (planner included) to the side stream's last kernel.
+        span = side_span_ms(ops, stream, max(5, args.steps // 4))
+        r["decode_span_ms"] = span
+        r["decode_GBps"] = dbytes / (span * 1e-3) / 1e9
+        r["decode_hbm_frac"] = dbytes / (span * 1e-3) / HBM_PEAK
         out["4_mixed_4x512+128dec"] = r
         del w, ops
 
