@@ -456,6 +456,18 @@ __device__ void merge_row(const float* __restrict__ ws_o, const float* __restric
                           int dr = D) {
     constexpr int kPer = D / 64;
     constexpr int kBatch = 8;
+    // The first batch of partial rows is loaded together with the (m, l) pairs, before the
+    // row max is known (two memory round trips per row instead of three).
+    float v_first[kBatch][kPer];
+    {
+        const float* po = ws_o + base * D + lane * kPer;
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int t = min(u, ns - 1);
+#pragma unroll
+            for (int x = 0; x < kPer; ++x) v_first[u][x] = po[t * D + x];
+        }
+    }
     float mmax = kNegInf;
     for (int s = lane; s < ns; s += 64) mmax = fmaxf(mmax, ws_ml[(base + s) * 2]);
 #pragma unroll
@@ -476,11 +488,18 @@ __device__ void merge_row(const float* __restrict__ ws_o, const float* __restric
             const float* po = ws_o + (base + sb) * D + lane * kPer;
             for (int t0 = 0; t0 < nt; t0 += kBatch) {
                 float v[kBatch][kPer];
+                if (sb == 0 && t0 == 0) {
 #pragma unroll
-                for (int u = 0; u < kBatch; ++u) {
-                    const int t = min(t0 + u, nt - 1);  // clamped: the weight of a repeat is 0
+                    for (int u = 0; u < kBatch; ++u)
 #pragma unroll
-                    for (int x = 0; x < kPer; ++x) v[u][x] = po[t * D + x];
+                        for (int x = 0; x < kPer; ++x) v[u][x] = v_first[u][x];
+                } else {
+#pragma unroll
+                    for (int u = 0; u < kBatch; ++u) {
+                        const int t = min(t0 + u, nt - 1);  // clamped: a repeat's weight is 0
+#pragma unroll
+                        for (int x = 0; x < kPer; ++x) v[u][x] = po[t * D + x];
+                    }
                 }
 #pragma unroll
                 for (int u = 0; u < kBatch; ++u) {
