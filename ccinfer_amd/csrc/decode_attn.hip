@@ -983,6 +983,20 @@ int decode_mfma_dim(int head_dim) {
     return head_dim <= 256 && head_dim % 16 == 0 ? 256 : 0;
 }
 
+DecodePlan plan_decode_items(int num_items, int num_kv_heads, int max_ctx) {
+    // The decode items of a prefill batch: their count is known on the device only, and is
+    // often zero (a pure prompt batch). One launch of one workgroup per possible (item,
+    // kv_head) costs far less than the split plan's two launches, each of which dispatches a
+    // grid sized for the batch's longest context.
+    constexpr int64_t kMaxGroups = 2048;
+    if (max_ctx <= kGroupMaxCtx && static_cast<int64_t>(num_items) * num_kv_heads <= kMaxGroups) {
+        DecodePlan p;
+        p.group = true;
+        return p;
+    }
+    return plan_decode(num_items, num_kv_heads, max_ctx, true);
+}
+
 size_t decode_workspace_bytes(int num_items, int num_q_heads, int head_dim,
                               const DecodePlan& plan) {
     if (plan.group || (!plan.balanced && plan.splits <= 1)) return 0;
