@@ -119,6 +119,10 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(
     int zero_words, int* __restrict__ big_ntiles, int* __restrict__ big_scan) {
     __shared__ int lds_ntiles[kBig ? 1 : kMaxPlanRequests];
     __shared__ int lds_scan[kBig ? 1 : kMaxPlanRequests];
+    // Each request's query length and cached prefix, read once (the bucket pass and the
+    // scatter pass need them again).
+    __shared__ int lds_qlen[kBig ? 1 : kMaxPlanRequests];
+    __shared__ int lds_prefix[kBig ? 1 : kMaxPlanRequests];
     int* s_ntiles = kBig ? big_ntiles : lds_ntiles;
     int* s_scan = kBig ? big_scan : lds_scan;
     __shared__ int s_hist[kBuckets];
@@ -140,6 +144,10 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(
         const int qe = qe_raw < total_tokens ? qe_raw : total_tokens;
         const int rows = qe - (qb > 0 ? qb : 0);
         const int prefix = context_lens[b] - qlen;
+        if constexpr (!kBig) {
+            lds_qlen[b] = qlen;
+            lds_prefix[b] = prefix;
+        }
         int n = 0;
         if (qlen > 0 && prefix >= 0 && qb >= 0 && rows > 0) {
             if (qlen == 1) {
@@ -168,8 +176,8 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(
         *r_out = t - (s_scan[lo] - s_ntiles[lo]);
     };
     auto bucket_of = [&](int b, int r) {
-        const int qlen = qsl[b + 1] - qsl[b];
-        const int prefix = context_lens[b] - qlen;
+        const int qlen = kBig ? qsl[b + 1] - qsl[b] : lds_qlen[b];
+        const int prefix = kBig ? context_lens[b] - qlen : lds_prefix[b];
         int last = (r + 1) * tile_tokens;
         if (last > qlen) last = qlen;
         const int cost = (prefix + last) >> 6;
