@@ -559,6 +559,18 @@ def sweep(kind: str) -> None:
                       f"{gbs:.0f} GB/s | {gbs * 1e9 / HBM_PEAK:.0%} HBM |", flush=True)
                 del w, ops
                 torch.cuda.empty_cache()
+        # other head dims (below 64 / 128 / 256: padded MFMA tiles) and query-group sizes
+        for hq, hkv, d in ((16, 8, 64), (16, 8, 96), (16, 8, 80), (8, 4, 192), (16, 8, 256),
+                           (64, 2, 128), (32, 1, 128)):
+            w = W.decode_batched(device=dev, batch=64, ctx_lo=4096, ctx_hi=4096, hq=hq,
+                                 hkv=hkv, d=d, with_write=False)
+            ops = Ops(w, dev, stream)
+            ms, _ = time_loop(ops.decode, 20, 3, stream)
+            gbs = w.kv_bytes() / (ms * 1e-3) / 1e9
+            print(f"| B=64 ctx=4096 Hq/Hkv={hq}/{hkv} d={d} | {ms * 1e3:.1f} | "
+                  f"{gbs:.0f} GB/s | {gbs * 1e9 / HBM_PEAK:.0%} HBM |", flush=True)
+            del w, ops
+            torch.cuda.empty_cache()
     else:
         for n_seqs, prefix, new, hq, hkv in ((8, 512, 1536, 16, 8), (8, 0, 2048, 16, 8),
                                              (4, 4096, 2048, 16, 8), (2, 16384, 2048, 16, 8),
@@ -570,6 +582,20 @@ def sweep(kind: str) -> None:
             ms, _ = time_loop(ops.prefill, 20, 3, stream)
             tf = W.prefill_flops(w) / (ms * 1e-3) / 1e12
             print(f"| {n_seqs} x ({prefix} cached + {new} new) Hq/Hkv={hq}/{hkv} | "
+                  f"{ms * 1e3:.1f} | {tf:.0f} TFLOP/s | {tf * 1e12 / BF16_PEAK:.0%} bf16 MFMA |",
+                  flush=True)
+            del w, ops
+            torch.cuda.empty_cache()
+        # other head dims (padded MFMA tiles below 64 / 128 / 256) and query-group sizes;
+        # the FLOPs count the real head dim
+        for hq, hkv, d in ((16, 8, 64), (16, 8, 96), (16, 8, 80), (8, 4, 192), (16, 8, 256),
+                           (64, 2, 128)):
+            w = W.prefill_prefix(device=dev, n_seqs=8, prefix=512, new=1536, hq=hq, hkv=hkv,
+                                 d=d, share_pairs=())
+            ops = Ops(w, dev, stream)
+            ms, _ = time_loop(ops.prefill, 20, 3, stream)
+            tf = W.prefill_flops(w) / (ms * 1e-3) / 1e12
+            print(f"| 8 x (512 cached + 1536 new) Hq/Hkv={hq}/{hkv} d={d} | "
                   f"{ms * 1e3:.1f} | {tf:.0f} TFLOP/s | {tf * 1e12 / BF16_PEAK:.0%} bf16 MFMA |",
                   flush=True)
             del w, ops

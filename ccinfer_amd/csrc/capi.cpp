@@ -241,7 +241,8 @@ size_t ccinfer_decode_workspace_size(int batch_size, int max_blocks_per_req, int
         return 0;
     if (!decode_fast_supported(num_q_heads, num_kv_heads, head_dim, cache_block_size)) return 0;
     const DecodePlan plan =
-        plan_decode(batch_size, num_kv_heads, max_blocks_per_req * cache_block_size, true);
+        plan_decode(batch_size, num_q_heads, num_kv_heads,
+                    max_blocks_per_req * cache_block_size, true);
     return decode_workspace_bytes(batch_size, num_q_heads, head_dim, plan);
 }
 
@@ -264,7 +265,8 @@ int ccinfer_decode_attention(const void* q, const void* k_cache, const void* v_c
             as_stream(stream)));
     }
     const DecodePlan plan =
-        plan_decode(batch_size, num_kv_heads, max_blocks_per_req * cache_block_size, true);
+        plan_decode(batch_size, num_q_heads, num_kv_heads,
+                    max_blocks_per_req * cache_block_size, true);
     const size_t need = decode_workspace_bytes(batch_size, num_q_heads, head_dim, plan);
     if (need > 0 && (workspace == nullptr || workspace_bytes < need))
         return CCINFER_ERR_INVALID_ARGUMENT;
@@ -309,7 +311,8 @@ int ccinfer_decode_attention_fp8(const void* q, const void* k_cache, const void*
     if (!fast_aligned(q, k_cache, v_cache, output) || !aligned16(k_scale) || !aligned16(v_scale))
         return CCINFER_ERR_INVALID_ARGUMENT;
     const DecodePlan plan =
-        plan_decode(batch_size, num_kv_heads, max_blocks_per_req * cache_block_size, true);
+        plan_decode(batch_size, num_q_heads, num_kv_heads,
+                    max_blocks_per_req * cache_block_size, true);
     const size_t need = decode_workspace_bytes(batch_size, num_q_heads, head_dim, plan);
     if (need > 0 && (workspace == nullptr || workspace_bytes < need))
         return CCINFER_ERR_INVALID_ARGUMENT;

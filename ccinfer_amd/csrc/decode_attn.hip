@@ -61,7 +61,13 @@ constexpr int64_t kTargetWaves = 4096;
 constexpr int kBalancedMinItems = 4;
 // Longest table row (positions) of the single-launch group plan: parts of at most 512
 // positions at 8 wavefronts (1024 at 4), within one split's 2048.
-constexpr int kGroupMaxCtx = 4096;
+// The group plan (one workgroup per (request, kv_head), parts merged in LDS) streams a row
+// from one CU, which reads ~30 GB/s; it pays off only where the row is short enough that
+// one launch beats the split plan's two. Measured (one MI355X, 16q/8kv or 32q/8kv, d=128):
+// batch 1, 512 positions, 16 q-heads: 8.1 us vs 8.6 (split + merge); batch 1 with 32
+// q-heads, batch 2 or 3, or 1,024+ positions: slower (10.1-67 us vs 8.9-26).
+constexpr int kGroupMaxCtx = 512;
+constexpr int kGroupMaxRows = 16;  // (request, q-head) rows of a plain decode batch
 
 struct ItemArgs {
     int num_items;
@@ -936,11 +942,15 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
 
 }  // namespace
 
-DecodePlan plan_decode(int num_items, int num_kv_heads, int max_ctx, bool allow_balanced) {
+DecodePlan plan_decode(int num_items, int num_q_heads, int num_kv_heads, int max_ctx,
+                       bool allow_balanced) {
+    // Query groups above one MFMA N-tile run as several virtual kv heads (launch_decode).
+    num_kv_heads *= decode_head_rep(num_q_heads / num_kv_heads);
     DecodePlan p;
-    // Batches of 1-3 requests: one workgroup per (request, kv_head) merges its parts in LDS
-    // (a single launch; these batches are latency-bound).
-    if (num_items < kBalancedMinItems && max_ctx <= kGroupMaxCtx) {
+    // Tiny batches: one workgroup per (request, kv_head) merges its parts in LDS (a single
+    // launch; these batches are latency-bound).
+    if (static_cast<int64_t>(num_items) * num_q_heads <= kGroupMaxRows &&
+        max_ctx <= kGroupMaxCtx) {
         p.group = true;
         return p;
     }
@@ -983,18 +993,20 @@ int decode_mfma_dim(int head_dim) {
     return head_dim <= 256 && head_dim % 16 == 0 ? 256 : 0;
 }
 
-DecodePlan plan_decode_items(int num_items, int num_kv_heads, int max_ctx) {
+DecodePlan plan_decode_items(int num_items, int num_q_heads, int num_kv_heads, int max_ctx) {
     // The decode items of a prefill batch: their count is known on the device only, and is
     // often zero (a pure prompt batch). One launch of one workgroup per possible (item,
     // kv_head) costs far less than the split plan's two launches, each of which dispatches a
     // grid sized for the batch's longest context.
     constexpr int64_t kMaxGroups = 2048;
-    if (max_ctx <= kGroupMaxCtx && static_cast<int64_t>(num_items) * num_kv_heads <= kMaxGroups) {
+    const int64_t groups = static_cast<int64_t>(num_items) * num_kv_heads *
+                           decode_head_rep(num_q_heads / num_kv_heads);
+    if (max_ctx <= kGroupMaxCtx && groups <= kMaxGroups) {
         DecodePlan p;
         p.group = true;
         return p;
     }
-    return plan_decode(num_items, num_kv_heads, max_ctx, true);
+    return plan_decode(num_items, num_q_heads, num_kv_heads, max_ctx, true);
 }
 
 size_t decode_workspace_bytes(int num_items, int num_q_heads, int head_dim,

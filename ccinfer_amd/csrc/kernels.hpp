@@ -35,10 +35,11 @@ constexpr int kBalancedMaxItems = 256;
 
 // Returns the plan for a batch whose longest context is max_ctx tokens. allow_balanced: the
 // balanced mode may be used (it resolves items through DecodeItems like the kernel does).
-DecodePlan plan_decode(int num_items, int num_kv_heads, int max_ctx, bool allow_balanced);
+DecodePlan plan_decode(int num_items, int num_q_heads, int num_kv_heads, int max_ctx,
+                       bool allow_balanced);
 
 // The plan for the single-token items of a prefill batch (at most num_items of them).
-DecodePlan plan_decode_items(int num_items, int num_kv_heads, int max_ctx);
+DecodePlan plan_decode_items(int num_items, int num_q_heads, int num_kv_heads, int max_ctx);
 
 // Scratch bytes the split-KV decode needs for `num_items` query rows.
 size_t decode_workspace_bytes(int num_items, int num_q_heads, int head_dim,

@@ -118,8 +118,8 @@ size_t ccinfer_decode_workspace_size(int batch_size, int max_blocks_per_req, int
  * kernels (32 padded to 64, 80-120 to 128, 192 to 256, with zeros), for any query group
  * size (groups above 16 heads run as several groups of at most 16 over the same KV head).
  * Unlike the reference, there is no
- * context-length ceiling (split-KV). Batches of 1-3 requests with table rows of at most
- * 4096 positions run in a single launch and need no workspace. */
+ * context-length ceiling (split-KV). Batches of at most 16 (request, q-head) rows with
+ * table rows of at most 512 positions run in a single launch and need no workspace. */
 int ccinfer_decode_attention(const void* q, const void* k_cache, const void* v_cache,
                              const int32_t* block_table, const int32_t* context_lens,
                              void* output, int batch_size, int max_blocks_per_req,

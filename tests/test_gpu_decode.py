@@ -116,7 +116,10 @@ def test_head_shapes(gpu, hq, hkv, d):
 
 
 @pytest.mark.parametrize("hq,hkv,d,batch,ctx_hi", [
-    (16, 8, 80, 2, 3000),     # one workgroup per (request, kv_head), parts merged in LDS
+    (16, 8, 80, 1, 500),      # one workgroup per (request, kv_head), parts merged in LDS
+    (8, 2, 32, 1, 400),
+    (8, 4, 192, 1, 300),
+    (16, 8, 80, 2, 3000),     # fixed split plan + merge kernel
     (8, 2, 32, 3, 900),
     (8, 4, 192, 2, 2500),
     (16, 8, 96, 40, 5000),    # balanced split plan + merge kernel

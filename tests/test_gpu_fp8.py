@@ -115,6 +115,7 @@ def _dequant_bf16(kc, ks, hkv):
 
 @pytest.mark.parametrize("hq,hkv,d,n_seqs,prefix,new", [
     (16, 8, 128, 3, 64, 200), (16, 4, 128, 2, 48, 130), (8, 8, 64, 3, 16, 90),
+    (32, 1, 128, 2, 32, 100),  # 32 query heads per KV head
 ])
 def test_prefill_fp8_equals_bf16_prefill_of_its_dequantised_cache(gpu, hq, hkv, d, n_seqs,
                                                                     prefix, new):
@@ -186,7 +187,8 @@ def test_prefill_fp8_config3_equals_bf16_prefill_of_dequantised_cache(gpu):
     assert bool(torch.isfinite(out8.float()).all())
 
 
-@pytest.mark.parametrize("hq,hkv,d", [(8, 2, 64), (16, 8, 256), (12, 4, 64)])
+@pytest.mark.parametrize("hq,hkv,d", [(8, 2, 64), (16, 8, 256), (12, 4, 64),
+                                      (32, 1, 128), (48, 2, 64)])  # G=32, G=24
 def test_decode_fp8_other_head_dims(gpu, hq, hkv, d):
     say(f"fp8 decode hq={hq} hkv={hkv} d={d}")
     w = W.decode_batched(device=gpu, batch=12, ctx_lo=20, ctx_hi=1500, hq=hq, hkv=hkv, d=d)

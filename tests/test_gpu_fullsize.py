@@ -114,13 +114,20 @@ def test_prefill_poisoned_shapes(gpu, hq, hkv, d, prefix, new, holes):
     assert_attn_close(f32(run_prefill(w, gpu)), oracle_prefill(w), "poisoned prefill")
 
 
-@pytest.mark.parametrize("d,hq,hkv", [(96, 8, 4), (192, 8, 4), (128, 32, 1)])
-def test_mixed_padded_head_dim_or_wide_group_poisoned(gpu, d, hq, hkv):
+@pytest.mark.parametrize("d,hq,hkv,dec_hi", [(96, 8, 4, 3000), (192, 8, 4, 3000),
+                                            (128, 32, 1, 3000),
+                                            (128, 32, 1, 300), (80, 16, 8, 300)])
+def test_mixed_padded_head_dim_or_wide_group_poisoned(gpu, d, hq, hkv, dec_hi):
     """A mixed batch (chunked prefills + decode items) at a padded head dim, or with 32
-    query heads per KV head."""
-    say(f"mixed batch d={d} hq={hq} hkv={hkv}, unused slots poisoned")
-    w = W.mixed_step(device=gpu, seed=d + hq, n_chunks=3, chunk=200, prefix_hi=512,
-                     n_decode=40, dec_lo=16, dec_hi=3000, hq=hq, hkv=hkv, d=d)
+    query heads per KV head; rows of at most 512 positions send the decode items to the
+    one-launch group kernel, longer ones to the split kernel + merge."""
+    say(f"mixed batch d={d} hq={hq} hkv={hkv} dec_hi={dec_hi}, unused slots poisoned")
+    short = dec_hi <= 512
+    w = W.mixed_step(device=gpu, seed=d + hq, n_chunks=3, chunk=100 if short else 200,
+                     prefix_hi=128 if short else 512, n_decode=40, dec_lo=16, dec_hi=dec_hi,
+                     hq=hq, hkv=hkv, d=d)
+    if short:
+        assert w.mbpr * 16 <= 512
     write_new(w, gpu)
     poison_unused(w, gpu)
     assert_attn_close(f32(run_prefill(w, gpu)), oracle_prefill(w), f"mixed d{d}")
