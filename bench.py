@@ -7,6 +7,9 @@ HBM. The headline (the JSON `value`) is BASELINE.json's decode metric on configs
 paged decode, batch 64, Qwen3-0.6B heads (16 q / 8 kv, d=128), contexts U[128, 4096], one
 step = KV-cache write of the 64 new tokens + decode attention; value = algorithmic KV bytes
 read per step (K+V of every context position, once per (sequence, kv_head)) / step time.
+The step runs as one launch pair (ccinfer_decode_attention_write_kv: the KV write inside the
+decode kernel, then the merge); the reference's two launcher calls (write_kv_cache, then
+decode_attention) are timed beside it (configs."2...".unfused_*).
 The other configurations are reported under "configs"; "6" is the fused decode prologue
 (split QKV + q/k RMSNorm + RoPE + KV write in one launch), in algorithmic bytes per second;
 "7" is the per-step batch metadata built on the device, beside the reference's host path;
@@ -78,6 +81,16 @@ class Ops:
             self.meta["block_table"].data_ptr(), self.meta["context_lens"].data_ptr(),
             self.out.data_ptr(), w.batch, w.mbpr, w.hq, w.hkv, w.d, 16, self.ws.data_ptr(),
             self.ws_bytes, self.s)
+        assert rc == 0, rc
+
+    def decode_write(self):
+        """The decode step with the new tokens' KV write in the decode launch."""
+        w = self.w
+        rc = self.lib.ccinfer_decode_attention_write_kv(
+            w.q.data_ptr(), w.k_new.data_ptr(), w.v_new.data_ptr(), w.k_cache.data_ptr(),
+            w.v_cache.data_ptr(), self.meta["block_table"].data_ptr(),
+            self.meta["context_lens"].data_ptr(), self.out.data_ptr(), w.batch, w.mbpr, w.hq,
+            w.hkv, w.d, 16, w.k_cache.shape[0], self.ws.data_ptr(), self.ws_bytes, self.s)
         assert rc == 0, rc
 
     def prefill(self):
@@ -269,15 +282,21 @@ def prefill_pair_flops(w: W.PagedWorkload, pairs) -> int:
 
 
 def bench_decode(w, dev, steps, warmup, with_write, stream):
+    """with_write: the step is the KV write of the new tokens + decode, timed both as one
+    launch (ccinfer_decode_attention_write_kv: the step) and as the reference's two launcher
+    calls (write_kv_cache, then decode_attention: "unfused_*")."""
     ops = Ops(w, dev, stream)
-    step = (lambda: (ops.write(), ops.decode())) if with_write else ops.decode
+    step = ops.decode_write if with_write else ops.decode
     ms, host_ms = time_loop(step, steps, warmup, stream)
     dec_ms, _ = time_loop(ops.decode, steps, warmup, stream)
     res = {"ms_per_step": ms, "host_ms_per_step": host_ms, "decode_ms": dec_ms,
            "kv_bytes": w.kv_bytes()}
     if with_write:
         wr_ms, _ = time_loop(ops.write, steps, warmup, stream)
+        un_ms, _ = time_loop(lambda: (ops.write(), ops.decode()), steps, warmup, stream)
         res["write_ms"] = wr_ms
+        res["unfused_ms_per_step"] = un_ms
+        res["unfused_kv_GBps"] = w.kv_bytes() / (un_ms * 1e-3) / 1e9
     res["kv_GBps"] = w.kv_bytes() / (ms * 1e-3) / 1e9
     res["decode_kernel_GBps"] = w.kv_bytes() / (dec_ms * 1e-3) / 1e9
     res["hbm_frac"] = res["decode_kernel_GBps"] * 1e9 / HBM_PEAK
@@ -651,7 +670,8 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) bf16 Q/K/V, random block tables)",
         "config": {"workload": "configs[1]: batched paged decode, batch 64, 16q/8kv heads, "
-                               "d=128, ctx U[128,4096], block 16, + KV write of 64 new tokens",
+                               "d=128, ctx U[128,4096], block 16, + KV write of 64 new tokens "
+                               "(in the decode launch: ccinfer_decode_attention_write_kv)",
                    "batch": w.batch, "num_q_heads": w.hq, "num_kv_heads": w.hkv,
                    "head_dim": w.d, "block_size": 16, "sum_ctx": int(w.context_lens.sum()),
                    "parallelism": "single GPU"},

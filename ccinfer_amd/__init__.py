@@ -12,6 +12,7 @@ from .ops import (  # noqa: F401
     build_batch_metadata,
     decode_attention,
     decode_attention_fp8,
+    decode_attention_write_kv,
     decode_workspace_size,
     prefill_attention,
     prefill_attention_fp8,
@@ -30,6 +31,7 @@ __all__ = [
     "build_batch_metadata",
     "decode_attention",
     "decode_attention_fp8",
+    "decode_attention_write_kv",
     "decode_workspace_size",
     "prefill_attention",
     "prefill_attention_fp8",

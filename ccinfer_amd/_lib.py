@@ -26,6 +26,8 @@ SIGNATURES = {
         _c_int,
         [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _c_size, _vp],
     ),
+    "ccinfer_decode_attention_write_kv": (
+        _c_int, [_vp] * 8 + [_c_int] * 7 + [_vp, _c_size, _vp]),
     "ccinfer_decode_attention_noalloc": (
         _c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _vp]),
     "ccinfer_write_kv_cache_fp8": (_c_int, [_vp] * 7 + [_c_int] * 4 + [_vp]),

@@ -246,36 +246,86 @@ size_t ccinfer_decode_workspace_size(int batch_size, int max_blocks_per_req, int
     return decode_workspace_bytes(batch_size, num_q_heads, head_dim, plan);
 }
 
+namespace {
+
+// Decode, optionally writing each request's new token first (new_k != nullptr).
+int decode_entry(const void* q, const void* k_cache, const void* v_cache,
+                 const int32_t* block_table, const int32_t* context_lens, void* output,
+                 int batch_size, int max_blocks_per_req, int num_q_heads, int num_kv_heads,
+                 int head_dim, int cache_block_size, void* workspace, size_t workspace_bytes,
+                 void* stream, const void* new_k, const void* new_v, int max_slots) {
+    if (!q || !k_cache || !v_cache || !block_table || !context_lens || !output)
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    if (!decode_shape_ok(batch_size, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
+                         cache_block_size))
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    const bool fast = decode_fast_supported(num_q_heads, num_kv_heads, head_dim,
+                                            cache_block_size) &&
+                      fast_aligned(q, k_cache, v_cache, output);
+    DecodePlan plan;
+    if (fast) {
+        plan = plan_decode(batch_size, num_q_heads, num_kv_heads,
+                           max_blocks_per_req * cache_block_size, true);
+        const size_t need = decode_workspace_bytes(batch_size, num_q_heads, head_dim, plan);
+        if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+            return CCINFER_ERR_INVALID_ARGUMENT;
+    }
+    // The new tokens go in with the decode launch when its kernels can write them (4-byte
+    // aligned rows), else by a separate launch before it.
+    const bool fused = new_k != nullptr && fast &&
+                       ((reinterpret_cast<uintptr_t>(new_k) | reinterpret_cast<uintptr_t>(new_v)) &
+                        3u) == 0;
+    if (new_k != nullptr && !fused) {
+        const hipError_t err = write_last_tokens(
+            new_k, new_v, const_cast<void*>(k_cache), const_cast<void*>(v_cache), block_table,
+            context_lens, batch_size, max_blocks_per_req, num_kv_heads, head_dim, max_slots,
+            as_stream(stream));
+        if (err != hipSuccess) return map_hip_error(err);
+    }
+    if (!fast) {
+        return map_hip_error(generic_decode_attention(
+            q, k_cache, v_cache, block_table, context_lens, output, batch_size,
+            max_blocks_per_req, num_q_heads, num_kv_heads, head_dim, cache_block_size,
+            as_stream(stream)));
+    }
+    DecodeItems items;
+    items.num_items = batch_size;
+    if (fused) {
+        items.new_k = new_k;
+        items.new_v = new_v;
+        items.max_slots = max_slots;
+    }
+    return map_hip_error(decode_attention(q, k_cache, v_cache, block_table, context_lens, output,
+                                          items, max_blocks_per_req, num_q_heads, num_kv_heads,
+                                          head_dim, cache_block_size, plan, workspace,
+                                          as_stream(stream)));
+}
+
+}  // namespace
+
 int ccinfer_decode_attention(const void* q, const void* k_cache, const void* v_cache,
                              const int32_t* block_table, const int32_t* context_lens,
                              void* output, int batch_size, int max_blocks_per_req,
                              int num_q_heads, int num_kv_heads, int head_dim,
                              int cache_block_size, void* workspace, size_t workspace_bytes,
                              void* stream) {
-    if (!q || !k_cache || !v_cache || !block_table || !context_lens || !output)
-        return CCINFER_ERR_INVALID_ARGUMENT;
-    if (!decode_shape_ok(batch_size, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
-                         cache_block_size))
-        return CCINFER_ERR_INVALID_ARGUMENT;
-    if (!decode_fast_supported(num_q_heads, num_kv_heads, head_dim, cache_block_size) ||
-        !fast_aligned(q, k_cache, v_cache, output)) {
-        return map_hip_error(generic_decode_attention(
-            q, k_cache, v_cache, block_table, context_lens, output, batch_size,
-            max_blocks_per_req, num_q_heads, num_kv_heads, head_dim, cache_block_size,
-            as_stream(stream)));
-    }
-    const DecodePlan plan =
-        plan_decode(batch_size, num_q_heads, num_kv_heads,
-                    max_blocks_per_req * cache_block_size, true);
-    const size_t need = decode_workspace_bytes(batch_size, num_q_heads, head_dim, plan);
-    if (need > 0 && (workspace == nullptr || workspace_bytes < need))
-        return CCINFER_ERR_INVALID_ARGUMENT;
-    DecodeItems items;
-    items.num_items = batch_size;
-    return map_hip_error(decode_attention(q, k_cache, v_cache, block_table, context_lens, output,
-                                          items, max_blocks_per_req, num_q_heads, num_kv_heads,
-                                          head_dim, cache_block_size, plan, workspace,
-                                          as_stream(stream)));
+    return decode_entry(q, k_cache, v_cache, block_table, context_lens, output, batch_size,
+                        max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
+                        cache_block_size, workspace, workspace_bytes, stream, nullptr, nullptr,
+                        0);
+}
+
+int ccinfer_decode_attention_write_kv(const void* q, const void* k_new, const void* v_new,
+                                      void* k_cache, void* v_cache, const int32_t* block_table,
+                                      const int32_t* context_lens, void* output, int batch_size,
+                                      int max_blocks_per_req, int num_q_heads, int num_kv_heads,
+                                      int head_dim, int cache_block_size, int max_slots,
+                                      void* workspace, size_t workspace_bytes, void* stream) {
+    if (!k_new || !v_new || max_slots <= 0) return CCINFER_ERR_INVALID_ARGUMENT;
+    return decode_entry(q, k_cache, v_cache, block_table, context_lens, output, batch_size,
+                        max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
+                        cache_block_size, workspace, workspace_bytes, stream, k_new, v_new,
+                        max_slots);
 }
 
 int ccinfer_write_kv_cache_fp8(const void* k_new, const void* v_new, void* k_cache,

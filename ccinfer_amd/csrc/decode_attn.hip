@@ -59,8 +59,6 @@ constexpr int kMaxSplitTokens = 2048;  // 128 blocks: two table entries per lane
 // Wavefronts the split plan aims for: two resident per SIMD on 1024 SIMDs, two rounds.
 constexpr int64_t kTargetWaves = 4096;
 constexpr int kBalancedMinItems = 4;
-// Longest table row (positions) of the single-launch group plan: parts of at most 512
-// positions at 8 wavefronts (1024 at 4), within one split's 2048.
 // The group plan (one workgroup per (request, kv_head), parts merged in LDS) streams a row
 // from one CU, which reads ~30 GB/s; it pays off only where the row is short enough that
 // one launch beats the split plan's two. Measured (one MI355X, 16q/8kv or 32q/8kv, d=128):
@@ -76,6 +74,11 @@ struct ItemArgs {
     const int32_t* qsl;
     float eps;
     int zero_invalid;
+    // Optional new token per request (bf16 [B][Hkv][dr]), written to the cache slot of the
+    // request's last position before it is read (nullptr: none).
+    const __bf16* new_k;
+    const __bf16* new_v;
+    int max_slots;
 };
 
 // Per (item, q_head) row: how many splits its partials span and where they start. Written
@@ -105,6 +108,38 @@ __device__ __forceinline__ bool resolve_item(const ItemArgs& it, int item, int* 
 
 // Number of context positions to visit for a request, or -1 when the output must be zero
 // (decode mode) / left untouched (prefill mode).
+// The wavefront whose split holds position ctx - 1 of request req writes that position's K
+// and V rows for its cache head from the new token of the request (block id checked against
+// the cache's slot count), and waits for the stores before any load of the split. No other
+// wavefront reads that slot (one split holds each position; other requests do not see a
+// request's newest position).
+template <bool kPad>
+__device__ __forceinline__ void write_new_token(const __bf16* k_cache, const __bf16* v_cache,
+                                                const ItemArgs& items,
+                                                const int32_t* __restrict__ req_blocks, int req,
+                                                int ctx, int hkv_c, int kvh, int ds, int lane) {
+    const int pos = ctx - 1;
+    const int pb = req_blocks[pos / kBlock];
+    const int64_t slot = static_cast<int64_t>(pb) * kBlock + pos % kBlock;
+    if (pb >= 0 && slot < items.max_slots) {
+        // Stores through the same (const-qualified) cache pointers the split's loads use, so
+        // the compiler keeps the loads after them.
+        uint32_t* kd = reinterpret_cast<uint32_t*>(
+            const_cast<__bf16*>(k_cache) + (slot * hkv_c + kvh) * ds);
+        uint32_t* vd = reinterpret_cast<uint32_t*>(
+            const_cast<__bf16*>(v_cache) + (slot * hkv_c + kvh) * ds);
+        const int64_t src = (static_cast<int64_t>(req) * hkv_c + kvh) * ds;
+        const uint32_t* ks = reinterpret_cast<const uint32_t*>(items.new_k + src);
+        const uint32_t* vs = reinterpret_cast<const uint32_t*>(items.new_v + src);
+        for (int x = lane; x < ds / 2; x += 64) {
+            kd[x] = ks[x];
+            vd[x] = vs[x];
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the rows are in L2 before any load
+    asm volatile("" ::: "memory");
+}
+
 __device__ __forceinline__ int effective_ctx(int ctx, int mbpr, int zero_invalid) {
     if (ctx <= 0) return -1;
     const int cap = mbpr * kBlock;
@@ -684,6 +719,11 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     const int begin = s * split_tokens;
     if (begin >= ctx) return;
     const int end = min(ctx, begin + split_tokens);
+    if constexpr (!F8) {
+        if (items.new_k != nullptr && end == ctx)
+            write_new_token<kPad>(k_cache, v_cache, items, block_table + static_cast<int64_t>(req) * mbpr,
+                                  req, ctx, hkv / rep, h / rep, ds, lane);
+    }
     SplitInputs<D> in;
     load_split_inputs<D, F8, kPad>(q, block_table + static_cast<int64_t>(req) * mbpr, mbpr, qrow,
                                    hq, h, G, begin, end, lane, in, dr);
@@ -793,6 +833,11 @@ __global__ __launch_bounds__(64 * GroupShape<D>::kWaves) void decode_group_kerne
         return;
     }
     const int end = min(ctx, tbl_end);
+    if constexpr (!F8) {
+        if (items.new_k != nullptr && begin < end && end == ctx)
+            write_new_token<kPad>(k_cache, v_cache, items, block_table + static_cast<int64_t>(req) * mbpr,
+                                  req, ctx, hkv / rep, h / rep, ds, lane);
+    }
     SoftmaxState<D> st;
     if (begin < end) {
         run_split<D, F8, kPad>(k_cache, v_cache, k_scale, v_scale, in, hkv / rep, h / rep, begin,
@@ -1038,7 +1083,9 @@ hipError_t decode_attention(const void* q, const void* k_cache, const void* v_ca
                             const DecodePlan& plan, void* workspace, hipStream_t stream) {
     (void)block_size;
     ItemArgs it{items.num_items, items.item_count, items.item_req, items.query_start_loc,
-                items.denom_eps, items.zero_invalid ? 1 : 0};
+                items.denom_eps, items.zero_invalid ? 1 : 0,
+                static_cast<const __bf16*>(items.new_k), static_cast<const __bf16*>(items.new_v),
+                items.max_slots};
     const int D = decode_mfma_dim(head_dim);
     const bool pad = D != head_dim;
 #define CCI_DECODE(DD, PP)                                                                   \
@@ -1069,7 +1116,9 @@ hipError_t decode_attention_fp8(const void* q, const void* k_cache, const void* 
                                 int num_q_heads, int num_kv_heads, int head_dim,
                                 const DecodePlan& plan, void* workspace, hipStream_t stream) {
     ItemArgs it{items.num_items, items.item_count, items.item_req, items.query_start_loc,
-                items.denom_eps, items.zero_invalid ? 1 : 0};
+                items.denom_eps, items.zero_invalid ? 1 : 0,
+                static_cast<const __bf16*>(items.new_k), static_cast<const __bf16*>(items.new_v),
+                items.max_slots};
     switch (head_dim) {
         case 64:
             return launch_decode<64, true, false>(q, k_cache, v_cache, k_scale, v_scale, block_table,

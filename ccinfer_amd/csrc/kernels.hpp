@@ -65,7 +65,20 @@ struct DecodeItems {
     const int32_t* query_start_loc = nullptr;  // device: q row = qsl[req] (nullptr -> req)
     float denom_eps = 1e-6f;              // decode adds 1e-6 to the softmax sum; prefill 0
     bool zero_invalid = true;             // decode writes zeros for bad ctx; prefill skips
+    // Optional: request r's new token (bf16 [B][Hkv][head_dim]) is written to the cache slot
+    // of its last position (if that block id is >= 0 and the slot < max_slots) before it is
+    // read; bf16 caches only.
+    const void* new_k = nullptr;
+    const void* new_v = nullptr;
+    int max_slots = 0;
 };
+
+// Request b's new token (bf16 [B][Hkv][head_dim]) into the cache slot of its last position
+// (the separate-launch form of DecodeItems::new_k / new_v).
+hipError_t write_last_tokens(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                             const int32_t* block_table, const int32_t* context_lens,
+                             int batch_size, int max_blocks_per_req, int n_kv_heads, int head_dim,
+                             int max_slots, hipStream_t stream);
 
 hipError_t decode_attention(const void* q, const void* k_cache, const void* v_cache,
                             const int32_t* block_table, const int32_t* context_lens, void* output,

@@ -50,6 +50,30 @@ __global__ __launch_bounds__(kThreads) void write_kv_rows2(
     }
 }
 
+// Request b's new token into the slot of its last position ctx_b - 1 (through its table
+// row); rows with ctx outside [1, mbpr * 16], a negative block id or a slot past max_slots
+// are skipped.
+__global__ __launch_bounds__(kThreads) void write_last_tokens_kernel(
+    const uint16_t* __restrict__ k_new, const uint16_t* __restrict__ v_new,
+    uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
+    const int32_t* __restrict__ block_table, const int32_t* __restrict__ context_lens, int mbpr,
+    int row_elems, int max_slots) {
+    const int b = blockIdx.x;
+    const int ctx = context_lens[b];
+    if (ctx < 1 || ctx > mbpr * 16) return;
+    const int pos = ctx - 1;
+    const int pb = block_table[static_cast<int64_t>(b) * mbpr + pos / 16];
+    if (pb < 0) return;
+    const int64_t slot = static_cast<int64_t>(pb) * 16 + pos % 16;
+    if (slot >= max_slots) return;
+    const int64_t src = static_cast<int64_t>(b) * row_elems;
+    const int64_t dst = slot * row_elems;
+    for (int e = threadIdx.x; e < row_elems; e += kThreads) {
+        k_cache[dst + e] = k_new[src + e];
+        v_cache[dst + e] = v_new[src + e];
+    }
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
@@ -71,6 +95,17 @@ hipError_t write_kv_cache(const void* k_new, const void* v_new, void* k_cache, v
             static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), slot_mapping,
             row_elems, max_slots);
     }
+    return hipGetLastError();
+}
+
+hipError_t write_last_tokens(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                             const int32_t* block_table, const int32_t* context_lens,
+                             int batch_size, int max_blocks_per_req, int n_kv_heads, int head_dim,
+                             int max_slots, hipStream_t stream) {
+    write_last_tokens_kernel<<<batch_size, kThreads, 0, stream>>>(
+        static_cast<const uint16_t*>(k_new), static_cast<const uint16_t*>(v_new),
+        static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), block_table,
+        context_lens, max_blocks_per_req, n_kv_heads * head_dim, max_slots);
     return hipGetLastError();
 }
 

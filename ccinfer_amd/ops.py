@@ -245,6 +245,40 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     return output
 
 
+def decode_attention_write_kv(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+                              k_cache: torch.Tensor, v_cache: torch.Tensor,
+                              block_table: torch.Tensor, context_lens: torch.Tensor,
+                              output: Optional[torch.Tensor] = None, cache_block_size: int = 16,
+                              workspace: Optional[torch.Tensor] = None,
+                              max_slots: Optional[int] = None) -> torch.Tensor:
+    """One decode step: write_kv_cache of each request's new token k_new[b] / v_new[b]
+    ([B, Hkv, D]) into the slot of its last position (context_lens[b] - 1, through its table
+    row), then decode_attention (write_kv_cache.cu:12-34 + decode_attn.cu:364-473
+    semantics, in one launch on the MFMA path). Returns output."""
+    op = "decode_attention_write_kv"
+    for t in (q, k_new, v_new, k_cache, v_cache):
+        _dev_tensor(t, torch.bfloat16, op)
+    _dev_tensor(block_table, torch.int32, op)
+    _dev_tensor(context_lens, torch.int32, op)
+    _require(q.dim() == 3 and block_table.dim() == 2, op)
+    b, hq, d = q.shape
+    slots, hkv, dk = _kv_shape(k_cache)
+    _require(dk == d and block_table.shape[0] == b and context_lens.numel() == b, op)
+    _require(k_new.shape == (b, hkv, d) and v_new.shape == k_new.shape, op)
+    if output is None:
+        output = torch.empty_like(q)
+    _dev_tensor(output, torch.bfloat16, op)
+    _require(output.shape == q.shape, op)
+    mbpr = block_table.shape[1]
+    need = decode_workspace_size(b, mbpr, hq, hkv, d, cache_block_size)
+    ws, ws_bytes = _workspace(need, q.device, workspace)
+    _check(_lib.load().ccinfer_decode_attention_write_kv(
+        _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(k_cache), _ptr(v_cache), _ptr(block_table),
+        _ptr(context_lens), _ptr(output), b, mbpr, hq, hkv, d, cache_block_size,
+        slots if max_slots is None else max_slots, _ptr(ws), ws_bytes, _stream()), op)
+    return output
+
+
 def fp8_scale_numel(max_slots: int, num_kv_heads: int, block_size: int = 16) -> int:
     """Floats in each scale array of an fp8 cache of `max_slots` slots."""
     return -(-max_slots // block_size) * block_size * num_kv_heads

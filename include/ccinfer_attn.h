@@ -127,6 +127,26 @@ int ccinfer_decode_attention(const void* q, const void* k_cache, const void* v_c
                              int cache_block_size, void* workspace, size_t workspace_bytes,
                              void* stream);
 
+/* One decode step: ccinfer_write_kv_cache of each request's new token into the slot of its
+ * last position, then ccinfer_decode_attention. No single counterpart in the reference: it
+ * replaces the pair launch_write_kv_cache + launch_decode_attention
+ * (src/kernel/cuda_kernels.h:61-77) as src/model/qwen3/qwen3_model.cpp:230-262 issues them
+ * for a decode batch, where token b is request b's newest position. k_new, v_new:
+ * [batch_size][num_kv_heads][head_dim] bf16. The slot of request b's token is derived from
+ * its table row: block_table[b][(ctx_b - 1) / 16] * 16 + (ctx_b - 1) % 16; rows with ctx_b
+ * outside [1, max_blocks_per_req * 16], a negative block id there or a slot >= max_slots
+ * write nothing (their output follows ccinfer_decode_attention). Requirement (true of any
+ * decode batch): no other request of the batch reads those slots. On the MFMA path the
+ * writes happen inside the decode launch (the wavefront that reads the slot writes it
+ * first); otherwise a separate launch writes them first. Workspace as
+ * ccinfer_decode_workspace_size. */
+int ccinfer_decode_attention_write_kv(const void* q, const void* k_new, const void* v_new,
+                                      void* k_cache, void* v_cache, const int32_t* block_table,
+                                      const int32_t* context_lens, void* output, int batch_size,
+                                      int max_blocks_per_req, int num_q_heads, int num_kv_heads,
+                                      int head_dim, int cache_block_size, int max_slots,
+                                      void* workspace, size_t workspace_bytes, void* stream);
+
 /* ccinfer_decode_attention without a workspace and without any allocation. No counterpart
  * in the reference: for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc). The split-KV scratch is

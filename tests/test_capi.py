@@ -78,6 +78,24 @@ def test_decode_validation(lib):
     assert _decode(lib, b=64, mbpr=256, hq=16, hkv=8, ws=FAKE, wsb=need - 1) == INVALID
 
 
+def test_decode_write_kv_validation(lib):
+    f = lib.ccinfer_decode_attention_write_kv
+    ok = [FAKE] * 8 + [2, 4, 16, 8, 128, 16, 1024, None, 0, None]
+    for i in range(8):                     # q, k_new, v_new, caches, table, ctx, output
+        a = list(ok)
+        a[i] = None
+        assert f(*a) == INVALID, i
+    a = list(ok)
+    a[14] = 0                              # max_slots
+    assert f(*a) == INVALID
+    a = list(ok)
+    a[12] = 100                            # not a decode head dim
+    assert f(*a) == INVALID
+    a = list(ok)
+    a[8], a[9] = 64, 256                   # needs a workspace: a missing one is rejected
+    assert f(*a) == INVALID
+
+
 def test_decode_workspace_size(lib):
     f = lib.ccinfer_decode_workspace_size
     assert f(0, 4, 8, 2, 128, 16) == 0            # invalid shape -> 0

@@ -234,3 +234,82 @@ def test_two_byte_aligned_views(gpu, which):
                            meta["context_lens"], output=out)
     torch.cuda.synchronize()
     assert_attn_close(f32(got), oracle_decode(w), f"misaligned {which}")
+
+
+def _write_then_decode(w, dev, slot_mapping, k_cache, v_cache):
+    meta = w.device_meta(dev)
+    write_kv_cache(w.k_new, w.v_new, k_cache, v_cache,
+                   torch.from_numpy(slot_mapping.astype(np.int32)).to(dev))
+    return decode_attention(w.q, k_cache, v_cache, meta["block_table"], meta["context_lens"])
+
+
+@pytest.mark.parametrize("batch,ctx_lo,ctx_hi,hq,hkv,d", [
+    (64, 128, 4096, 16, 8, 128),   # configs[1]: balanced split plan + merge
+    (1, 512, 512, 16, 8, 128),     # group plan (one launch)
+    (2, 100, 3000, 16, 8, 128),    # fixed split plan
+    (9, 1, 700, 16, 8, 96),        # padded head dim
+    (6, 20, 900, 32, 1, 128),      # two virtual kv heads write the same row
+    (300, 1, 400, 16, 8, 64),      # more than 256 requests
+])
+def test_fused_kv_write_equals_write_then_decode(gpu, batch, ctx_lo, ctx_hi, hq, hkv, d):
+    """decode_attention_write_kv == write_kv_cache (slot of each request's last position)
+    followed by decode_attention: output and both caches bit-equal."""
+    from ccinfer_amd import decode_attention_write_kv
+    say(f"fused write+decode B={batch} ctx=[{ctx_lo},{ctx_hi}] hq={hq} hkv={hkv} d={d}")
+    w = W.decode_batched(device=gpu, seed=batch + d, batch=batch, ctx_lo=ctx_lo, ctx_hi=ctx_hi,
+                         hq=hq, hkv=hkv, d=d, with_write=True)
+    kc, vc = w.k_cache.clone(), w.v_cache.clone()
+    want = _write_then_decode(w, gpu, w.slot_mapping, kc, vc)
+    meta = w.device_meta(gpu)
+    got = decode_attention_write_kv(w.q, w.k_new, w.v_new, w.k_cache, w.v_cache,
+                                    meta["block_table"], meta["context_lens"])
+    torch.cuda.synchronize()
+    assert torch.equal(w.k_cache, kc) and torch.equal(w.v_cache, vc)
+    assert torch.equal(got, want)
+    assert_attn_close(f32(got), oracle_decode(w), "fused write+decode vs oracle")
+
+
+def test_fused_kv_write_skips_rows_without_a_slot(gpu):
+    """Rows with ctx 0, ctx past the table row, a hole at the last position or a slot past
+    max_slots write nothing; the rest write. Also the separate-launch path (k_new only
+    2-byte aligned) and the generic decode path (q only 2-byte aligned)."""
+    from ccinfer_amd import decode_attention_write_kv
+    say("fused write+decode edge rows")
+    w = W.decode_batched(device=gpu, seed=31, batch=8, ctx_lo=40, ctx_hi=300, with_write=True)
+    ctx = w.context_lens.copy()
+    bt = w.block_table.copy()
+    ctx[0] = 0
+    ctx[1] = bt.shape[1] * 16 + 1
+    bt[2, (ctx[2] - 1) // 16] = -1
+    w.context_lens, w.block_table = ctx.astype(np.int32), bt
+    max_slots = int(w.k_cache.shape[0])
+    pos = np.maximum(ctx - 1, 0)
+    slots = (bt[np.arange(8), np.minimum(pos // 16, bt.shape[1] - 1)] * 16 + pos % 16)
+    slots = slots.astype(np.int64)
+    slots[[0, 1, 2]] = -1
+    limit = int(slots[3])          # row 3's slot (and any above it) is past max_slots
+    slots[slots >= limit] = -1
+    assert limit < max_slots and (slots >= 0).sum() >= 2
+    for variant in ("fused", "split_write", "generic"):
+        w2 = W.decode_batched(device=gpu, seed=31, batch=8, ctx_lo=40, ctx_hi=300,
+                              with_write=True)
+        w2.context_lens, w2.block_table = w.context_lens, w.block_table
+        kc, vc = w2.k_cache.clone(), w2.v_cache.clone()
+        want = _write_then_decode(w2, gpu, slots, kc, vc)
+        meta = w2.device_meta(gpu)
+        q, k_new, v_new = w2.q, w2.k_new, w2.v_new
+        if variant == "split_write":
+            k_new = _offset_view(k_new)
+            v_new = _offset_view(v_new)
+        if variant == "generic":
+            q = _offset_view(q)
+        got = decode_attention_write_kv(q, k_new, v_new, w2.k_cache, w2.v_cache,
+                                        meta["block_table"], meta["context_lens"],
+                                        max_slots=limit)
+        torch.cuda.synchronize()
+        assert torch.equal(w2.k_cache, kc) and torch.equal(w2.v_cache, vc), variant
+        if variant == "generic":
+            assert_attn_close(f32(got), f32(want), variant)
+        else:
+            assert torch.equal(got, want), variant
+
