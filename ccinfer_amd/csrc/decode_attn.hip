@@ -249,6 +249,17 @@ __device__ __forceinline__ T nt_load(const T* p) {
     return __builtin_nontemporal_load(p);
 }
 
+// K/V chunk loads: nontemporal (each byte is read once per launch) unless kTL, where the same
+// lines are read again soon (padded rows re-read a piece of their own row; virtual kv heads
+// read their cache head's blocks once per virtual head) and should stay in L2.
+template <bool kTL, typename T>
+__device__ __forceinline__ T kv_load(const T* p) {
+    if constexpr (kTL)
+        return *p;
+    else
+        return __builtin_nontemporal_load(p);
+}
+
 template <int D>
 struct ChunkRegs {
     u32x4 k[2][DecodeShape<D>::kSteps];
@@ -258,7 +269,7 @@ struct ChunkRegs {
 // kPad: the cache rows hold dr < D dims (dr a multiple of D/16); the kernel runs at the
 // MFMA size D with dims [dr, D) zero. Loads of missing dims read a valid piece of the row
 // instead (so every lane still issues the same loads) and are replaced by zeros.
-template <int D, bool kPad = false>
+template <int D, bool kPad = false, bool kTL = false>
 __device__ __forceinline__ void load_chunk(ChunkRegs<D>& c, const __bf16* __restrict__ k_cache,
                                            const __bf16* __restrict__ v_cache, int pb0, int pb1,
                                            int kv_head, int hkv, int lane, int dr = D) {
@@ -276,7 +287,7 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<D>& c, const __bf16* __rest
         for (int kk = 0; kk < S; ++kk) {
             const int dim0 = (kk * 4 + g) * 8;
             const bool ok = !kPad || dim0 < dr;
-            c.k[kb][kk] = nt_load(reinterpret_cast<const u32x4*>(row + (ok ? dim0 : 0)));
+            c.k[kb][kk] = kv_load<kTL>(reinterpret_cast<const u32x4*>(row + (ok ? dim0 : 0)));
             if (!ok) c.k[kb][kk] = u32x4{0, 0, 0, 0};
         }
     }
@@ -289,16 +300,16 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<D>& c, const __bf16* __rest
             v_cache + ((static_cast<int64_t>(pbs[kb]) * kBlock + off) * hkv + kv_head) * rs +
             (vok ? i * NV : 0);
         if constexpr (NV == 8) {
-            const u32x4 w = nt_load(reinterpret_cast<const u32x4*>(row));
+            const u32x4 w = kv_load<kTL>(reinterpret_cast<const u32x4*>(row));
 #pragma unroll
             for (int x = 0; x < 4; ++x) c.v[e][x] = vok ? w[x] : 0u;
         } else if constexpr (NV == 4) {
-            const u32x2 w = nt_load(reinterpret_cast<const u32x2*>(row));
+            const u32x2 w = kv_load<kTL>(reinterpret_cast<const u32x2*>(row));
             c.v[e][0] = vok ? w[0] : 0u;
             c.v[e][1] = vok ? w[1] : 0u;
         } else {
-            const u32x4 w0 = nt_load(reinterpret_cast<const u32x4*>(row));
-            const u32x4 w1 = nt_load(reinterpret_cast<const u32x4*>(row + 8));
+            const u32x4 w0 = kv_load<kTL>(reinterpret_cast<const u32x4*>(row));
+            const u32x4 w1 = kv_load<kTL>(reinterpret_cast<const u32x4*>(row + 8));
 #pragma unroll
             for (int x = 0; x < 4; ++x) {
                 c.v[e][x] = vok ? w0[x] : 0u;
@@ -324,7 +335,7 @@ struct ChunkRegsF8 {
     u32x4 vs[2];
 };
 
-template <int D>
+template <int D, bool kTL = false>
 __device__ __forceinline__ void load_chunk(ChunkRegsF8<D>& c, const uint8_t* __restrict__ k_cache,
                                            const uint8_t* __restrict__ v_cache,
                                            const float* __restrict__ k_scale,
@@ -357,13 +368,13 @@ __device__ __forceinline__ void load_chunk(ChunkRegsF8<D>& c, const uint8_t* __r
             v_cache + ((static_cast<int64_t>(pbs[kb]) * kBlock + off) * hkv + kv_head) * D +
             i * NV;
         if constexpr (NV == 4) {
-            c.v[e][0] = nt_load(reinterpret_cast<const uint32_t*>(row));
+            c.v[e][0] = kv_load<kTL>(reinterpret_cast<const uint32_t*>(row));
         } else if constexpr (NV == 8) {
-            const u32x2 w = nt_load(reinterpret_cast<const u32x2*>(row));
+            const u32x2 w = kv_load<kTL>(reinterpret_cast<const u32x2*>(row));
             c.v[e][0] = w[0];
             c.v[e][1] = w[1];
         } else {
-            const u32x4 w = nt_load(reinterpret_cast<const u32x4*>(row));
+            const u32x4 w = kv_load<kTL>(reinterpret_cast<const u32x4*>(row));
 #pragma unroll
             for (int x = 0; x < 4; ++x) c.v[e][x] = w[x];
         }
@@ -602,7 +613,7 @@ __device__ __forceinline__ void load_split_inputs(const __bf16* __restrict__ q,
 
 // Attention of the G query heads of kv_head h over context positions [begin, end) (at most
 // 2048) with the split's inputs: the online-softmax state of one wavefront.
-template <int D, bool F8, bool kPad = false>
+template <int D, bool F8, bool kPad = false, bool kTL = false>
 __device__ __forceinline__ void run_split(
     const std::conditional_t<F8, uint8_t, __bf16>* __restrict__ k_cache,
     const std::conditional_t<F8, uint8_t, __bf16>* __restrict__ v_cache,
@@ -631,9 +642,9 @@ __device__ __forceinline__ void run_split(
     Regs ra, rb;
     auto load = [&](Regs& r, int p0, int p1) {
         if constexpr (F8)
-            load_chunk<D>(r, k_cache, v_cache, k_scale, v_scale, p0, p1, h, hkv, lane);
+            load_chunk<D, kTL>(r, k_cache, v_cache, k_scale, v_scale, p0, p1, h, hkv, lane);
         else
-            load_chunk<D, kPad>(r, k_cache, v_cache, p0, p1, h, hkv, lane, dr);
+            load_chunk<D, kPad, kTL>(r, k_cache, v_cache, p0, p1, h, hkv, lane, dr);
     };
     int a0, a1, b0, b1;
     chunk_blocks(0, &a0, &a1);
@@ -651,7 +662,8 @@ __device__ __forceinline__ void run_split(
 
 // F8: the cache holds E4M3 bytes with row scales (k_scale / v_scale); else bf16.
 // kPad: head_dim dr < D (see load_chunk); q and output rows hold dr elements.
-template <int D, bool F8, bool kPad>
+// kTL: the K/V loads stay in L2 (see kv_load).
+template <int D, bool F8, bool kPad, bool kTL>
 __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     const __bf16* __restrict__ q, const void* __restrict__ k_cache_v,
     const void* __restrict__ v_cache_v, const float* __restrict__ k_scale,
@@ -728,8 +740,8 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     load_split_inputs<D, F8, kPad>(q, block_table + static_cast<int64_t>(req) * mbpr, mbpr, qrow,
                                    hq, h, G, begin, end, lane, in, dr);
     SoftmaxState<D> st;
-    run_split<D, F8, kPad>(k_cache, v_cache, k_scale, v_scale, in, hkv / rep, h / rep, begin, end,
-                           scale_log2, lane, st, dr);
+    run_split<D, F8, kPad, kTL>(k_cache, v_cache, k_scale, v_scale, in, hkv / rep, h / rep,
+                                begin, end, scale_log2, lane, st, dr);
     const float l_tot = wave_sum_xor16_32(st.l);
     const bool live = j < G;
     const int head = h * G + j;
@@ -790,7 +802,7 @@ struct GroupShape {
     static constexpr int kMaxG = 16;                 // LDS: kWaves * 16 * D floats = 64 KiB
 };
 
-template <int D, bool F8, bool kPad>
+template <int D, bool F8, bool kPad, bool kTL>
 __global__ __launch_bounds__(64 * GroupShape<D>::kWaves) void decode_group_kernel(
     const __bf16* __restrict__ q, const void* __restrict__ k_cache_v,
     const void* __restrict__ v_cache_v, const float* __restrict__ k_scale,
@@ -840,8 +852,8 @@ __global__ __launch_bounds__(64 * GroupShape<D>::kWaves) void decode_group_kerne
     }
     SoftmaxState<D> st;
     if (begin < end) {
-        run_split<D, F8, kPad>(k_cache, v_cache, k_scale, v_scale, in, hkv / rep, h / rep, begin,
-                               end, scale_log2, lane, st, dr);
+        run_split<D, F8, kPad, kTL>(k_cache, v_cache, k_scale, v_scale, in, hkv / rep, h / rep,
+                                    begin, end, scale_log2, lane, st, dr);
     } else {
 #pragma unroll
         for (int n = 0; n < NV; ++n) st.acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -955,12 +967,21 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
     // rep query heads each; virtual head v reads cache head v / rep.
     const int rep = decode_head_rep(hq / hkv);
     hkv *= rep;
+    // Padded rows and virtual heads read lines twice: those loads stay in L2.
+    const bool tl = kPad || rep > 1;
     if (plan.group) {
         const int64_t groups = static_cast<int64_t>(it.num_items) * hkv;
-        decode_group_kernel<D, F8, kPad><<<static_cast<unsigned>(groups),
-                                           64 * GroupShape<D>::kWaves, 0, stream>>>(
-            static_cast<const __bf16*>(q), k_cache, v_cache, k_scale, v_scale, block_table,
-            context_lens, static_cast<__bf16*>(output), it, mbpr, hq, hkv, scale_log2, dr, rep);
+        auto go = [&](auto tl_tag) {
+            decode_group_kernel<D, F8, kPad, decltype(tl_tag)::value>
+                <<<static_cast<unsigned>(groups), 64 * GroupShape<D>::kWaves, 0, stream>>>(
+                    static_cast<const __bf16*>(q), k_cache, v_cache, k_scale, v_scale,
+                    block_table, context_lens, static_cast<__bf16*>(output), it, mbpr, hq, hkv,
+                    scale_log2, dr, rep);
+        };
+        if (kPad || tl)
+            go(std::true_type{});
+        else if constexpr (!kPad)
+            go(std::false_type{});
         return hipGetLastError();
     }
     const int64_t waves = plan.balanced
@@ -971,11 +992,16 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
     DecodeWs w{};
     if (merge) w = carve(workspace, partial_rows(it.num_items, hq, plan), D);
     const int bw = plan.balanced ? plan.wave_target : 0;
-    decode_split_kernel<D, F8, kPad><<<grid, 256, 0, stream>>>(
-        static_cast<const __bf16*>(q), k_cache, v_cache, k_scale, v_scale, block_table,
-        context_lens,
-        static_cast<__bf16*>(output), w.o, w.ml, w.desc, it, mbpr, hq, hkv, plan.splits,
-        plan.split_tokens, bw, plan.slots, scale_log2, dr, rep);
+    auto go = [&](auto tl_tag) {
+        decode_split_kernel<D, F8, kPad, decltype(tl_tag)::value><<<grid, 256, 0, stream>>>(
+            static_cast<const __bf16*>(q), k_cache, v_cache, k_scale, v_scale, block_table,
+            context_lens, static_cast<__bf16*>(output), w.o, w.ml, w.desc, it, mbpr, hq, hkv,
+            plan.splits, plan.split_tokens, bw, plan.slots, scale_log2, dr, rep);
+    };
+    if (tl)
+        go(std::true_type{});
+    else if constexpr (!kPad)
+        go(std::false_type{});
     hipError_t err = hipGetLastError();
     if (err != hipSuccess || !merge) return err;
     const int64_t rows = static_cast<int64_t>(it.num_items) * hq;
