@@ -81,12 +81,13 @@ __device__ __forceinline__ f32x16 mfma32x32x16(const bf16x8& a, const bf16x8& b,
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// Two OCP E4M3 bytes (the low or high half of `w`) -> a bf16 pair; exact (every E4M3
-// value is a bf16 value).
+// Two OCP E4M3 bytes (the low or high half of `w`) -> a bf16 pair, times 2^e where e is
+// the exponent of `pow2` (the conversion uses only the scale's exponent field); exact
+// (every E4M3 value times a power of two in bf16's range is a bf16 value).
 template <bool kHi>
-__device__ __forceinline__ uint32_t e4m3x2_to_bf16x2(uint32_t w) {
+__device__ __forceinline__ uint32_t e4m3x2_to_bf16x2(uint32_t w, float pow2 = 1.0f) {
     return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(
-                                            static_cast<int>(w), 1.0f, kHi));
+                                            static_cast<int>(w), pow2, kHi));
 }
 
 __device__ __forceinline__ u32x4 load16(const void* p) {

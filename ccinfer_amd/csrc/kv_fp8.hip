@@ -8,10 +8,14 @@
 // so the 16 scales of one block's rows for one head are contiguous (a 64-byte line the
 // decode kernel reads with two 16-byte loads per chunk).
 //
-// Quantisation of one row x[0..D): amax = max |x|; inv = 448 / amax; q = e4m3(clamp(x *
-// inv, +-448)) rounded to nearest even; scale = amax / 448 (an all-zero row stores zeros
-// and scale 0). Dequantised value = q * scale. Per-row scales make appends exact: a decode
-// step writes one new row and never has to requantise earlier rows of the block.
+// Quantisation of one row x[0..D): amax = max |x|; scale = the smallest power of two P
+// (at least 2^-126) with amax <= 448 P; q = e4m3(clamp(x / P, +-448)) rounded to nearest
+// even (an all-zero row stores zeros and scale 0). Dequantised value = q * scale. Per-row
+// scales make appends exact: a decode step writes one new row and never has to requantise
+// earlier rows of the block. A power-of-two scale (as in the OCP microscaling formats'
+// E8M0 scales) loses no relative precision -- x / P is exact and E4M3 has the same
+// relative spacing at every exponent -- and lets a consumer apply it inside the hardware's
+// scaled fp8 -> bf16 conversion, which uses only the exponent of its scale operand.
 //
 // Head dims 64/128/256/512 (aligned buffers): D/8 lanes per row, 8 elements per lane.
 // Other even head dims: one wavefront per (token, kv_head, K or V) row, lane l holding
@@ -28,6 +32,17 @@ namespace ccinfer::hipk {
 namespace {
 
 constexpr int kWaves = 4;
+
+// The row scale: the smallest power of two P >= 2^-126 with amax <= 448 P (448 = 0.875 *
+// 2^9), or 0 for an all-zero row.
+__device__ __forceinline__ float fp8_row_scale(float amax) {
+    if (!(amax > 0.f)) return 0.f;
+    int e;
+    const float f = frexpf(amax, &e);  // amax = f * 2^e, f in [0.5, 1)
+    int p = e - 9 + (f > 0.875f ? 1 : 0);
+    p = p < -126 ? -126 : p;
+    return ldexpf(1.0f, p);
+}
 
 __device__ __forceinline__ float wave_max_all(float v) {
 #pragma unroll
@@ -63,7 +78,8 @@ __global__ __launch_bounds__(256) void write_kv_fp8_kernel(
         amax = fmaxf(amax, fmaxf(fabsf(x[s][0]), fabsf(x[s][1])));
     }
     amax = wave_max_all(amax);
-    const float inv = amax > 0.f ? 448.0f / amax : 0.f;
+    const float scale = fp8_row_scale(amax);
+    const float inv = amax > 0.f ? 1.0f / scale : 0.f;  // exact: a power of two
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) {
         const int e = s * 128 + 2 * lane;
@@ -76,7 +92,7 @@ __global__ __launch_bounds__(256) void write_kv_fp8_kernel(
     if (lane == 0) {
         const int64_t si = (static_cast<int64_t>(slot / kFp8Block) * hkv + h) * kFp8Block +
                            slot % kFp8Block;
-        (is_v ? v_scale : k_scale)[si] = amax > 0.f ? amax / 448.0f : 0.f;
+        (is_v ? v_scale : k_scale)[si] = scale;
     }
 }
 
@@ -114,7 +130,8 @@ __global__ __launch_bounds__(256) void write_kv_fp8_vec_kernel(
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(x[i]));
 #pragma unroll
     for (int off = LPR / 2; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-    const float inv = amax > 0.f ? 448.0f / amax : 0.f;
+    const float scale = fp8_row_scale(amax);
+    const float inv = amax > 0.f ? 1.0f / scale : 0.f;  // exact: a power of two
     uint32_t q[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -130,7 +147,7 @@ __global__ __launch_bounds__(256) void write_kv_fp8_vec_kernel(
     if (sub == 0) {
         const int64_t si = (static_cast<int64_t>(slot / kFp8Block) * hkv + h) * kFp8Block +
                            slot % kFp8Block;
-        (is_v ? v_scale : k_scale)[si] = amax > 0.f ? amax / 448.0f : 0.f;
+        (is_v ? v_scale : k_scale)[si] = scale;
     }
 }
 

@@ -906,7 +906,10 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
         }
     };
     // Bytes of one staged tile -> bf16 tile (byte * row scale, rounded to bf16), written in
-    // the swizzled layout the operand reads expect.
+    // the swizzled layout the operand reads expect. A row whose scale is a normal power of
+    // two (what the fp8 write stores) converts in one instruction per byte pair: the
+    // hardware's scaled conversion applies exactly the exponent of its scale operand, and
+    // byte * 2^e is exact in bf16. Any other scale takes the general path.
     auto convert8 = [&](const uint8_t* lk8, const uint8_t* lv8, __bf16* lk, __bf16* lv,
                         float sk, float sv) __attribute__((always_inline)) {
         const int p = threadIdx.x;
@@ -916,6 +919,17 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
         auto deq = [&](const uint8_t* src, __bf16* dst, float sc) __attribute__((always_inline)) {
             const u32x4 w = *reinterpret_cast<const u32x4*>(src + p * 16);
             u32x4 o[2];
+            const uint32_t sb = __float_as_uint(sc);
+            if ((sb & 0x007fffffu) == 0u && (sb & 0x7f800000u) != 0u) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    o[i >> 1][(i & 1) * 2] = e4m3x2_to_bf16x2<false>(w[i], sc);
+                    o[i >> 1][(i & 1) * 2 + 1] = e4m3x2_to_bf16x2<true>(w[i], sc);
+                }
+                *reinterpret_cast<u32x4*>(dst + lds_off<D>(row, 2 * c)) = o[0];
+                *reinterpret_cast<u32x4*>(dst + lds_off<D>(row, 2 * c + 1)) = o[1];
+                return;
+            }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint32_t lo = e4m3x2_to_bf16x2<false>(w[i]);

@@ -166,8 +166,10 @@ int ccinfer_decode_attention_noalloc(const void* q, const void* k_cache, const v
  * [head_dim] layout and block-table contract, one OCP E4M3 byte per element, plus one fp32
  * scale per cache row in k_scale / v_scale, indexed ((slot / 16) * n_kv_heads + kv_head) * 16
  * + slot % 16 (arrays of ceil(max_slots / 16) * 16 * n_kv_heads floats). A row x is stored
- * as e4m3(clamp(x * (448 / amax), +-448)) with scale amax / 448 (round to nearest even;
- * an all-zero row stores zeros and scale 0); its value is byte * scale. Halves decode bytes.
+ * as e4m3(clamp(x / P, +-448)) with scale P, the smallest power of two >= 2^-126 with
+ * max|x| <= 448 P (round to nearest even; an all-zero row stores zeros and scale 0); its
+ * value is byte * scale. The attention entries accept any fp32 scale; a power of two takes
+ * the faster conversion in the fp8 prefill. Halves decode bytes.
  *
  * Replaces launch_write_kv_cache (src/kernel/cuda_kernels.h:80-83) for an fp8 cache:
  * quantises each new token's K and V rows into its slot; tokens whose slot is outside

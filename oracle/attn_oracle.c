@@ -548,8 +548,9 @@ int orc_build_batch_metadata(const int32_t* item_kv_written, const int32_t* item
 /* src/base/traits.h:117-124 anticipates other KV profiles). OCP E4M3 ("fn": */
 /* no infinities, 0x7f/0xff NaN, largest finite 448), round to nearest even.  */
 /* Each cache row (slot, kv_head) is quantised with its own fp32 scale:        */
-/*   amax = max |x|; inv = 448 / amax; q = e4m3(clamp(x * inv, +-448));        */
-/*   scale = amax / 448 (0 and inv 0 for an all-zero row); value = q * scale.  */
+/*   amax = max |x|; scale = the smallest power of two P >= 2^-126 with         */
+/*   amax <= 448 P; q = e4m3(clamp(x / P, +-448)) (scale 0 and q 0 for an       */
+/*   all-zero row); value = q * scale.                                          */
 /* Scales live in [slot / bs][kv_head][slot % bs] order, so the 16 scales of a  */
 /* block's rows for one head are contiguous.                                   */
 /* ------------------------------------------------------------------------- */
@@ -590,14 +591,22 @@ int64_t orc_fp8_scale_index(int slot, int kv_head, int num_kv_heads, int block_s
            slot % block_size;
 }
 
+float orc_fp8_row_scale(float amax) {
+    if (!(amax > 0.0f)) return 0.0f;
+    /* smallest p with amax <= 448 * 2^p, by search (448 * 2^p is exact in float) */
+    int p = -126;
+    while (p < 127 && amax > ldexpf(448.0f, p)) ++p;
+    return ldexpf(1.0f, p);
+}
+
 void orc_quantize_row_fp8(const uint16_t* x, int n, uint8_t* q, float* scale) {
     float amax = 0.0f;
     for (int d = 0; d < n; ++d) {
         const float a = fabsf(orc_bf16_to_f32(x[d]));
         if (a > amax) amax = a;
     }
-    const float inv = amax > 0.0f ? 448.0f / amax : 0.0f;
-    *scale = amax > 0.0f ? amax / 448.0f : 0.0f;
+    *scale = orc_fp8_row_scale(amax);
+    const float inv = amax > 0.0f ? 1.0f / *scale : 0.0f;
     for (int d = 0; d < n; ++d) {
         float v = orc_bf16_to_f32(x[d]) * inv;
         v = v > 448.0f ? 448.0f : (v < -448.0f ? -448.0f : v);

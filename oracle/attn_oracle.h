@@ -134,6 +134,7 @@ int orc_build_batch_metadata(const int32_t* item_kv_written, const int32_t* item
 uint8_t orc_f32_to_e4m3(float x);
 float orc_e4m3_to_f32(uint8_t b);
 int64_t orc_fp8_scale_index(int slot, int kv_head, int num_kv_heads, int block_size);
+float orc_fp8_row_scale(float amax);
 void orc_quantize_row_fp8(const uint16_t* x, int n, uint8_t* q, float* scale);
 void orc_write_kv_cache_fp8(const uint16_t* k_new, const uint16_t* v_new, uint8_t* k_cache,
                             uint8_t* v_cache, float* k_scale, float* v_scale,

@@ -28,6 +28,12 @@ def test_write_bit_exact(gpu, hkv, d):
     v = rnd_bf16(rng, (t, hkv, d), 1e-3)
     k[4] = 0                                       # all-zero rows: scale 0
     v[6, 0, 1] = oracle.f32_to_bf16(np.float32(1e30))   # one huge element
+    # scale boundaries: amax exactly 448 (scale 1), just above (scale 2), tiny (2^-126)
+    k[7] = oracle.f32_to_bf16(np.float32(0.5))
+    k[7, :, 3] = oracle.f32_to_bf16(np.float32(448.0))
+    k[8] = oracle.f32_to_bf16(np.float32(-1.0))
+    k[8, :, 5] = oracle.f32_to_bf16(np.float32(-450.0))
+    k[10] = oracle.f32_to_bf16(np.float32(2e-38))
     sm = rng.permutation(slots)[:t].astype(np.int32)
     sm[2], sm[9] = -1, slots + 4                   # skipped
     nsc = fp8_scale_numel(slots, hkv)
@@ -236,3 +242,31 @@ def test_prefill_fp8_holes_ragged_and_untouched_rows(gpu):
     assert np.all(got[qsl[3]:qsl[4]] == 7.0)
     assert np.all(np.isfinite(got))
     assert_attn_close(got, want, "fp8 edge")
+
+
+def test_prefill_fp8_any_scale_equals_bf16_prefill_of_dequantised_cache(gpu):
+    """Scales that are not powers of two (a caller's own quantiser) take the general
+    conversion (float product, rounded to bf16); power-of-two rows of the same tiles take the
+    one-instruction conversion. Both must equal the bf16 prefill over bf16(byte * scale)."""
+    from ccinfer_amd import prefill_attention, prefill_attention_fp8
+    say("fp8 prefill with arbitrary scales")
+    hq, hkv, d = 16, 8, 128
+    w = W.prefill_prefix(device=gpu, seed=77, n_seqs=3, prefix=96, new=150, hq=hq, hkv=hkv,
+                         d=d)
+    meta = w.device_meta(gpu)
+    kc, vc, ks, vs = quantised_cache(gpu, w, hkv, d)
+    rng = np.random.default_rng(3)
+    for s in (ks, vs):
+        f = rng.uniform(0.6, 1.9, s.numel()).astype(np.float32)
+        f[rng.random(s.numel()) < 0.5] = 1.0      # about half the rows keep a power of two
+        s.mul_(torch.from_numpy(f).to(gpu))
+    sc = ks.cpu().numpy().view(np.uint32)
+    assert 0.2 < np.mean((sc & 0x7FFFFF) == 0) < 0.8
+    out8 = prefill_attention_fp8(w.q, kc, vc, ks, vs, meta["block_table"],
+                                 meta["query_start_loc"], meta["context_lens"])
+    kb = from_u16(_dequant_bf16(kc.cpu().numpy(), ks.cpu().numpy(), hkv), gpu)
+    vb = from_u16(_dequant_bf16(vc.cpu().numpy(), vs.cpu().numpy(), hkv), gpu)
+    out16 = prefill_attention(w.q, kb, vb, meta["block_table"], meta["query_start_loc"],
+                              meta["context_lens"])
+    torch.cuda.synchronize()
+    assert torch.equal(out8, out16)

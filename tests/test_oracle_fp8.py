@@ -80,14 +80,16 @@ def test_write_quantises_each_row_within_half_an_e4m3_step():
                 if amax == 0:
                     assert s == 0 and np.all(deq[sm[i], h] == 0)
                     continue
-                assert s == np.float32(amax) / np.float32(448)
+                # the smallest power of two with amax <= 448 s
+                assert s == 2.0 ** np.ceil(np.log2(np.float64(amax) / 448.0))
+                assert amax <= 448 * s and amax > 224 * s
                 # E4M3 spacing at |q| is 2^(floor(log2|q|) - 3) (2^-9 below 2^-6): the error
                 # is at most half a step, times the scale
                 q = np.abs(row) / s
                 step = np.where(q < 2 ** -6, 2.0 ** -9, 2.0 ** (np.floor(np.log2(np.maximum(
                     q, 2 ** -6))) - 3))
                 assert np.all(np.abs(deq[sm[i], h] - row) <= 0.5 * step * s * (1 + 1e-5) + 1e-30)
-                assert np.max(np.abs(deq[sm[i], h])) == pytest.approx(amax, rel=1e-6)
+                assert np.max(np.abs(deq[sm[i], h])) == pytest.approx(amax, rel=2.0 ** -4)
     # skipped slot and untouched slots keep their bytes
     written = set(sm[sm >= 0].tolist())
     for sl in range(slots):
@@ -182,3 +184,20 @@ def test_fp8_prefill_equals_float64_causal_attention():
         ref = F.scaled_dot_product_attention(qq, kk, vv,
                                              attn_mask=torch.from_numpy(mask)[None])[0].numpy()
         np.testing.assert_allclose(got[:, h], ref, rtol=2e-5, atol=2e-6)
+
+
+def test_row_scale_boundaries():
+    # amax exactly 448 * 2^k keeps scale 2^k; just above doubles it; tiny rows stop at 2^-126
+    rows = [(448.0, 1.0), (450.0, 2.0), (224.0, 0.5), (1.0, 2.0 ** -8), (7.0, 2.0 ** -6),
+            (2e-38, 2.0 ** -126), (3.0e38, 2.0 ** 120)]
+    hkv, d = 1, 4
+    for amax, want in rows:
+        x = np.zeros((1, hkv, d), np.float32)
+        x[0, 0, 1] = -amax
+        k = oracle.f32_to_bf16(x)
+        amax_b = float(np.abs(oracle.bf16_to_f32(k)).max())
+        kc = np.zeros((16, hkv, d), np.uint8)
+        ks = np.zeros(16 * hkv, np.float32)
+        oracle.write_kv_cache_fp8(k, k, kc, kc.copy(), ks, ks.copy(), np.array([0], np.int32))
+        assert ks[0] == want, (amax, ks[0])
+        assert amax_b <= 448 * ks[0] and (amax_b > 224 * ks[0] or ks[0] == 2.0 ** -126)
