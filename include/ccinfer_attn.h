@@ -19,8 +19,10 @@
  * ccinfer::ErrorCode (src/base/error_code.h:8-45) -- the same codes the reference returns
  * through Result<void>.
  *
- * Thread safety: stateless and re-entrant (the library keeps no global state); concurrent
- * calls on different streams must use different workspaces.
+ * Thread safety: re-entrant. The library keeps no global state except the per-device scratch
+ * array of ccinfer_decode_attention_noalloc (and that array's cached device address), so
+ * concurrent calls on different streams need only different workspaces -- apart from that
+ * entry, whose calls on one GPU share the array.
  *
  * Alignment: the reference launchers accept any bf16 (2-byte aligned) view. The MFMA paths
  * move q, output and K/V cache rows in 16-byte pieces, so bf16 decode / prefill calls with
