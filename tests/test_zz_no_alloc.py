@@ -61,3 +61,29 @@ def test_no_alloc_rejects_shapes_beyond_the_static_scratch(gpu):
     fake = ctypes.c_void_p(0x1000)
     assert lib.ccinfer_decode_attention_noalloc(fake, fake, fake, fake, fake, fake, b, mbpr, hq,
                                                 hkv, d, 16, None) == INVALID
+
+
+def test_no_alloc_decode_under_graph_capture(gpu):
+    """The entry's intended caller: a decode captured in a HIP graph without a workspace.
+    Each replay (with eager work and synchronisations between) equals the eager call."""
+    say("no-alloc decode captured in a graph")
+    lib = _lib.load()
+    w = W.decode_batched(device=gpu, seed=53, batch=40, ctx_hi=3000, with_write=False)
+    meta = w.device_meta(gpu)
+    out = torch.full_like(w.q, float("nan"))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        assert _no_alloc(lib, w, meta, out, s.cuda_stream) == 0
+    torch.cuda.synchronize()
+    eager = out.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        rc = _no_alloc(lib, w, meta, out, s.cuda_stream)
+    assert rc == 0
+    for rep in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), rep
