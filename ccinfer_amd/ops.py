@@ -287,7 +287,8 @@ def fp8_scale_numel(max_slots: int, num_kv_heads: int, block_size: int = 16) -> 
 def write_kv_cache_fp8(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor,
                        v_cache: torch.Tensor, k_scale: torch.Tensor, v_scale: torch.Tensor,
                        slot_mapping: torch.Tensor, max_slots: Optional[int] = None) -> None:
-    """write_kv_cache into an fp8 (OCP E4M3) cache with one fp32 scale per cache row.
+    """write_kv_cache into an fp8 (OCP E4M3) cache with one fp32 scale per cache row (the
+    smallest power of two P with max|row| <= 448 P; the row is stored as e4m3(row / P)).
     k_cache / v_cache: uint8 [slots, Hkv, D] (or [blocks, 16, Hkv, D]); scales: float32 of
     fp8_scale_numel(slots, Hkv) elements."""
     op = "write_kv_cache_fp8"
