@@ -56,8 +56,16 @@ constexpr int kBlock = 16;        // tokens per KV block (the reference's kKVBlo
 constexpr int kChunk = 32;        // tokens per PV MFMA
 constexpr int kWavesPerGroup = 4;
 constexpr int kMaxSplitTokens = 2048;  // 128 blocks: two table entries per lane
-// Wavefronts the split plan aims for: two resident per SIMD on 1024 SIMDs, two rounds.
+// Wavefronts the split plan aims for: two resident per SIMD on 1024 SIMDs, two rounds. That
+// suits ragged batches, whose splits vary in length; batches of equal-length rows run
+// fastest with one 4-wavefront workgroup per CU (kEvenWaves: fewer, longer splits, a
+// shallower merge), measured on 4-128 requests of 2-16K positions: 7-51 % faster, e.g.
+// 8 x 4096 positions 36.2 -> 27.5 us, 64 x 4096 171 -> 162 us.
 constexpr int64_t kTargetWaves = 4096;
+constexpr int64_t kEvenWaves = 1024;
+// Rows count as equal-length when the batch's chunks are at least this share (percent) of
+// batch size x longest row (75 % already slowed a 3000-4096-position batch).
+constexpr int kEvenRowsPct = 90;
 constexpr int kBalancedMinItems = 4;
 // The group plan (one workgroup per (request, kv_head), parts merged in LDS) streams a row
 // from one CU, which reads ~30 GB/s; it pays off only where the row is short enough that
@@ -154,7 +162,9 @@ __device__ __forceinline__ int effective_ctx(int ctx, int mbpr, int zero_invalid
 // ---- balanced split plan (evaluated identically by every wavefront) ----
 // C = total 32-token chunks of the batch's valid contexts; every split covers
 // T = clamp(ceil(C / W), 1, kMaxSplitTokens / kChunk) chunks, so all wavefronts stream about
-// the same number of tokens whatever the spread of context lengths. Request r gets
+// the same number of tokens whatever the spread of context lengths. W, the wavefronts per kv
+// head, is the host's kTargetWaves share, cut by kTargetWaves / kEvenWaves when the rows are
+// near equal in length (C >= kEvenRowsPct % of B x the longest row). Request r gets
 // ceil(c_r / T) splits (one zero-writing split if its context is invalid), laid out
 // request-major in split slots 0, 1, ... of each kv_head.
 struct BalancedSplit {
@@ -214,6 +224,15 @@ __device__ bool balanced_lookup(const int32_t* __restrict__ context_lens, const 
         }
     }
     const int C = wave_sum_i32(total);
+    {
+        int longest = 0;
+#pragma unroll
+        for (int k = 0; k < kBalancedMaxItems / 64; ++k) longest = max(longest, cr[k]);
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) longest = max(longest, __shfl_xor(longest, off));
+        if (static_cast<int64_t>(C) * 100 >= static_cast<int64_t>(kEvenRowsPct) * B * longest)
+            W = max(1, static_cast<int>(W * kEvenWaves / kTargetWaves));
+    }
     int T = (C + W - 1) / W;
     T = T < 1 ? 1 : (T > kMaxSplitTokens / kChunk ? kMaxSplitTokens / kChunk : T);
     int carry = 0;
@@ -1043,10 +1062,19 @@ DecodePlan plan_decode(int num_items, int num_q_heads, int num_kv_heads, int max
         p.split_tokens = 0;
         return p;
     }
-    const int64_t target_waves = kTargetWaves;
-    const int64_t total = static_cast<int64_t>(num_items) * num_kv_heads * chunks;
-    int64_t cpw = (total + target_waves - 1) / target_waves;
+    // Splits sized for the longest possible row. Batches of 1-3 requests: at most kEvenWaves
+    // wavefronts after rounding (one workgroup per CU: a few workgroups more than CUs would
+    // leave those CUs running two in a row); measured against the kTargetWaves sizing, one
+    // request of 8K / 16K / 32K positions 26.7 / 50.4 / 61.6 -> 18.0 / 23.2 / 32.6 us. Larger
+    // batches on this plan (past the balanced plan's request limit, or without it) keep
+    // kTargetWaves: 300 requests of 100-3000 positions ran 456 -> 497 us with kEvenWaves.
+    const int64_t groups = static_cast<int64_t>(num_items) * num_kv_heads;
+    const int64_t target = num_items < kBalancedMinItems ? kEvenWaves : kTargetWaves;
+    int64_t cpw = (groups * chunks + target - 1) / target;
     if (cpw < 1) cpw = 1;
+    while (num_items < kBalancedMinItems && cpw < chunks &&
+           groups * ((chunks + cpw - 1) / cpw) > kEvenWaves)
+        ++cpw;
     if (cpw > kMaxChunksPerSplit) cpw = kMaxChunksPerSplit;
     if (cpw > chunks) cpw = chunks;
     p.split_tokens = static_cast<int>(cpw) * kChunk;
