@@ -56,16 +56,12 @@ constexpr int kBlock = 16;        // tokens per KV block (the reference's kKVBlo
 constexpr int kChunk = 32;        // tokens per PV MFMA
 constexpr int kWavesPerGroup = 4;
 constexpr int kMaxSplitTokens = 2048;  // 128 blocks: two table entries per lane
-// Wavefronts the split plan aims for: two resident per SIMD on 1024 SIMDs, two rounds. That
-// suits ragged batches, whose splits vary in length; batches of equal-length rows run
-// fastest with one 4-wavefront workgroup per CU (kEvenWaves: fewer, longer splits, a
-// shallower merge), measured on 4-128 requests of 2-16K positions: 7-51 % faster, e.g.
-// 8 x 4096 positions 36.2 -> 27.5 us, 64 x 4096 171 -> 162 us.
+// Wavefronts the fixed split plan aims for on batches of 4+ requests: two resident per SIMD
+// on 1024 SIMDs, two rounds (splits are sized for the longest possible row, so their work
+// varies). Plans whose splits carry equal work -- the on-device flat plan, and the fixed plan
+// of 1-3 requests -- run fastest with kEvenWaves, one 4-wavefront workgroup per CU.
 constexpr int64_t kTargetWaves = 4096;
 constexpr int64_t kEvenWaves = 1024;
-// Rows count as equal-length when the batch's chunks are at least this share (percent) of
-// batch size x longest row (75 % already slowed a 3000-4096-position batch).
-constexpr int kEvenRowsPct = 90;
 constexpr int kBalancedMinItems = 4;
 // The group plan (one workgroup per (request, kv_head), parts merged in LDS) streams a row
 // from one CU, which reads ~30 GB/s; it pays off only where the row is short enough that
@@ -159,23 +155,6 @@ __device__ __forceinline__ int effective_ctx(int ctx, int mbpr, int zero_invalid
     return ctx < cap ? ctx : cap;
 }
 
-// ---- balanced split plan (evaluated identically by every wavefront) ----
-// C = total 32-token chunks of the batch's valid contexts; every split covers
-// T = clamp(ceil(C / W), 1, kMaxSplitTokens / kChunk) chunks, so all wavefronts stream about
-// the same number of tokens whatever the spread of context lengths. W, the wavefronts per kv
-// head, is the host's kTargetWaves share, cut by kTargetWaves / kEvenWaves when the rows are
-// near equal in length (C >= kEvenRowsPct % of B x the longest row). Request r gets
-// ceil(c_r / T) splits (one zero-writing split if its context is invalid), laid out
-// request-major in split slots 0, 1, ... of each kv_head.
-struct BalancedSplit {
-    int req;          // request of the split
-    int split;        // split index within the request
-    int nsplit;       // splits of the request
-    int first_slot;   // slot of the request's first split
-    int split_tokens; // T * kChunk
-    int ctx;          // effective context of the request (-1: invalid)
-};
-
 __device__ __forceinline__ int wave_inclusive_scan(int v, int lane) {
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -191,71 +170,98 @@ __device__ __forceinline__ int wave_sum_i32(int v) {
     return v;
 }
 
-// Finds the split of slot `slot` (by_request == false) or the splits of request `slot`
-// (by_request == true). Returns false when the slot is past the last split.
-__device__ bool balanced_lookup(const int32_t* __restrict__ context_lens, const ItemArgs& items,
-                                int mbpr, int W, int slot, bool by_request, int lane,
-                                BalancedSplit* out) {
-    // Items (query rows) in order; item i is request item_req[i] when a list is given, and
-    // items past the device-side count have no splits.
+// ---- flat split plan (evaluated identically by every wavefront) ----
+// The rows' 32-token chunks laid end to end (C in total, per kv head) are cut into ranges of
+// T = clamp(ceil(C / W), 1, kMaxSplitTokens / kChunk) chunks, one per wavefront, whatever
+// the row boundaries: every wavefront streams the same number of chunks (the last one
+// fewer), so W wavefronts -- one 4-wavefront workgroup per CU -- stay evenly loaded on
+// ragged batches. A range that crosses a row boundary is processed as one segment per row.
+// Row r (chunk offset P_r, c_r chunks) gets one split per range it meets, numbered from
+// the range that holds its first chunk, with its partial rows at S_r, the exclusive sum of
+// the split counts before it.
+struct FlatSegment {
+    int req;         // request (item) of the segment
+    int split;       // split index within the request
+    int nsplit;      // splits of the request
+    int first_slot;  // partial slot of the request's first split (S_r)
+    int begin, end;  // positions of the segment
+    int ctx;         // effective context of the request
+    bool more;       // the range continues into a later request
+};
+
+// The k-th segment of wavefront w's range. Returns false past the last one. *invalid_w:
+// whether request w's context is invalid (then no range holds a chunk of it).
+__device__ bool flat_segment(const int32_t* __restrict__ context_lens, const ItemArgs& items,
+                             int mbpr, int W, int w, int k, int lane, FlatSegment* out,
+                             bool* invalid_w) {
     int B = items.num_items;
     if (items.item_count != nullptr) B = min(B, *items.item_count);
-    const int zero_invalid = items.zero_invalid;
     const int rounds = (B + 63) / 64;  // B <= kBalancedMaxItems
     int cr[kBalancedMaxItems / 64];
     int ectx[kBalancedMaxItems / 64];
-    bool valid[kBalancedMaxItems / 64];
     int total = 0;
 #pragma unroll
-    for (int k = 0; k < kBalancedMaxItems / 64; ++k) {
-        cr[k] = 0;
-        ectx[k] = -1;
-        valid[k] = false;
-        if (k < rounds) {
-            const int r = k * 64 + lane;
+    for (int x = 0; x < kBalancedMaxItems / 64; ++x) {
+        cr[x] = 0;
+        ectx[x] = -1;
+        if (x < rounds) {
+            const int r = x * 64 + lane;
             if (r < B) {
                 const int req = items.item_req != nullptr ? items.item_req[r] : r;
-                const int ctx = effective_ctx(context_lens[req], mbpr, zero_invalid);
-                ectx[k] = ctx;
-                valid[k] = ctx >= 0;
-                cr[k] = ctx > 0 ? (ctx + kChunk - 1) / kChunk : 0;
+                const int ctx = effective_ctx(context_lens[req], mbpr, items.zero_invalid);
+                ectx[x] = ctx;
+                cr[x] = ctx > 0 ? (ctx + kChunk - 1) / kChunk : 0;
             }
-            total += cr[k];
+            total += cr[x];
         }
     }
     const int C = wave_sum_i32(total);
-    {
-        int longest = 0;
+    if (w < B) {
+        const int e = __builtin_amdgcn_readlane(ectx[0], w & 63);
+        int ew = e;
 #pragma unroll
-        for (int k = 0; k < kBalancedMaxItems / 64; ++k) longest = max(longest, cr[k]);
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) longest = max(longest, __shfl_xor(longest, off));
-        if (static_cast<int64_t>(C) * 100 >= static_cast<int64_t>(kEvenRowsPct) * B * longest)
-            W = max(1, static_cast<int>(W * kEvenWaves / kTargetWaves));
+        for (int x = 1; x < kBalancedMaxItems / 64; ++x)
+            if ((w >> 6) == x) ew = __builtin_amdgcn_readlane(ectx[x], w & 63);
+        *invalid_w = ew < 0;
+    } else {
+        *invalid_w = false;
     }
     int T = (C + W - 1) / W;
     T = T < 1 ? 1 : (T > kMaxSplitTokens / kChunk ? kMaxSplitTokens / kChunk : T);
-    int carry = 0;
+    const int lo = w * T;
+    if (lo >= C) return false;
+    const int hi = min(lo + T, C);
+    int carry_p = 0, carry_s = 0, found = 0;
 #pragma unroll
-    for (int k = 0; k < kBalancedMaxItems / 64; ++k) {
-        if (k >= rounds) break;
-        const int r = k * 64 + lane;
-        const int sr = r < B ? (valid[k] && cr[k] > 0 ? (cr[k] + T - 1) / T : 1) : 0;
-        const int incl = wave_inclusive_scan(sr, lane) + carry;
-        const int excl = incl - sr;
-        const bool hit = by_request ? (r == slot) : (slot >= excl && slot < incl);
+    for (int x = 0; x < kBalancedMaxItems / 64; ++x) {
+        if (x >= rounds) break;
+        const int r = x * 64 + lane;
+        const int c = cr[x];
+        const int p = wave_inclusive_scan(c, lane) - c + carry_p;
+        const int nsr = c > 0 ? (p + c - 1) / T - p / T + 1 : 0;
+        const int sr = wave_inclusive_scan(nsr, lane) - nsr + carry_s;
+        const bool hit = r < B && c > 0 && p < hi && p + c > lo;
         const uint64_t m = __builtin_amdgcn_ballot_w64(hit);
-        if (m != 0) {
-            const int src = __builtin_ffsll(static_cast<long long>(m)) - 1;
-            out->req = k * 64 + src;
-            out->first_slot = __builtin_amdgcn_readlane(excl, src);
-            out->nsplit = __builtin_amdgcn_readlane(sr, src);
-            out->split = slot - out->first_slot;
-            out->split_tokens = T * kChunk;
-            out->ctx = __builtin_amdgcn_readlane(ectx[k], src);
+        const int n = __builtin_popcountll(static_cast<long long>(m));
+        if (k < found + n) {
+            uint64_t mm = m;
+            for (int i = 0; i < k - found; ++i) mm &= mm - 1;  // drop the lower segments
+            const int src = __builtin_ffsll(static_cast<long long>(mm)) - 1;
+            const int ps = __builtin_amdgcn_readlane(p, src);
+            const int cs = __builtin_amdgcn_readlane(c, src);
+            out->req = x * 64 + src;
+            out->ctx = __builtin_amdgcn_readlane(ectx[x], src);
+            out->nsplit = __builtin_amdgcn_readlane(nsr, src);
+            out->first_slot = __builtin_amdgcn_readlane(sr, src);
+            out->split = w - ps / T;
+            out->begin = (max(lo, ps) - ps) * kChunk;
+            out->end = min(out->ctx, (min(hi, ps + cs) - ps) * kChunk);
+            out->more = ps + cs < hi;
             return true;
         }
-        carry = __builtin_amdgcn_readlane(incl, 63);
+        found += n;
+        carry_p = __builtin_amdgcn_readlane(p + c, 63);
+        carry_s = __builtin_amdgcn_readlane(sr + nsr, 63);
     }
     return false;
 }
@@ -704,37 +710,23 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     // slot next to each other), which measured 10-20% faster than split-fastest ordering.
     const int h = wi % hkv;
     const int rest = wi / hkv;
-    int s, item, ns_bal = 0, first_slot = 0, ctx_bal = 0;
-    if (balanced_w > 0) {
-        BalancedSplit bs;
-        if (rest >= slots ||
-            !balanced_lookup(context_lens, items, mbpr, balanced_w, rest, false, lane, &bs))
-            return;
-        item = bs.req;
-        s = bs.split;
-        ns_bal = bs.nsplit;
-        first_slot = bs.first_slot;
-        split_tokens = bs.split_tokens;
-        ctx_bal = bs.ctx;
-    } else {
-        s = rest % splits;
-        item = rest / splits;
-    }
-
-    int req, qrow;
-    if (!resolve_item(items, item, &req, &qrow)) return;
-    const int ctx =
-        balanced_w > 0 ? ctx_bal : effective_ctx(context_lens[req], mbpr, items.zero_invalid);
+    // balanced_w > 0: the on-device flat plan with W = balanced_w wavefronts per kv head,
+    // partial slots numbered per q-head from 0 to slots; 0: the fixed plan.
+    const bool slotted = balanced_w != 0;
     const int G = hq / hkv;
     const int j = lane & 15;
     const int g = lane >> 4;
-    const int ns = balanced_w > 0 ? ns_bal
-                                  : (ctx > 0 ? (ctx + split_tokens - 1) / split_tokens : 0);
+
+    // One split (the item's s-th of ns, over positions [begin, end)).
+    auto process = [&](int item, int s, int ns, int first_slot, int ctx, int begin,
+                       int end) __attribute__((always_inline)) {
+    int req, qrow;
+    if (!resolve_item(items, item, &req, &qrow)) return;
     if (desc != nullptr && s == 0 && lane < G) {
         const int head = h * G + lane;
         desc[static_cast<int64_t>(item) * hq + head] = MergeDesc{
-            balanced_w > 0 ? static_cast<int64_t>(head) * slots + first_slot
-                           : (static_cast<int64_t>(item) * hq + head) * splits,
+            slotted ? static_cast<int64_t>(head) * slots + first_slot
+                    : (static_cast<int64_t>(item) * hq + head) * splits,
             ctx > 0 ? ns : 0};
     }
 
@@ -747,9 +739,7 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
         }
         return;
     }
-    const int begin = s * split_tokens;
-    if (begin >= ctx) return;
-    const int end = min(ctx, begin + split_tokens);
+    if (begin >= end) return;
     if constexpr (!F8) {
         if (items.new_k != nullptr && end == ctx)
             write_new_token<kPad>(k_cache, v_cache, items, block_table + static_cast<int64_t>(req) * mbpr,
@@ -785,9 +775,8 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     // Partial of this split; decode_merge_kernel combines the splits.
     if (!live) return;
     // Partials of one row are contiguous over its splits.
-    const int64_t slot = balanced_w > 0
-                             ? static_cast<int64_t>(head) * slots + first_slot + s
-                             : (static_cast<int64_t>(item) * hq + head) * splits + s;
+    const int64_t slot = slotted ? static_cast<int64_t>(head) * slots + first_slot + s
+                                 : (static_cast<int64_t>(item) * hq + head) * splits + s;
     float* po = ws_o + slot * D;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -808,6 +797,33 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
         ws_ml[slot * 2 + 0] = st.m;
         ws_ml[slot * 2 + 1] = l_tot;
     }
+    };
+
+    if (balanced_w > 0) {
+        // Flat plan: wavefront `rest` walks the segments of its chunk range; it also owns
+        // the zero output and empty merge descriptor of request `rest` when that request's
+        // context is invalid (no range holds a chunk of it).
+        if (rest >= slots) return;
+        const int W = balanced_w;
+        FlatSegment fs;
+        bool invalid_w = false;
+        bool ok = flat_segment(context_lens, items, mbpr, W, rest, 0, lane, &fs, &invalid_w);
+        if (invalid_w) process(rest, 0, 0, 0, -1, 0, 0);
+        for (int k = 1; ok; ++k) {
+            process(fs.req, fs.split, fs.nsplit, fs.first_slot, fs.ctx, fs.begin, fs.end);
+            if (!fs.more) break;
+            ok = flat_segment(context_lens, items, mbpr, W, rest, k, lane, &fs, &invalid_w);
+        }
+        return;
+    }
+    const int s = rest % splits;
+    const int item = rest / splits;
+    int req, qrow;
+    if (!resolve_item(items, item, &req, &qrow)) return;
+    const int ctx = effective_ctx(context_lens[req], mbpr, items.zero_invalid);
+    const int ns = ctx > 0 ? (ctx + split_tokens - 1) / split_tokens : 0;
+    const int begin = s * split_tokens;
+    process(item, s, ns, 0, ctx, begin, ctx > 0 ? min(ctx, begin + split_tokens) : 0);
 }
 
 // Single-launch decode for batches with few (item, kv_head) groups: one workgroup of W
@@ -1051,9 +1067,13 @@ DecodePlan plan_decode(int num_items, int num_q_heads, int num_kv_heads, int max
     if (allow_balanced && num_items >= kBalancedMinItems &&
         num_items <= kBalancedMaxItems && chunks > 1) {
         p.balanced = true;
-        p.wave_target = static_cast<int>(std::max<int64_t>(1, kTargetWaves / num_kv_heads));
-        // Splits per kv_head: at most C/T + B with T >= C/W (or, with T at its cap,
-        // B * chunks / cap + B), and never more than one per chunk.
+        // One workgroup per CU, and at least one range per request and kv head (many short
+        // rows would otherwise crowd several segments into each range).
+        p.wave_target = static_cast<int>(std::max<int64_t>(
+            std::max<int64_t>(1, kEvenWaves / num_kv_heads), num_items));
+        // Splits per kv_head: one per range plus one per row boundary inside a range, so at
+        // most C/T + B with T >= C/W (or, with T at its cap, B * chunks / cap + B), and
+        // never more than one per chunk.
         const int64_t capped =
             static_cast<int64_t>(num_items) * ((chunks + kMaxChunksPerSplit - 1) / kMaxChunksPerSplit);
         const int64_t bound = std::max<int64_t>(p.wave_target, capped) + num_items;

@@ -17,11 +17,11 @@ hipError_t write_kv_cache(const void* k_new, const void* v_new, void* k_cache, v
 // ---- decode ---------------------------------------------------------------
 // Split-KV plan: `splits` partitions of `split_tokens` tokens per (request, kv_head).
 // Split-KV plan. Fixed mode: `splits` partitions of `split_tokens` tokens per (request,
-// kv_head), sized from the longest possible context. Balanced mode (plain decode batches of
-// up to kBalancedMaxItems requests): the split length is chosen on the device from the
-// batch's actual total context so that every wavefront streams about the same number of
-// tokens; `slots` bounds the number of splits per kv_head and `wave_target` is the number
-// of wavefronts per kv_head the split length aims for.
+// kv_head), sized from the longest possible context. Balanced mode (decode batches of 4 to
+// kBalancedMaxItems requests): the flat plan -- on the device, the batch's 32-token chunks
+// laid end to end are cut into wave_target equal ranges per kv_head, one per wavefront,
+// across request boundaries, so every wavefront streams the same number of tokens whatever
+// the spread of context lengths; `slots` bounds the number of splits per kv_head.
 struct DecodePlan {
     int splits = 1;
     int split_tokens = 0;  // multiple of 32
