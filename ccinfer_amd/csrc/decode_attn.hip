@@ -216,16 +216,10 @@ __device__ bool flat_segment(const int32_t* __restrict__ context_lens, const Ite
         }
     }
     const int C = wave_sum_i32(total);
-    if (w < B) {
-        const int e = __builtin_amdgcn_readlane(ectx[0], w & 63);
-        int ew = e;
+    *invalid_w = false;
 #pragma unroll
-        for (int x = 1; x < kBalancedMaxItems / 64; ++x)
-            if ((w >> 6) == x) ew = __builtin_amdgcn_readlane(ectx[x], w & 63);
-        *invalid_w = ew < 0;
-    } else {
-        *invalid_w = false;
-    }
+    for (int x = 0; x < kBalancedMaxItems / 64; ++x)
+        if (w < B && (w >> 6) == x) *invalid_w = __builtin_amdgcn_readlane(ectx[x], w & 63) < 0;
     int T = (C + W - 1) / W;
     T = T < 1 ? 1 : (T > kMaxSplitTokens / kChunk ? kMaxSplitTokens / kChunk : T);
     const int lo = w * T;
@@ -714,12 +708,16 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     // partial slots numbered per q-head from 0 to slots; 0: the fixed plan.
     const bool slotted = balanced_w != 0;
     const int G = hq / hkv;
+
+    // One split (the item's s-th of ns, over positions [begin, end)). The lane index comes
+    // in as an argument: at the padded head dims up to 128 the flat plan passes it through
+    // an empty asm on every segment, so the compiler recomputes the lane-derived addressing
+    // per segment instead of holding it across the segment loop (70 spilled VGPRs without,
+    // 17 with, outside the chunk loop); elsewhere that recomputation measured slower.
+    auto process = [&](int lane, int item, int s, int ns, int first_slot, int ctx, int begin,
+                       int end) __attribute__((always_inline)) {
     const int j = lane & 15;
     const int g = lane >> 4;
-
-    // One split (the item's s-th of ns, over positions [begin, end)).
-    auto process = [&](int item, int s, int ns, int first_slot, int ctx, int begin,
-                       int end) __attribute__((always_inline)) {
     int req, qrow;
     if (!resolve_item(items, item, &req, &qrow)) return;
     if (desc != nullptr && s == 0 && lane < G) {
@@ -808,9 +806,12 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
         FlatSegment fs;
         bool invalid_w = false;
         bool ok = flat_segment(context_lens, items, mbpr, W, rest, 0, lane, &fs, &invalid_w);
-        if (invalid_w) process(rest, 0, 0, 0, -1, 0, 0);
+        if (invalid_w) process(lane, rest, 0, 0, 0, -1, 0, 0);
         for (int k = 1; ok; ++k) {
-            process(fs.req, fs.split, fs.nsplit, fs.first_slot, fs.ctx, fs.begin, fs.end);
+            int lane_k = lane;
+            if constexpr (kPad && D == 128) asm volatile("" : "+v"(lane_k));
+            process(lane_k, fs.req, fs.split, fs.nsplit, fs.first_slot, fs.ctx, fs.begin,
+                    fs.end);
             if (!fs.more) break;
             ok = flat_segment(context_lens, items, mbpr, W, rest, k, lane, &fs, &invalid_w);
         }
@@ -823,7 +824,7 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     const int ctx = effective_ctx(context_lens[req], mbpr, items.zero_invalid);
     const int ns = ctx > 0 ? (ctx + split_tokens - 1) / split_tokens : 0;
     const int begin = s * split_tokens;
-    process(item, s, ns, 0, ctx, begin, ctx > 0 ? min(ctx, begin + split_tokens) : 0);
+    process(lane, item, s, ns, 0, ctx, begin, ctx > 0 ? min(ctx, begin + split_tokens) : 0);
 }
 
 // Single-launch decode for batches with few (item, kv_head) groups: one workgroup of W
