@@ -5,19 +5,20 @@
 //   positions addressed through block_table (16-token blocks), negative block ids skipped,
 //   ctx <= 0 or ceil(ctx/16) > max_blocks_per_req -> zeros, denominator sum + 1e-6.
 //
-// Work decomposition (one wavefront = one work item):
-//   item = (query row, kv_head, split). A split covers `split_tokens` consecutive context
-//   positions (a multiple of 32, at most 2048). All Hq/Hkv query heads of the GQA group are
-//   handled by the same wavefront, so every K/V byte of a (request, kv_head) is read from
-//   HBM exactly once.
-//   Split length: batches of 4..256 items use the balanced plan -- every wavefront reads the
-//   items' context lengths, derives the split length from the actual total (so ragged
-//   batches get equal-length splits instead of splits sized for the longest possible
-//   context) and finds its (item, split) with a wave-wide prefix scan. Split 0 of every
+// Work decomposition: a split is a run of consecutive 32-token chunks of one (query row,
+//   kv_head) (at most 2048 positions). All Hq/Hkv query heads of the GQA group are handled
+//   by the same wavefront, so every K/V byte of a (request, kv_head) is read from HBM
+//   exactly once.
+//   Batches of 4..256 items use the flat plan -- every wavefront reads the items' context
+//   lengths, lays their chunks end to end and takes one of W equal ranges of them, across
+//   item boundaries (a range that crosses one is processed as one split per item), so a
+//   ragged batch is evenly loaded in one round of one workgroup per CU; wave-wide prefix
+//   scans find the range's splits and number each item's partial rows. Split 0 of every
 //   row writes a merge descriptor (first partial slot, split count) that the merge kernel
-//   reads, so the merge does not repeat the scan. This also covers the decode items of a mixed prefill
-//   batch, whose list and count the prefill planner writes on the device. Other batches use
-//   a fixed split length chosen on the host from the longest possible context.
+//   reads, so the merge does not repeat the scan. This also covers the decode items of a
+//   mixed prefill batch, whose list and count the prefill planner writes on the device.
+//   Other batches use a fixed split length chosen on the host from the longest possible
+//   context (one wavefront per (item, kv_head, split)).
 //
 // Per 32-token chunk (two 16-token cache blocks) the wavefront computes
 //   S^T[token][head] = K[token][:] . Q^T           (v_mfma_f32_16x16x32_bf16, D/32 steps/block)
@@ -62,7 +63,7 @@ constexpr int kMaxSplitTokens = 2048;  // 128 blocks: two table entries per lane
 // of 1-3 requests -- run fastest with kEvenWaves, one 4-wavefront workgroup per CU.
 constexpr int64_t kTargetWaves = 4096;
 constexpr int64_t kEvenWaves = 1024;
-constexpr int kBalancedMinItems = 4;
+constexpr int kFlatMinItems = 4;
 // The group plan (one workgroup per (request, kv_head), parts merged in LDS) streams a row
 // from one CU, which reads ~30 GB/s; it pays off only where the row is short enough that
 // one launch beats the split plan's two. Measured (one MI355X, 16q/8kv or 32q/8kv, d=128):
@@ -196,12 +197,12 @@ __device__ bool flat_segment(const int32_t* __restrict__ context_lens, const Ite
                              bool* invalid_w) {
     int B = items.num_items;
     if (items.item_count != nullptr) B = min(B, *items.item_count);
-    const int rounds = (B + 63) / 64;  // B <= kBalancedMaxItems
-    int cr[kBalancedMaxItems / 64];
-    int ectx[kBalancedMaxItems / 64];
+    const int rounds = (B + 63) / 64;  // B <= kFlatMaxItems
+    int cr[kFlatMaxItems / 64];
+    int ectx[kFlatMaxItems / 64];
     int total = 0;
 #pragma unroll
-    for (int x = 0; x < kBalancedMaxItems / 64; ++x) {
+    for (int x = 0; x < kFlatMaxItems / 64; ++x) {
         cr[x] = 0;
         ectx[x] = -1;
         if (x < rounds) {
@@ -218,7 +219,7 @@ __device__ bool flat_segment(const int32_t* __restrict__ context_lens, const Ite
     const int C = wave_sum_i32(total);
     *invalid_w = false;
 #pragma unroll
-    for (int x = 0; x < kBalancedMaxItems / 64; ++x)
+    for (int x = 0; x < kFlatMaxItems / 64; ++x)
         if (w < B && (w >> 6) == x) *invalid_w = __builtin_amdgcn_readlane(ectx[x], w & 63) < 0;
     int T = (C + W - 1) / W;
     T = T < 1 ? 1 : (T > kMaxSplitTokens / kChunk ? kMaxSplitTokens / kChunk : T);
@@ -227,7 +228,7 @@ __device__ bool flat_segment(const int32_t* __restrict__ context_lens, const Ite
     const int hi = min(lo + T, C);
     int carry_p = 0, carry_s = 0, found = 0;
 #pragma unroll
-    for (int x = 0; x < kBalancedMaxItems / 64; ++x) {
+    for (int x = 0; x < kFlatMaxItems / 64; ++x) {
         if (x >= rounds) break;
         const int r = x * 64 + lane;
         const int c = cr[x];
@@ -689,7 +690,7 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     const float* __restrict__ v_scale, const int32_t* __restrict__ block_table,
     const int32_t* __restrict__ context_lens, __bf16* __restrict__ out, float* __restrict__ ws_o,
     float* __restrict__ ws_ml, MergeDesc* __restrict__ desc, ItemArgs items, int mbpr, int hq,
-    int hkv, int splits, int split_tokens, int balanced_w, int slots, float scale_log2, int dr,
+    int hkv, int splits, int split_tokens, int flat_w, int slots, float scale_log2, int dr,
     int rep) {
     const int ds = kPad ? dr : D;  // q / output row stride
     constexpr int NV = DecodeShape<D>::kNV;
@@ -704,9 +705,9 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     // slot next to each other), which measured 10-20% faster than split-fastest ordering.
     const int h = wi % hkv;
     const int rest = wi / hkv;
-    // balanced_w > 0: the on-device flat plan with W = balanced_w wavefronts per kv head,
+    // flat_w > 0: the on-device flat plan with W = flat_w wavefronts per kv head,
     // partial slots numbered per q-head from 0 to slots; 0: the fixed plan.
-    const bool slotted = balanced_w != 0;
+    const bool slotted = flat_w != 0;
     const int G = hq / hkv;
 
     // One split (the item's s-th of ns, over positions [begin, end)). The lane index comes
@@ -797,12 +798,12 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     }
     };
 
-    if (balanced_w > 0) {
+    if (flat_w > 0) {
         // Flat plan: wavefront `rest` walks the segments of its chunk range; it also owns
         // the zero output and empty merge descriptor of request `rest` when that request's
         // context is invalid (no range holds a chunk of it).
         if (rest >= slots) return;
-        const int W = balanced_w;
+        const int W = flat_w;
         FlatSegment fs;
         bool invalid_w = false;
         bool ok = flat_segment(context_lens, items, mbpr, W, rest, 0, lane, &fs, &invalid_w);
@@ -830,7 +831,7 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
 // Single-launch decode for batches with few (item, kv_head) groups: one workgroup of W
 // wavefronts per group, wavefront w attending over the w-th of W equal parts of the
 // context; the parts are merged through LDS with the same log-sum-exp weighting as
-// merge_row, so no second kernel and no workspace. (For many groups the balanced split plan
+// merge_row, so no second kernel and no workspace. (For many groups the flat split plan
 // spreads ragged contexts better.)
 template <int D>
 struct GroupShape {
@@ -964,9 +965,9 @@ struct DecodeWs {
     MergeDesc* desc;
 };
 
-// Partial rows of the plan: (item, q_head, split) in fixed mode, (q_head, slot) balanced.
+// Partial rows of the plan: (item, q_head, split) in fixed mode, (q_head, slot) flat.
 size_t partial_rows(int num_items, int hq, const DecodePlan& plan) {
-    return plan.balanced ? static_cast<size_t>(hq) * plan.slots
+    return plan.flat ? static_cast<size_t>(hq) * plan.slots
                          : static_cast<size_t>(num_items) * hq * plan.splits;
 }
 
@@ -1020,14 +1021,14 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
             go(std::false_type{});
         return hipGetLastError();
     }
-    const int64_t waves = plan.balanced
+    const int64_t waves = plan.flat
                               ? static_cast<int64_t>(plan.slots) * hkv
                               : static_cast<int64_t>(it.num_items) * hkv * plan.splits;
     const int grid = static_cast<int>((waves + kWavesPerGroup - 1) / kWavesPerGroup);
-    const bool merge = plan.balanced || plan.splits > 1;
+    const bool merge = plan.flat || plan.splits > 1;
     DecodeWs w{};
     if (merge) w = carve(workspace, partial_rows(it.num_items, hq, plan), D);
-    const int bw = plan.balanced ? plan.wave_target : 0;
+    const int bw = plan.flat ? plan.wave_target : 0;
     auto go = [&](auto tl_tag) {
         decode_split_kernel<D, F8, kPad, decltype(tl_tag)::value><<<grid, 256, 0, stream>>>(
             static_cast<const __bf16*>(q), k_cache, v_cache, k_scale, v_scale, block_table,
@@ -1050,7 +1051,7 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
 }  // namespace
 
 DecodePlan plan_decode(int num_items, int num_q_heads, int num_kv_heads, int max_ctx,
-                       bool allow_balanced) {
+                       bool allow_flat) {
     // Query groups above one MFMA N-tile run as several virtual kv heads (launch_decode).
     num_kv_heads *= decode_head_rep(num_q_heads / num_kv_heads);
     DecodePlan p;
@@ -1065,9 +1066,9 @@ DecodePlan plan_decode(int num_items, int num_q_heads, int num_kv_heads, int max
     constexpr int kMaxChunksPerSplit = kMaxSplitTokens / kChunk;
     // Small batches keep the fixed plan: their splits are already even and the on-device
     // plan would only add its lookup to a latency-bound launch.
-    if (allow_balanced && num_items >= kBalancedMinItems &&
-        num_items <= kBalancedMaxItems && chunks > 1) {
-        p.balanced = true;
+    if (allow_flat && num_items >= kFlatMinItems &&
+        num_items <= kFlatMaxItems && chunks > 1) {
+        p.flat = true;
         // One workgroup per CU, and at least one range per request and kv head (many short
         // rows would otherwise crowd several segments into each range).
         p.wave_target = static_cast<int>(std::max<int64_t>(
@@ -1087,13 +1088,13 @@ DecodePlan plan_decode(int num_items, int num_q_heads, int num_kv_heads, int max
     // wavefronts after rounding (one workgroup per CU: a few workgroups more than CUs would
     // leave those CUs running two in a row); measured against the kTargetWaves sizing, one
     // request of 8K / 16K / 32K positions 26.7 / 50.4 / 61.6 -> 18.0 / 23.2 / 32.6 us. Larger
-    // batches on this plan (past the balanced plan's request limit, or without it) keep
+    // batches on this plan (past the flat plan's request limit, or without it) keep
     // kTargetWaves: 300 requests of 100-3000 positions ran 456 -> 497 us with kEvenWaves.
     const int64_t groups = static_cast<int64_t>(num_items) * num_kv_heads;
-    const int64_t target = num_items < kBalancedMinItems ? kEvenWaves : kTargetWaves;
+    const int64_t target = num_items < kFlatMinItems ? kEvenWaves : kTargetWaves;
     int64_t cpw = (groups * chunks + target - 1) / target;
     if (cpw < 1) cpw = 1;
-    while (num_items < kBalancedMinItems && cpw < chunks &&
+    while (num_items < kFlatMinItems && cpw < chunks &&
            groups * ((chunks + cpw - 1) / cpw) > kEvenWaves)
         ++cpw;
     if (cpw > kMaxChunksPerSplit) cpw = kMaxChunksPerSplit;
@@ -1131,7 +1132,7 @@ DecodePlan plan_decode_items(int num_items, int num_q_heads, int num_kv_heads, i
 
 size_t decode_workspace_bytes(int num_items, int num_q_heads, int head_dim,
                               const DecodePlan& plan) {
-    if (plan.group || (!plan.balanced && plan.splits <= 1)) return 0;
+    if (plan.group || (!plan.flat && plan.splits <= 1)) return 0;
     // partial O (rows of the MFMA head dim) + (m, l) per partial row, then the merge
     // descriptors
     const int d = decode_mfma_dim(head_dim);

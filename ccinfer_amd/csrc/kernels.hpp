@@ -15,28 +15,27 @@ hipError_t write_kv_cache(const void* k_new, const void* v_new, void* k_cache, v
                           int head_dim, int max_slots, hipStream_t stream);
 
 // ---- decode ---------------------------------------------------------------
-// Split-KV plan: `splits` partitions of `split_tokens` tokens per (request, kv_head).
 // Split-KV plan. Fixed mode: `splits` partitions of `split_tokens` tokens per (request,
-// kv_head), sized from the longest possible context. Balanced mode (decode batches of 4 to
-// kBalancedMaxItems requests): the flat plan -- on the device, the batch's 32-token chunks
+// kv_head), sized from the longest possible context. Flat mode (decode batches of 4 to
+// kFlatMaxItems requests): the flat plan -- on the device, the batch's 32-token chunks
 // laid end to end are cut into wave_target equal ranges per kv_head, one per wavefront,
 // across request boundaries, so every wavefront streams the same number of tokens whatever
 // the spread of context lengths; `slots` bounds the number of splits per kv_head.
 struct DecodePlan {
     int splits = 1;
     int split_tokens = 0;  // multiple of 32
-    bool balanced = false;
+    bool flat = false;  // the on-device flat plan (equal chunk ranges across items)
     int slots = 0;
     int wave_target = 0;
     bool group = false;  // one workgroup per (item, kv_head), parts merged in LDS
 };
 
-constexpr int kBalancedMaxItems = 256;
+constexpr int kFlatMaxItems = 256;
 
-// Returns the plan for a batch whose longest context is max_ctx tokens. allow_balanced: the
-// balanced mode may be used (it resolves items through DecodeItems like the kernel does).
+// Returns the plan for a batch whose longest context is max_ctx tokens. allow_flat: the
+// flat mode may be used (it resolves items through DecodeItems like the kernel does).
 DecodePlan plan_decode(int num_items, int num_q_heads, int num_kv_heads, int max_ctx,
-                       bool allow_balanced);
+                       bool allow_flat);
 
 // The plan for the single-token items of a prefill batch (at most num_items of them).
 DecodePlan plan_decode_items(int num_items, int num_q_heads, int num_kv_heads, int max_ctx);
