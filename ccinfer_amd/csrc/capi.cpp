@@ -13,6 +13,7 @@
 
 #include <climits>
 #include <cstring>
+#include <algorithm>
 #include <cstdint>
 
 #include "ccinfer_attn.h"
@@ -240,10 +241,16 @@ size_t ccinfer_decode_workspace_size(int batch_size, int max_blocks_per_req, int
                          cache_block_size))
         return 0;
     if (!decode_fast_supported(num_q_heads, num_kv_heads, head_dim, cache_block_size)) return 0;
-    const DecodePlan plan =
-        plan_decode(batch_size, num_q_heads, num_kv_heads,
-                    max_blocks_per_req * cache_block_size, true);
-    return decode_workspace_bytes(batch_size, num_q_heads, head_dim, plan);
+    // One size serves ccinfer_decode_attention and ccinfer_decode_attention_fp8, whose flat
+    // plans differ in wavefront count.
+    size_t bytes = 0;
+    for (const bool fp8 : {false, true}) {
+        const DecodePlan plan =
+            plan_decode(batch_size, num_q_heads, num_kv_heads,
+                        max_blocks_per_req * cache_block_size, true, fp8);
+        bytes = std::max(bytes, decode_workspace_bytes(batch_size, num_q_heads, head_dim, plan));
+    }
+    return bytes;
 }
 
 namespace {
@@ -266,7 +273,10 @@ int decode_entry(const void* q, const void* k_cache, const void* v_cache,
     if (fast) {
         plan = plan_decode(batch_size, num_q_heads, num_kv_heads,
                            max_blocks_per_req * cache_block_size, true);
-        const size_t need = decode_workspace_bytes(batch_size, num_q_heads, head_dim, plan);
+        // the size the query returns (it covers the fp8 entry's plan too)
+        const size_t need = ccinfer_decode_workspace_size(batch_size, max_blocks_per_req,
+                                                          num_q_heads, num_kv_heads, head_dim,
+                                                          cache_block_size);
         if (need > 0 && (workspace == nullptr || workspace_bytes < need))
             return CCINFER_ERR_INVALID_ARGUMENT;
     }
@@ -362,8 +372,10 @@ int ccinfer_decode_attention_fp8(const void* q, const void* k_cache, const void*
         return CCINFER_ERR_INVALID_ARGUMENT;
     const DecodePlan plan =
         plan_decode(batch_size, num_q_heads, num_kv_heads,
-                    max_blocks_per_req * cache_block_size, true);
-    const size_t need = decode_workspace_bytes(batch_size, num_q_heads, head_dim, plan);
+                    max_blocks_per_req * cache_block_size, true, true);
+    const size_t need = ccinfer_decode_workspace_size(batch_size, max_blocks_per_req,
+                                                      num_q_heads, num_kv_heads, head_dim,
+                                                      cache_block_size);
     if (need > 0 && (workspace == nullptr || workspace_bytes < need))
         return CCINFER_ERR_INVALID_ARGUMENT;
     DecodeItems items;

@@ -63,6 +63,10 @@ constexpr int kMaxSplitTokens = 2048;  // 128 blocks: two table entries per lane
 // of 1-3 requests -- run fastest with kEvenWaves, one 4-wavefront workgroup per CU.
 constexpr int64_t kTargetWaves = 4096;
 constexpr int64_t kEvenWaves = 1024;
+// The fp8 cache's flat plan: twice the wavefronts (half the bytes per chunk, the same
+// conversion and MFMA work): configs[1]'s batch 61.2 -> 56.0 us against kEvenWaves, while
+// bf16 runs 96.3 us at kEvenWaves and 98.3 at twice that.
+constexpr int64_t kEvenWavesFp8 = 2048;
 constexpr int kFlatMinItems = 4;
 // The group plan (one workgroup per (request, kv_head), parts merged in LDS) streams a row
 // from one CU, which reads ~30 GB/s; it pays off only where the row is short enough that
@@ -1051,7 +1055,7 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
 }  // namespace
 
 DecodePlan plan_decode(int num_items, int num_q_heads, int num_kv_heads, int max_ctx,
-                       bool allow_flat) {
+                       bool allow_flat, bool fp8) {
     // Query groups above one MFMA N-tile run as several virtual kv heads (launch_decode).
     num_kv_heads *= decode_head_rep(num_q_heads / num_kv_heads);
     DecodePlan p;
@@ -1072,7 +1076,8 @@ DecodePlan plan_decode(int num_items, int num_q_heads, int num_kv_heads, int max
         // One workgroup per CU, and at least one range per request and kv head (many short
         // rows would otherwise crowd several segments into each range).
         p.wave_target = static_cast<int>(std::max<int64_t>(
-            std::max<int64_t>(1, kEvenWaves / num_kv_heads), num_items));
+            std::max<int64_t>(1, (fp8 ? kEvenWavesFp8 : kEvenWaves) / num_kv_heads),
+            num_items));
         // Splits per kv_head: one per range plus one per row boundary inside a range, so at
         // most C/T + B with T >= C/W (or, with T at its cap, B * chunks / cap + B), and
         // never more than one per chunk.
@@ -1114,7 +1119,8 @@ int decode_mfma_dim(int head_dim) {
     return head_dim <= 256 && head_dim % 16 == 0 ? 256 : 0;
 }
 
-DecodePlan plan_decode_items(int num_items, int num_q_heads, int num_kv_heads, int max_ctx) {
+DecodePlan plan_decode_items(int num_items, int num_q_heads, int num_kv_heads, int max_ctx,
+                             bool fp8) {
     // The decode items of a prefill batch: their count is known on the device only, and is
     // often zero (a pure prompt batch). One launch of one workgroup per possible (item,
     // kv_head) costs far less than the split plan's two launches, each of which dispatches a
@@ -1127,7 +1133,7 @@ DecodePlan plan_decode_items(int num_items, int num_q_heads, int num_kv_heads, i
         p.group = true;
         return p;
     }
-    return plan_decode(num_items, num_q_heads, num_kv_heads, max_ctx, true);
+    return plan_decode(num_items, num_q_heads, num_kv_heads, max_ctx, true, fp8);
 }
 
 size_t decode_workspace_bytes(int num_items, int num_q_heads, int head_dim,

@@ -1354,14 +1354,15 @@ int tile_tokens_for(int head_dim, int G) {
 }
 
 PrefillLayout prefill_layout(int batch_size, int total_query_tokens, int max_blocks_per_req,
-                             int num_q_heads, int num_kv_heads, int head_dim, int block_size) {
+                             int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                             bool fp8) {
     PrefillLayout L{};
     const int G = num_q_heads / num_kv_heads;
     const int D = decode_mfma_dim(head_dim);  // the kernels' (padded) head dim
     L.tile_tokens = tile_tokens_for(D, G);
     L.max_tiles = total_query_tokens / L.tile_tokens + batch_size;
     L.plan = plan_decode_items(batch_size, num_q_heads, num_kv_heads,
-                               max_blocks_per_req * block_size);
+                               max_blocks_per_req * block_size, fp8);
     size_t off = 0;
     L.counts_off = off;
     off = align256(off + 2 * sizeof(int32_t));
@@ -1433,9 +1434,13 @@ bool prefill_fp8_supported(int head_dim, int max_blocks_per_req) {
 size_t prefill_workspace_bytes(int batch_size, int total_query_tokens, int max_blocks_per_req,
                                int num_q_heads, int num_kv_heads, int head_dim,
                                int block_size) {
-    return prefill_layout(batch_size, total_query_tokens, max_blocks_per_req, num_q_heads,
-                          num_kv_heads, head_dim, block_size)
-        .total;
+    // One size serves the bf16 and the fp8 prefill, whose decode-item plans differ.
+    return std::max(prefill_layout(batch_size, total_query_tokens, max_blocks_per_req,
+                                   num_q_heads, num_kv_heads, head_dim, block_size, false)
+                        .total,
+                    prefill_layout(batch_size, total_query_tokens, max_blocks_per_req,
+                                   num_q_heads, num_kv_heads, head_dim, block_size, true)
+                        .total);
 }
 
 namespace {
@@ -1459,7 +1464,7 @@ hipError_t prefill_impl(const void* q, const void* k_cache, const void* v_cache,
                         int block_size, void* workspace, hipStream_t stream,
                         const PrefillOverlap* overlap) {
     const PrefillLayout L = prefill_layout(batch_size, total_query_tokens, max_blocks_per_req,
-                                           num_q_heads, num_kv_heads, head_dim, block_size);
+                                           num_q_heads, num_kv_heads, head_dim, block_size, F8);
     char* ws = static_cast<char*>(workspace);
     int32_t* counts = reinterpret_cast<int32_t*>(ws + L.counts_off);
     TileEntry* tiles = reinterpret_cast<TileEntry*>(ws + L.tiles_off);
