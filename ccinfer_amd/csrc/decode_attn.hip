@@ -68,6 +68,9 @@ constexpr int64_t kEvenWaves = 1024;
 // bf16 runs 96.3 us at kEvenWaves and 98.3 at twice that.
 constexpr int64_t kEvenWavesFp8 = 2048;
 constexpr int kFlatMinItems = 4;
+// Flat launches of at least this many wavefronts (two rounds at the split kernel's two waves
+// per SIMD) snap their ranges to request boundaries (decode_flat_index_kernel).
+constexpr int kSnapWaves = 4096;
 // The group plan (one workgroup per (request, kv_head), parts merged in LDS) streams a row
 // from one CU, which reads ~30 GB/s; it pays off only where the row is short enough that
 // one launch beats the split plan's two. Measured (one MI355X, 16q/8kv or 32q/8kv, d=128):
@@ -169,6 +172,12 @@ __device__ __forceinline__ int wave_inclusive_scan(int v, int lane) {
     return v;
 }
 
+__device__ __forceinline__ int wave_max_int(int v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = max(v, __shfl_xor(v, off));
+    return v;
+}
+
 __device__ __forceinline__ int wave_sum_i32(int v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
@@ -196,7 +205,7 @@ struct FlatSegment {
 
 // The k-th segment of wavefront w's range. Returns false past the last one. *invalid_w:
 // whether request w's context is invalid (then no range holds a chunk of it).
-__device__ bool flat_segment(const int32_t* __restrict__ context_lens, const ItemArgs& items,
+__device__ __forceinline__ bool flat_segment(const int32_t* __restrict__ context_lens, const ItemArgs& items,
                              int mbpr, int W, int w, int k, int lane, FlatSegment* out,
                              bool* invalid_w) {
     int B = items.num_items;
@@ -261,6 +270,230 @@ __device__ bool flat_segment(const int32_t* __restrict__ context_lens, const Ite
         found += n;
         carry_p = __builtin_amdgcn_readlane(p + c, 63);
         carry_s = __builtin_amdgcn_readlane(sr + nsr, 63);
+    }
+    return false;
+}
+
+// ---- the flat plan's index: batches past kFlatMaxItems requests, and snapped ranges ----
+// Scanning every request in every wavefront gets costly for large batches, so one
+// 1024-thread workgroup (decode_flat_index_kernel, launched just before the split kernel)
+// writes the plan once:
+//   idx[0] = T, idx[1] = C,
+//   P[0..B]       chunk offset of each request (P[B] = C),
+//   S[0..B]       first partial slot of each request (S[B] = total splits),
+//   V[0..B)       the first range that holds a chunk of the request,
+//   L[0..slots]   the first chunk of each range (L[slots] = C),
+//   F[0..slots)   the request holding chunk L[w].
+// Range w is the chunks [L[w], L[w+1]). Unsnapped, L[w] = min(w * T, C) as in flat_segment.
+// Snapped, a range start that lies within min(T / 2, (kMaxSplitTokens / kChunk - T) / 2)
+// chunks of a request boundary moves to the nearer boundary: a request of about T chunks
+// then runs whole in one wavefront instead of two segments of two wavefronts (one pipeline
+// start, one partial write and a merge saved), and no range outgrows a split. Launches of many rounds of wavefronts snap: the
+// dispatcher evens out the longer ranges there, and the split rows cost more than they save.
+__device__ __forceinline__ int items_live(const ItemArgs& items) {
+    int B = items.num_items;
+    if (items.item_count != nullptr) B = min(B, *items.item_count);
+    return B;
+}
+
+__device__ __forceinline__ int item_chunks(const int32_t* __restrict__ context_lens,
+                                           const ItemArgs& items, int mbpr, int r, int* ectx) {
+    const int req = items.item_req != nullptr ? items.item_req[r] : r;
+    const int ctx = effective_ctx(context_lens[req], mbpr, items.zero_invalid);
+    *ectx = ctx;
+    return ctx > 0 ? (ctx + kChunk - 1) / kChunk : 0;
+}
+
+// Exclusive prefix sum of v over the 1024 threads of the block (s_part: 16 ints of LDS);
+// *total receives the sum of all. Every thread must call it.
+__device__ int block_exclusive_scan_1024(int v, int* s_part, int* total) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int incl = wave_inclusive_scan(v, lane);
+    if (lane == 63) s_part[wave] = incl;
+    __syncthreads();
+    int base = 0, all = 0;
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+        const int t = s_part[x];
+        base += x < wave ? t : 0;
+        all += t;
+    }
+    __syncthreads();
+    *total = all;
+    return base + incl - v;
+}
+
+struct FlatIndex {
+    int32_t *P, *S, *V, *L, *F;
+};
+
+__device__ __forceinline__ FlatIndex flat_index_arrays(int32_t* idx, int num_items, int slots) {
+    FlatIndex x;
+    x.P = idx + 2;
+    x.S = x.P + num_items + 1;
+    x.V = x.S + num_items + 1;
+    x.L = x.V + num_items;
+    x.F = x.L + slots + 1;
+    return x;
+}
+
+// The last range starting at or before chunk c (c < C). L[w] lies within T / 2 of w * T, so
+// the search starts just above c / T and steps down at most a few ranges.
+__device__ __forceinline__ int range_of(const int32_t* L, int c, int T, int slots) {
+    int w = min(slots, (c + T) / T);
+    while (L[w] > c) --w;
+    return w;
+}
+
+__global__ __launch_bounds__(1024) void decode_flat_index_kernel(
+    const int32_t* __restrict__ context_lens, ItemArgs items, int mbpr, int W, int slots,
+    int snap, int resident, int32_t* __restrict__ idx) {
+    __shared__ int s_part[16];
+    __shared__ int s_max[16];
+    constexpr int kMaxT = kMaxSplitTokens / kChunk;
+    const int B = items_live(items);
+    const FlatIndex x = flat_index_arrays(idx, items.num_items, slots);
+    const int per = (B + 1023) / 1024;
+    const int lo = static_cast<int>(threadIdx.x) * per;
+    const int hi = min(B, lo + per);
+    int e;
+    int sum = 0, cmax = 0;
+    for (int r = lo; r < hi; ++r) {
+        const int c = item_chunks(context_lens, items, mbpr, r, &e);
+        sum += c;
+        cmax = max(cmax, c);
+    }
+    cmax = wave_max_int(cmax);
+    if ((threadIdx.x & 63) == 0) s_max[threadIdx.x >> 6] = cmax;
+    int C;
+    int run = block_exclusive_scan_1024(sum, s_part, &C);  // its barriers publish s_max
+#pragma unroll
+    for (int v = 0; v < 16; ++v) cmax = max(cmax, s_max[v]);
+    int T = (C + W - 1) / W;
+    T = T < 1 ? 1 : (T > kMaxT ? kMaxT : T);
+    // Whole rows: the longest request holds at most half of one resident wavefront's share of
+    // the launch, so one range per request (pieces of at most kMaxT chunks) leaves no tail
+    // worth balancing, and no request is cut into two segments.
+    const bool rows = snap && 2 * static_cast<int64_t>(cmax) * resident <= C;
+    if (rows) {
+        int npieces = 0;
+        for (int r = lo; r < hi; ++r) {
+            const int c = item_chunks(context_lens, items, mbpr, r, &e);
+            npieces += (c + kMaxT - 1) / kMaxT;
+        }
+        int NS;
+        int srun = block_exclusive_scan_1024(npieces, s_part, &NS);
+        for (int r = lo; r < hi; ++r) {
+            const int c = item_chunks(context_lens, items, mbpr, r, &e);
+            const int ns = (c + kMaxT - 1) / kMaxT;
+            const int len = ns > 0 ? (c + ns - 1) / ns : 0;
+            x.P[r] = run;
+            x.S[r] = srun;
+            x.V[r] = srun;
+            for (int k = 0; k < ns && srun + k < slots; ++k) {
+                x.L[srun + k] = run + k * len;
+                x.F[srun + k] = r;
+            }
+            run += c;
+            srun += ns;
+        }
+        for (int w = NS + static_cast<int>(threadIdx.x); w <= slots; w += 1024) x.L[w] = C;
+        if (threadIdx.x == 0) {
+            idx[0] = T;
+            idx[1] = C;
+            x.P[B] = C;
+            x.S[B] = NS;
+        }
+        return;
+    }
+    // Range starts: every grid point w * T < C lies in exactly one non-empty request. A start
+    // moves by at most `slack` chunks, so a range holds at most T + 2 * slack chunks, within
+    // the split kernel's table load.
+    const int slack = snap ? min(T / 2, (kMaxT - T) / 2) : -1;
+    for (int r = lo; r < hi; ++r) {
+        const int c = item_chunks(context_lens, items, mbpr, r, &e);
+        x.P[r] = run;
+        for (int w = (run + T - 1) / T; w * T < run + c && w < slots; ++w) {
+            const int dl = w * T - run, dr = run + c - w * T;
+            int start = w * T, req = r;
+            if (dl <= slack && dl <= dr) {
+                start = run;
+            } else if (dr <= slack) {
+                start = run + c;
+                req = r + 1;
+            }
+            x.L[w] = start;
+            x.F[w] = req;
+        }
+        run += c;
+    }
+    for (int w = (C + T - 1) / T + static_cast<int>(threadIdx.x); w <= slots; w += 1024)
+        x.L[w] = C;
+    if (threadIdx.x == 0) x.P[B] = C;
+    __syncthreads();  // L is complete (workgroup-scope visibility of the global writes)
+    // Splits of each request: the ranges from the one holding its first chunk to the one
+    // holding its last (a snapped range that starts and ends on one boundary is empty and
+    // never the last range at or before a chunk).
+    int nsum = 0;
+    for (int r = lo; r < hi; ++r) {
+        const int p = x.P[r], q = x.P[r + 1];
+        if (q > p) {
+            const int v = range_of(x.L, p, T, slots);
+            x.V[r] = v;
+            nsum += range_of(x.L, q - 1, T, slots) - v + 1;
+        }
+    }
+    int NS;
+    int srun = block_exclusive_scan_1024(nsum, s_part, &NS);
+    for (int r = lo; r < hi; ++r) {
+        const int p = x.P[r], q = x.P[r + 1];
+        x.S[r] = srun;
+        if (q > p) srun += range_of(x.L, q - 1, T, slots) - x.V[r] + 1;
+    }
+    if (threadIdx.x == 0) {
+        idx[0] = T;
+        idx[1] = C;
+        x.S[B] = NS;
+    }
+}
+
+// flat_segment from the index: the k-th request with chunks in range w.
+__device__ __forceinline__ bool flat_segment_indexed(const int32_t* __restrict__ idx,
+                                                     const int32_t* __restrict__ context_lens,
+                                                     const ItemArgs& items, int mbpr,
+                                                     int slots, int w, int k, FlatSegment* out,
+                                                     bool* invalid_w) {
+    const int B = __builtin_amdgcn_readfirstlane(items_live(items));
+    const FlatIndex x = flat_index_arrays(const_cast<int32_t*>(idx), items.num_items, slots);
+    *invalid_w = false;
+    if (w < B) {
+        int e;
+        item_chunks(context_lens, items, mbpr, w, &e);
+        *invalid_w = __builtin_amdgcn_readfirstlane(e) < 0;
+    }
+    const int lo = __builtin_amdgcn_readfirstlane(x.L[w]);
+    const int hi = __builtin_amdgcn_readfirstlane(x.L[w + 1]);
+    if (lo >= hi) return false;
+    int found = 0;
+    for (int r = __builtin_amdgcn_readfirstlane(x.F[w]); r < B; ++r) {
+        const int p = __builtin_amdgcn_readfirstlane(x.P[r]);
+        if (p >= hi) break;
+        const int c = __builtin_amdgcn_readfirstlane(x.P[r + 1]) - p;
+        if (c == 0) continue;
+        if (found++ < k) continue;
+        int e;
+        item_chunks(context_lens, items, mbpr, r, &e);
+        const int s0 = __builtin_amdgcn_readfirstlane(x.S[r]);
+        out->req = r;
+        out->ctx = __builtin_amdgcn_readfirstlane(e);
+        out->nsplit = __builtin_amdgcn_readfirstlane(x.S[r + 1]) - s0;
+        out->first_slot = s0;
+        out->split = w - __builtin_amdgcn_readfirstlane(x.V[r]);
+        out->begin = (max(lo, p) - p) * kChunk;
+        out->end = min(out->ctx, (min(hi, p + c) - p) * kChunk);
+        out->more = p + c < hi;
+        return true;
     }
     return false;
 }
@@ -695,7 +928,7 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     const int32_t* __restrict__ context_lens, __bf16* __restrict__ out, float* __restrict__ ws_o,
     float* __restrict__ ws_ml, MergeDesc* __restrict__ desc, ItemArgs items, int mbpr, int hq,
     int hkv, int splits, int split_tokens, int flat_w, int slots, float scale_log2, int dr,
-    int rep) {
+    int rep, const int32_t* __restrict__ flat_idx) {
     const int ds = kPad ? dr : D;  // q / output row stride
     constexpr int NV = DecodeShape<D>::kNV;
     using Cache = std::conditional_t<F8, uint8_t, __bf16>;
@@ -810,7 +1043,14 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
         const int W = flat_w;
         FlatSegment fs;
         bool invalid_w = false;
-        bool ok = flat_segment(context_lens, items, mbpr, W, rest, 0, lane, &fs, &invalid_w);
+        auto segment = [&](int k) __attribute__((always_inline)) {
+            return flat_idx != nullptr
+                       ? flat_segment_indexed(flat_idx, context_lens, items, mbpr, slots, rest, k,
+                                              &fs, &invalid_w)
+                       : flat_segment(context_lens, items, mbpr, W, rest, k, lane, &fs,
+                                      &invalid_w);
+        };
+        bool ok = segment(0);
         if (invalid_w) process(lane, rest, 0, 0, 0, -1, 0, 0);
         for (int k = 1; ok; ++k) {
             int lane_k = lane;
@@ -818,7 +1058,7 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
             process(lane_k, fs.req, fs.split, fs.nsplit, fs.first_slot, fs.ctx, fs.begin,
                     fs.end);
             if (!fs.more) break;
-            ok = flat_segment(context_lens, items, mbpr, W, rest, k, lane, &fs, &invalid_w);
+            ok = segment(k);
         }
         return;
     }
@@ -967,6 +1207,7 @@ struct DecodeWs {
     float* o;
     float* ml;
     MergeDesc* desc;
+    int32_t* index;  // the flat plan's index (batches past kFlatMaxItems)
 };
 
 // Partial rows of the plan: (item, q_head, split) in fixed mode, (q_head, slot) flat.
@@ -980,12 +1221,25 @@ size_t desc_offset(size_t rows, int d) {
     return (rows * (d + 2) * sizeof(float) + 15) & ~static_cast<size_t>(15);
 }
 
-DecodeWs carve(void* workspace, size_t rows, int d) {
+// The flat plan's index follows the merge descriptors: T, C, P[B + 1], S[B + 1], F[slots].
+size_t index_offset(size_t rows, int d, int num_items, int hq) {
+    return (desc_offset(rows, d) + static_cast<size_t>(num_items) * hq * sizeof(MergeDesc) +
+            15) & ~static_cast<size_t>(15);
+}
+
+size_t index_bytes(int num_items, int slots) {
+    // T, C, P[B + 1], S[B + 1], V[B], L[slots + 1], F[slots]
+    return (2 + 3 * static_cast<size_t>(num_items) + 2 + 2 * static_cast<size_t>(slots) + 1) *
+           sizeof(int32_t);
+}
+
+DecodeWs carve(void* workspace, size_t rows, int d, int num_items, int hq) {
     DecodeWs w{};
     char* p = static_cast<char*>(workspace);
     w.o = reinterpret_cast<float*>(p);
     w.ml = reinterpret_cast<float*>(p + rows * d * sizeof(float));
     w.desc = reinterpret_cast<MergeDesc*>(p + desc_offset(rows, d));
+    w.index = reinterpret_cast<int32_t*>(p + index_offset(rows, d, num_items, hq));
     return w;
 }
 
@@ -997,6 +1251,13 @@ int decode_head_rep(int G) {
 }
 
 // dr: the head dim of q / cache / output rows (dr == D unless kPad).
+// Split-kernel wavefronts resident on the chip at once: 256 CUs x 4 SIMDs x the waves per
+// SIMD its registers allow (about 156 / 217 / 430 VGPRs at head dims 64 / 128 / 256).
+template <int D>
+constexpr int resident_waves() {
+    return 1024 * (D <= 64 ? 3 : D <= 128 ? 2 : 1);
+}
+
 template <int D, bool F8, bool kPad>
 hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache,
                          const float* k_scale, const float* v_scale,
@@ -1031,13 +1292,21 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
     const int grid = static_cast<int>((waves + kWavesPerGroup - 1) / kWavesPerGroup);
     const bool merge = plan.flat || plan.splits > 1;
     DecodeWs w{};
-    if (merge) w = carve(workspace, partial_rows(it.num_items, hq, plan), D);
+    if (merge) w = carve(workspace, partial_rows(it.num_items, hq, plan), D, it.num_items, hq);
+    if (plan.flat_index) {
+        decode_flat_index_kernel<<<1, 1024, 0, stream>>>(context_lens, it, mbpr, plan.wave_target,
+                                                         plan.slots, plan.flat_snap ? 1 : 0,
+                                                         resident_waves<D>() / hkv, w.index);
+        const hipError_t ie = hipGetLastError();
+        if (ie != hipSuccess) return ie;
+    }
     const int bw = plan.flat ? plan.wave_target : 0;
     auto go = [&](auto tl_tag) {
         decode_split_kernel<D, F8, kPad, decltype(tl_tag)::value><<<grid, 256, 0, stream>>>(
             static_cast<const __bf16*>(q), k_cache, v_cache, k_scale, v_scale, block_table,
             context_lens, static_cast<__bf16*>(output), w.o, w.ml, w.desc, it, mbpr, hq, hkv,
-            plan.splits, plan.split_tokens, bw, plan.slots, scale_log2, dr, rep);
+            plan.splits, plan.split_tokens, bw, plan.slots, scale_log2, dr, rep,
+            plan.flat_index ? w.index : nullptr);
     };
     if (tl)
         go(std::true_type{});
@@ -1070,14 +1339,15 @@ DecodePlan plan_decode(int num_items, int num_q_heads, int num_kv_heads, int max
     constexpr int kMaxChunksPerSplit = kMaxSplitTokens / kChunk;
     // Small batches keep the fixed plan: their splits are already even and the on-device
     // plan would only add its lookup to a latency-bound launch.
-    if (allow_flat && num_items >= kFlatMinItems &&
-        num_items <= kFlatMaxItems && chunks > 1) {
+    if (allow_flat && num_items >= kFlatMinItems && chunks > 1) {
         p.flat = true;
         // One workgroup per CU, and at least one range per request and kv head (many short
         // rows would otherwise crowd several segments into each range).
         p.wave_target = static_cast<int>(std::max<int64_t>(
             std::max<int64_t>(1, (fp8 ? kEvenWavesFp8 : kEvenWaves) / num_kv_heads),
             num_items));
+        p.flat_snap = static_cast<int64_t>(p.wave_target) * num_kv_heads >= kSnapWaves;
+        p.flat_index = num_items > kFlatMaxItems || p.flat_snap;
         // Splits per kv_head: one per range plus one per row boundary inside a range, so at
         // most C/T + B with T >= C/W (or, with T at its cap, B * chunks / cap + B), and
         // never more than one per chunk.
@@ -1142,7 +1412,11 @@ size_t decode_workspace_bytes(int num_items, int num_q_heads, int head_dim,
     // partial O (rows of the MFMA head dim) + (m, l) per partial row, then the merge
     // descriptors
     const int d = decode_mfma_dim(head_dim);
-    return desc_offset(partial_rows(num_items, num_q_heads, plan), d) +
+    const size_t rows = partial_rows(num_items, num_q_heads, plan);
+    if (plan.flat_index)
+        return index_offset(rows, d, num_items, num_q_heads) +
+               index_bytes(num_items, plan.slots);
+    return desc_offset(rows, d) +
            static_cast<size_t>(num_items) * num_q_heads * sizeof(MergeDesc);
 }
 

@@ -28,8 +28,11 @@ struct DecodePlan {
     int slots = 0;
     int wave_target = 0;
     bool group = false;  // one workgroup per (item, kv_head), parts merged in LDS
+    bool flat_index = false;  // flat plan for > kFlatMaxItems items: an index kernel first
+    bool flat_snap = false;   // the index snaps range starts to request boundaries
 };
 
+// Requests the flat plan's in-kernel scan covers; larger batches get the index kernel.
 constexpr int kFlatMaxItems = 256;
 
 // Returns the plan for a batch whose longest context is max_ctx tokens. allow_flat: the

@@ -105,8 +105,8 @@ def test_decode_workspace_size(lib):
     n = f(32, 2048, 32, 8, 128, 16) - 32 * 32 * 16
     assert n > 0 and n % (32 * 130 * 4) == 0      # Hq * partial slots * (D + 2) floats
     assert n <= 32 * 32 * 2048 * 130 * 4          # never more than one slot per 32 tokens
-    big = f(300, 2048, 32, 8, 128, 16) - 300 * 32 * 16  # past the balanced-plan batch limit
-    assert big > 0 and big % (300 * 32 * 130 * 4) == 0  # B * Hq * splits * (D + 2) floats
+    big = f(300, 2048, 32, 8, 128, 16) - 300 * 32 * 16  # flat plan with its index kernel
+    assert big >= 300 * 32 * 130 * 4                    # at least one partial slot per row
     # head_dim 80 runs the MFMA kernels at 128 with zero padding: partial rows of 128 floats
     assert f(32, 2048, 32, 8, 80, 16) == f(32, 2048, 32, 8, 128, 16)
     assert f(32, 2048, 32, 8, 72, 16) == 0        # not a decode head dim: invalid shape

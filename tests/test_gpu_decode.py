@@ -313,3 +313,102 @@ def test_fused_kv_write_skips_rows_without_a_slot(gpu):
         else:
             assert torch.equal(got, want), variant
 
+
+
+@pytest.mark.parametrize("batch,lo,hi,hq,hkv,seed", [
+    (300, 100, 3000, 32, 8, 61),     # index, equal ranges
+    (257, 4000, 4096, 32, 8, 63),    # index, equal ranges, long rows
+    (1000, 1, 700, 32, 8, 62),       # index, snapped ranges (8000 wavefronts)
+    (600, 100, 3000, 32, 8, 64),     # snapped, rows from under T to several T
+    (200, 100, 3000, 32, 32, 65),    # snapped below the index's request limit
+])
+def test_flat_plan_index_for_large_batches(gpu, batch, lo, hi, hq, hkv, seed):
+    """The flat plan's index kernel (more than 256 requests, or launches of many rounds of
+    wavefronts, whose range starts snap to request boundaries): it writes the chunk and split
+    prefixes and the range starts, and each wavefront walks its segments from them. Holes in
+    the table, invalid contexts (0, longer than the table row) and every unused cache slot
+    poisoned (NaN K, Inf V); every row against the oracle, and the fused KV write bit-equal
+    to write + decode."""
+    from ccinfer_amd import decode_attention_write_kv
+    say(f"flat plan index: B={batch} ctx=[{lo},{hi}] hq={hq} hkv={hkv}")
+    w = W.decode_batched(device=gpu, seed=seed, batch=batch, ctx_lo=lo, ctx_hi=hi, hq=hq,
+                         hkv=hkv, with_write=True)
+    rng = np.random.default_rng(seed)
+    ctx = w.context_lens.copy()
+    bt = w.block_table.copy()
+    ctx[3] = 0                                   # invalid: zeros
+    ctx[7] = w.mbpr * 16 + 17                    # longer than the table row: zeros
+    for b in range(10, batch, 37):
+        nb = int(np.count_nonzero(bt[b] >= 0))
+        if nb > 2:
+            bt[b, int(rng.integers(0, nb - 1))] = -1   # a hole, never the last block
+    w.context_lens = ctx
+    w.block_table = bt
+    w.slot_mapping = w.slot_mapping.copy()
+    w.slot_mapping[[3, 7]] = -1                  # invalid rows have no new-token slot
+    meta = w.device_meta(gpu)
+    kc, vc = w.k_cache.clone(), w.v_cache.clone()
+    write_kv_cache(w.k_new, w.v_new, kc, vc, meta["slot_mapping"])
+    want = decode_attention(w.q, kc, vc, meta["block_table"], meta["context_lens"])
+    got = decode_attention_write_kv(w.q, w.k_new, w.v_new, w.k_cache, w.v_cache,
+                                    meta["block_table"], meta["context_lens"])
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert torch.equal(w.k_cache, kc) and torch.equal(w.v_cache, vc)
+    used = np.zeros(w.num_blocks * 16, bool)
+    for b in range(batch):
+        n = min(int(ctx[b]), w.mbpr * 16)
+        if n <= 0 or (n + 15) // 16 > w.mbpr:
+            continue
+        pos = np.arange(n)
+        blk = bt[b, pos // 16]
+        ok = blk >= 0
+        used[blk[ok] * 16 + pos[ok] % 16] = True
+    rows = torch.from_numpy(np.nonzero(~used)[0]).to(gpu)
+    w.k_cache[rows] = float("nan")
+    w.v_cache[rows] = float("inf")
+    out = run_decode(w, gpu)
+    res = f32(out)
+    assert np.all(res[3] == 0) and np.all(res[7] == 0)
+    assert_attn_close(res, oracle_decode(w), f"B={batch}")
+
+
+def test_flat_plan_snapped_fp8(gpu):
+    """fp8 cache through the snapped index (600 requests, 4800 wavefronts), unused slots
+    holding the E4M3 NaN code, against the oracle's fp8 decode."""
+    from ccinfer_amd import decode_attention_fp8
+    from tests.test_gpu_fp8 import quantised_cache
+    from tests.test_gpu_random_shapes import _unused_rows
+    say("flat plan snapped fp8: B=600 ctx=[100,3000]")
+    w = W.decode_batched(device=gpu, seed=66, batch=600, ctx_lo=100, ctx_hi=3000,
+                         with_write=False)
+    kc, vc, ks, vs = quantised_cache(gpu, w, w.hkv, w.d)
+    rows = _unused_rows(w, gpu)
+    kc[rows] = 0x7F
+    vc[rows] = 0x7F
+    meta = w.device_meta(gpu)
+    got = decode_attention_fp8(w.q, kc, vc, ks, vs, meta["block_table"], meta["context_lens"])
+    torch.cuda.synchronize()
+    ref = oracle.decode_fp8(u16(w.q), kc.cpu().numpy(), vc.cpu().numpy(), ks.cpu().numpy(),
+                            vs.cpu().numpy(), w.block_table, w.context_lens)
+    assert_attn_close(f32(got), ref, "fp8 B=600")
+
+
+@pytest.mark.parametrize("batch,lo,hi,hq,hkv,seed", [
+    (2048, 100, 1000, 8, 8, 67),     # one range per request
+    (2500, 2100, 2200, 4, 2, 68),    # requests of 34-35 chunks: two pieces each
+])
+def test_flat_plan_whole_rows(gpu, batch, lo, hi, hq, hkv, seed):
+    """Launches whose longest request is short next to one resident wavefront's share: the
+    index kernel gives each request its own ranges (pieces of at most 32 chunks) instead of
+    equal ranges across requests. Every output finite and a sample of rows against the
+    oracle."""
+    say(f"flat plan whole rows: B={batch} ctx=[{lo},{hi}] hq={hq} hkv={hkv}")
+    w = W.decode_batched(device=gpu, seed=seed, batch=batch, ctx_lo=lo, ctx_hi=hi, hq=hq,
+                         hkv=hkv, with_write=False)
+    res = f32(run_decode(w, gpu))
+    assert np.all(np.isfinite(res))
+    rows = np.r_[0:64, 64:batch:23, batch - 5:batch]
+    ref = oracle.decode(u16(w.q)[rows], u16(w.k_cache), u16(w.v_cache), w.block_table[rows],
+                        w.context_lens[rows])
+    assert_attn_close(res[rows], ref, f"B={batch}")
