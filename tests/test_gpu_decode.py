@@ -396,11 +396,11 @@ def test_flat_plan_snapped_fp8(gpu):
 
 @pytest.mark.parametrize("batch,lo,hi,hq,hkv,seed", [
     (2048, 100, 1000, 8, 8, 67),     # one range per request
-    (2500, 2100, 2200, 4, 2, 68),    # requests of 34-35 chunks: two pieces each
+    (2500, 2100, 2200, 4, 2, 68),    # requests of 66-69 chunks: two pieces each
 ])
 def test_flat_plan_whole_rows(gpu, batch, lo, hi, hq, hkv, seed):
     """Launches whose longest request is short next to one resident wavefront's share: the
-    index kernel gives each request its own ranges (pieces of at most 32 chunks) instead of
+    index kernel gives each request its own ranges (pieces of at most 64 chunks) instead of
     equal ranges across requests. Every output finite and a sample of rows against the
     oracle."""
     say(f"flat plan whole rows: B={batch} ctx=[{lo},{hi}] hq={hq} hkv={hkv}")
