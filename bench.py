@@ -590,6 +590,20 @@ def sweep(kind: str) -> None:
                   f"{gbs:.0f} GB/s | {gbs * 1e9 / HBM_PEAK:.0%} HBM |", flush=True)
             del w, ops
             torch.cuda.empty_cache()
+        # spread context lengths and batches past 256 requests (the flat plan's index kernel:
+        # equal, snapped or whole-request ranges)
+        for batch, lo, hi, hq, hkv in ((64, 100, 3000, 32, 8), (256, 100, 3000, 32, 8),
+                                       (600, 100, 3000, 32, 8), (1024, 100, 3000, 32, 4),
+                                       (1000, 500, 1500, 32, 8), (2048, 100, 1000, 32, 8)):
+            w = W.decode_batched(device=dev, seed=5, batch=batch, ctx_lo=lo, ctx_hi=hi, hq=hq,
+                                 hkv=hkv, with_write=False)
+            ops = Ops(w, dev, stream)
+            ms, _ = time_loop(ops.decode, 20, 3, stream)
+            gbs = w.kv_bytes() / (ms * 1e-3) / 1e9
+            print(f"| B={batch} ctx=U[{lo},{hi}] Hq/Hkv={hq}/{hkv} | {ms * 1e3:.1f} | "
+                  f"{gbs:.0f} GB/s | {gbs * 1e9 / HBM_PEAK:.0%} HBM |", flush=True)
+            del w, ops
+            torch.cuda.empty_cache()
     else:
         for n_seqs, prefix, new, hq, hkv in ((8, 512, 1536, 16, 8), (8, 0, 2048, 16, 8),
                                              (4, 4096, 2048, 16, 8), (2, 16384, 2048, 16, 8),
