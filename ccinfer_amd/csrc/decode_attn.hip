@@ -1207,7 +1207,7 @@ struct DecodeWs {
     float* o;
     float* ml;
     MergeDesc* desc;
-    int32_t* index;  // the flat plan's index (batches past kFlatMaxItems)
+    int32_t* index;  // the flat plan's index (when plan.flat_index)
 };
 
 // Partial rows of the plan: (item, q_head, split) in fixed mode, (q_head, slot) flat.

@@ -16,11 +16,13 @@ hipError_t write_kv_cache(const void* k_new, const void* v_new, void* k_cache, v
 
 // ---- decode ---------------------------------------------------------------
 // Split-KV plan. Fixed mode: `splits` partitions of `split_tokens` tokens per (request,
-// kv_head), sized from the longest possible context. Flat mode (decode batches of 4 to
-// kFlatMaxItems requests): the flat plan -- on the device, the batch's 32-token chunks
-// laid end to end are cut into wave_target equal ranges per kv_head, one per wavefront,
-// across request boundaries, so every wavefront streams the same number of tokens whatever
-// the spread of context lengths; `slots` bounds the number of splits per kv_head.
+// kv_head), sized from the longest possible context. Flat mode (decode batches of 4 or more
+// requests): on the device, the batch's 32-token chunks laid end to end are cut into
+// wave_target equal ranges per kv_head, one per wavefront, across request boundaries, so
+// every wavefront streams the same number of tokens whatever the spread of context
+// lengths; `slots` bounds the number of splits per kv_head. Past kFlatMaxItems requests,
+// or at 4096 wavefronts and more, an index kernel writes the plan first; at 4096 and more
+// it also snaps the ranges to request boundaries or gives each request its own ranges.
 struct DecodePlan {
     int splits = 1;
     int split_tokens = 0;  // multiple of 32
@@ -28,8 +30,8 @@ struct DecodePlan {
     int slots = 0;
     int wave_target = 0;
     bool group = false;  // one workgroup per (item, kv_head), parts merged in LDS
-    bool flat_index = false;  // flat plan for > kFlatMaxItems items: an index kernel first
-    bool flat_snap = false;   // the index snaps range starts to request boundaries
+    bool flat_index = false;  // the flat plan's index kernel runs first
+    bool flat_snap = false;   // the index reshapes the ranges (snapped or whole requests)
 };
 
 // Requests the flat plan's in-kernel scan covers; larger batches get the index kernel.
