@@ -340,3 +340,22 @@ def test_table_row_longer_than_4096_blocks(gpu):
     want = oracle_prefill(w, pairs=pairs)
     r, h = pairs[:, 0], pairs[:, 1]
     assert_attn_close(got[r, h], want[r, h], "long table")
+
+
+def test_mixed_batch_with_600_decode_items(gpu):
+    """600 single-token requests of 100..3000 positions in a prefill call: the decode items
+    run the flat plan's index with snapped ranges (4816 wavefronts), reaching requests
+    through the item list. Unused slots poisoned; every decode row against the oracle."""
+    from tests.test_gpu_random_shapes import _poison_unused
+    say("prefill mixed 2x64 chunks + 600 decodes of 100..3000 positions (all decode rows)")
+    w = W.mixed_step(device=gpu, seed=31, n_chunks=2, chunk=64, prefix_hi=256, n_decode=600,
+                     dec_lo=100, dec_hi=3000)
+    write_new(w, gpu)
+    _poison_unused(w, gpu)
+    got = f32(run_prefill(w, gpu))
+    assert np.all(np.isfinite(got))
+    nc = w.info["n_chunks"]
+    rows = w.query_start_loc[nc:-1]
+    ref = oracle.decode(u16(w.q)[rows], u16(w.k_cache), u16(w.v_cache), w.block_table[nc:],
+                        w.context_lens[nc:])
+    assert_attn_close(got[rows], ref, "600 decode items")
