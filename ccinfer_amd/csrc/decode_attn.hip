@@ -524,8 +524,11 @@ struct ChunkRegs {
 };
 
 // kPad: the cache rows hold dr < D dims (dr a multiple of D/16); the kernel runs at the
-// MFMA size D with dims [dr, D) zero. Loads of missing dims read a valid piece of the row
-// instead (so every lane still issues the same loads) and are replaced by zeros.
+// MFMA size D with dims [dr, D) zero. At D = 128 (head dims 80-120) the lanes of missing
+// dims load nothing (exec-masked loads): the L2 re-reads they would make cost 4-11 % of
+// the batch (d=80 151.5 -> 139.7 us, d=120 191.4 -> 183.4 us at 64 x 4096). At D = 64 and
+// 256 such loads read a valid piece of the row instead and are replaced by zeros: masking
+// measured 11-23 % slower at d=32, and spills 137 VGPRs at D = 256.
 template <int D, bool kPad = false, bool kTL = false>
 __device__ __forceinline__ void load_chunk(ChunkRegs<D>& c, const __bf16* __restrict__ k_cache,
                                            const __bf16* __restrict__ v_cache, int pb0, int pb1,
@@ -533,6 +536,7 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<D>& c, const __bf16* __rest
     constexpr int S = DecodeShape<D>::kSteps;
     constexpr int NV = DecodeShape<D>::kNV;
     const int rs = kPad ? dr : D;  // row stride (elements)
+    constexpr bool kMasked = kPad && D == 128;
     const int i = lane & 15;
     const int g = lane >> 4;
     const int pbs[2] = {pb0 < 0 ? 0 : pb0, pb1 < 0 ? 0 : pb1};
@@ -544,8 +548,13 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<D>& c, const __bf16* __rest
         for (int kk = 0; kk < S; ++kk) {
             const int dim0 = (kk * 4 + g) * 8;
             const bool ok = !kPad || dim0 < dr;
-            c.k[kb][kk] = kv_load<kTL>(reinterpret_cast<const u32x4*>(row + (ok ? dim0 : 0)));
-            if (!ok) c.k[kb][kk] = u32x4{0, 0, 0, 0};
+            if constexpr (kMasked) {
+                c.k[kb][kk] = u32x4{0, 0, 0, 0};
+                if (ok) c.k[kb][kk] = kv_load<kTL>(reinterpret_cast<const u32x4*>(row + dim0));
+            } else {
+                c.k[kb][kk] = kv_load<kTL>(reinterpret_cast<const u32x4*>(row + (ok ? dim0 : 0)));
+                if (!ok) c.k[kb][kk] = u32x4{0, 0, 0, 0};
+            }
         }
     }
     const bool vok = !kPad || i * NV < dr;
@@ -557,11 +566,13 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<D>& c, const __bf16* __rest
             v_cache + ((static_cast<int64_t>(pbs[kb]) * kBlock + off) * hkv + kv_head) * rs +
             (vok ? i * NV : 0);
         if constexpr (NV == 8) {
-            const u32x4 w = kv_load<kTL>(reinterpret_cast<const u32x4*>(row));
+            u32x4 w = u32x4{0, 0, 0, 0};
+            if (!kMasked || vok) w = kv_load<kTL>(reinterpret_cast<const u32x4*>(row));
 #pragma unroll
             for (int x = 0; x < 4; ++x) c.v[e][x] = vok ? w[x] : 0u;
         } else if constexpr (NV == 4) {
-            const u32x2 w = kv_load<kTL>(reinterpret_cast<const u32x2*>(row));
+            u32x2 w = u32x2{0, 0};
+            if (!kMasked || vok) w = kv_load<kTL>(reinterpret_cast<const u32x2*>(row));
             c.v[e][0] = vok ? w[0] : 0u;
             c.v[e][1] = vok ? w[1] : 0u;
         } else {
