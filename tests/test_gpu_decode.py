@@ -315,6 +315,39 @@ def test_fused_kv_write_skips_rows_without_a_slot(gpu):
 
 
 
+def _poison_unread_slots(w, gpu):
+    """NaN K / Inf V in every cache slot no request of w reads (rows with an invalid
+    context read nothing)."""
+    used = np.zeros(w.num_blocks * 16, bool)
+    for b in range(w.batch):
+        n = int(w.context_lens[b])
+        if n <= 0 or (n + 15) // 16 > w.mbpr:
+            continue
+        pos = np.arange(n)
+        blk = w.block_table[b, pos // 16]
+        ok = blk >= 0
+        used[blk[ok] * 16 + pos[ok] % 16] = True
+    rows = torch.from_numpy(np.nonzero(~used)[0]).to(gpu)
+    w.k_cache[rows] = float("nan")
+    w.v_cache[rows] = float("inf")
+
+
+def _invalidate_and_hole(w, seed, step):
+    """Rows 3 (context 0) and 7 (longer than the table row) become invalid; every
+    step-th row from 10 loses one block that is not its last."""
+    rng = np.random.default_rng(seed)
+    ctx = w.context_lens.copy()
+    bt = w.block_table.copy()
+    ctx[3] = 0
+    ctx[7] = w.mbpr * 16 + 17
+    for b in range(10, w.batch, step):
+        nb = int(np.count_nonzero(bt[b] >= 0))
+        if nb > 2:
+            bt[b, int(rng.integers(0, nb - 1))] = -1
+    w.context_lens = ctx
+    w.block_table = bt
+
+
 @pytest.mark.parametrize("batch,lo,hi,hq,hkv,seed", [
     (300, 100, 3000, 32, 8, 61),     # index, equal ranges
     (257, 4000, 4096, 32, 8, 63),    # index, equal ranges, long rows
@@ -333,17 +366,7 @@ def test_flat_plan_index_for_large_batches(gpu, batch, lo, hi, hq, hkv, seed):
     say(f"flat plan index: B={batch} ctx=[{lo},{hi}] hq={hq} hkv={hkv}")
     w = W.decode_batched(device=gpu, seed=seed, batch=batch, ctx_lo=lo, ctx_hi=hi, hq=hq,
                          hkv=hkv, with_write=True)
-    rng = np.random.default_rng(seed)
-    ctx = w.context_lens.copy()
-    bt = w.block_table.copy()
-    ctx[3] = 0                                   # invalid: zeros
-    ctx[7] = w.mbpr * 16 + 17                    # longer than the table row: zeros
-    for b in range(10, batch, 37):
-        nb = int(np.count_nonzero(bt[b] >= 0))
-        if nb > 2:
-            bt[b, int(rng.integers(0, nb - 1))] = -1   # a hole, never the last block
-    w.context_lens = ctx
-    w.block_table = bt
+    _invalidate_and_hole(w, seed, 37)
     w.slot_mapping = w.slot_mapping.copy()
     w.slot_mapping[[3, 7]] = -1                  # invalid rows have no new-token slot
     meta = w.device_meta(gpu)
@@ -355,18 +378,7 @@ def test_flat_plan_index_for_large_batches(gpu, batch, lo, hi, hq, hkv, seed):
     torch.cuda.synchronize()
     assert torch.equal(got, want)
     assert torch.equal(w.k_cache, kc) and torch.equal(w.v_cache, vc)
-    used = np.zeros(w.num_blocks * 16, bool)
-    for b in range(batch):
-        n = min(int(ctx[b]), w.mbpr * 16)
-        if n <= 0 or (n + 15) // 16 > w.mbpr:
-            continue
-        pos = np.arange(n)
-        blk = bt[b, pos // 16]
-        ok = blk >= 0
-        used[blk[ok] * 16 + pos[ok] % 16] = True
-    rows = torch.from_numpy(np.nonzero(~used)[0]).to(gpu)
-    w.k_cache[rows] = float("nan")
-    w.v_cache[rows] = float("inf")
+    _poison_unread_slots(w, gpu)
     out = run_decode(w, gpu)
     res = f32(out)
     assert np.all(res[3] == 0) and np.all(res[7] == 0)
@@ -402,12 +414,15 @@ def test_flat_plan_whole_rows(gpu, batch, lo, hi, hq, hkv, seed):
     """Launches whose longest request is short next to one resident wavefront's share: the
     index kernel gives each request its own ranges (pieces of at most 64 chunks) instead of
     equal ranges across requests. Every output finite and a sample of rows against the
-    oracle."""
+    oracle, with invalid rows, table holes and every unread slot poisoned."""
     say(f"flat plan whole rows: B={batch} ctx=[{lo},{hi}] hq={hq} hkv={hkv}")
     w = W.decode_batched(device=gpu, seed=seed, batch=batch, ctx_lo=lo, ctx_hi=hi, hq=hq,
                          hkv=hkv, with_write=False)
+    _invalidate_and_hole(w, seed, 29)
+    _poison_unread_slots(w, gpu)
     res = f32(run_decode(w, gpu))
     assert np.all(np.isfinite(res))
+    assert np.all(res[3] == 0) and np.all(res[7] == 0)
     rows = np.r_[0:64, 64:batch:23, batch - 5:batch]
     ref = oracle.decode(u16(w.q)[rows], u16(w.k_cache), u16(w.v_cache), w.block_table[rows],
                         w.context_lens[rows])
