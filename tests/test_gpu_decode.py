@@ -427,3 +427,25 @@ def test_flat_plan_whole_rows(gpu, batch, lo, hi, hq, hkv, seed):
     ref = oracle.decode(u16(w.q)[rows], u16(w.k_cache), u16(w.v_cache), w.block_table[rows],
                         w.context_lens[rows])
     assert_attn_close(res[rows], ref, f"B={batch}")
+
+
+@pytest.mark.parametrize("batch,hkv", [(300, 8), (700, 8)])
+def test_flat_plan_index_with_no_or_one_valid_row(gpu, batch, hkv):
+    """The index kernel when the batch holds no chunks at all (every context 0 or too long
+    for the table row: zeros everywhere), and when a single row holds them all."""
+    say(f"flat plan index, degenerate batches: B={batch}")
+    w = W.decode_batched(device=gpu, seed=69, batch=batch, ctx_lo=100, ctx_hi=3000,
+                         hkv=hkv, with_write=False)
+    full = w.context_lens.copy()
+    ctx = np.zeros_like(full)
+    ctx[1::2] = w.mbpr * 16 + 1                  # longer than the table row
+    w.context_lens = ctx
+    out = f32(run_decode(w, gpu))
+    assert np.all(out == 0)
+    ctx = np.zeros_like(full)
+    ctx[batch // 2] = full[batch // 2]
+    w.context_lens = ctx
+    out = f32(run_decode(w, gpu))
+    assert np.all(np.delete(out, batch // 2, axis=0) == 0)
+    ref = oracle_decode(w)
+    assert_attn_close(out, ref, "one valid row")
