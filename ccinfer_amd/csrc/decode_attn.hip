@@ -274,7 +274,7 @@ __device__ __forceinline__ bool flat_segment(const int32_t* __restrict__ context
     return false;
 }
 
-// ---- the flat plan's index: batches past kFlatMaxItems requests, and snapped ranges ----
+// ---- the flat plan's index: batches past kFlatMaxItems requests, and reshaped ranges ----
 // Scanning every request in every wavefront gets costly for large batches, so one
 // 1024-thread workgroup (decode_flat_index_kernel, launched just before the split kernel)
 // writes the plan once:
@@ -284,12 +284,15 @@ __device__ __forceinline__ bool flat_segment(const int32_t* __restrict__ context
 //   V[0..B)       the first range that holds a chunk of the request,
 //   L[0..slots]   the first chunk of each range (L[slots] = C),
 //   F[0..slots)   the request holding chunk L[w].
-// Range w is the chunks [L[w], L[w+1]). Unsnapped, L[w] = min(w * T, C) as in flat_segment.
-// Snapped, a range start that lies within min(T / 2, (kMaxSplitTokens / kChunk - T) / 2)
-// chunks of a request boundary moves to the nearer boundary: a request of about T chunks
-// then runs whole in one wavefront instead of two segments of two wavefronts (one pipeline
-// start, one partial write and a merge saved), and no range outgrows a split. Launches of many rounds of wavefronts snap: the
-// dispatcher evens out the longer ranges there, and the split rows cost more than they save.
+// Range w is the chunks [L[w], L[w+1]). Equal ranges: L[w] = min(w * T, C), as in
+// flat_segment. Launches of many rounds of wavefronts (snap) reshape them, since the
+// dispatcher evens out unequal ranges there and a request cut in two costs a second
+// segment (a pipeline start, a partial write and a merge):
+// - whole requests: when the longest request is short next to one resident wavefront's
+//   share, each request gets its own ranges (pieces of at most kMaxSplitTokens tokens);
+// - snapped ranges otherwise: a range start within min(T / 2, (kMaxSplitTokens / kChunk -
+//   T) / 2) chunks of a request boundary moves to the nearer boundary, so a request of
+//   about T chunks runs whole in one wavefront and no range outgrows a split.
 __device__ __forceinline__ int items_live(const ItemArgs& items) {
     int B = items.num_items;
     if (items.item_count != nullptr) B = min(B, *items.item_count);
