@@ -532,6 +532,13 @@ def profile(op: str, iters: int) -> None:
         fn = lambda: dst.copy_(src)  # noqa: E731
     elif op == "prologue":
         fn = prologue_call(W.prologue(device=dev, tokens=12288), stream)
+    elif op in ("decode_b600", "decode_b2048"):
+        # batches past 256 requests (the flat plan's index kernel): 600 x U[100, 3000]
+        # positions (snapped ranges), 2048 x U[100, 1000] (one range per request)
+        batch, lo, hi = (600, 100, 3000) if op == "decode_b600" else (2048, 100, 1000)
+        w = W.decode_batched(device=dev, seed=5, batch=batch, ctx_lo=lo, ctx_hi=hi, hq=32,
+                             hkv=8, with_write=False)
+        fn = Ops(w, dev, stream).decode
     elif op in ("shared_prefix", "private_prefix"):
         # 16 sequences x (4096 cached + 256 new): one prefix shared by all, or 16 copies
         share = tuple((i, 0) for i in range(1, 16)) if op == "shared_prefix" else ()
@@ -646,6 +653,7 @@ def main():
     ap.add_argument("--sweep", choices=("decode", "prefill"),
                     help="print a table of the op across shapes and exit")
     ap.add_argument("--profile-op", choices=["decode", "write", "prefill", "mixed", "long",
+                                             "decode_b600", "decode_b2048",
                                              "prologue", "shared_prefix", "private_prefix",
                                              "shared_prefix_ragged", "private_prefix_ragged",
                                              "copy"], default=None)
