@@ -212,3 +212,35 @@ def test_random_mixed(gpu, seed):
     ref = oracle.prefill(u16(w.q), u16(w.k_cache), u16(w.v_cache), w.block_table,
                          w.query_start_loc, w.context_lens)
     assert_attn_close(f32(got), ref, f"mixed seed {seed}")
+
+
+@pytest.mark.parametrize("seed", range(9))
+def test_random_large_batch_decode(gpu, seed):
+    """Batches of 257-1200 requests (the flat plan's index kernel, equal, snapped or
+    whole-request ranges) over every decode head dim and group size, holes in the table and
+    unread slots poisoned: every output finite, a sample of rows against the oracle."""
+    rng = np.random.default_rng(900 + seed)
+    d = HEAD_DIMS[seed]
+    g = int(rng.choice(GROUPS))
+    hkv = max(1, min(int(rng.choice((1, 2, 4, 8))), 32 // g))
+    batch = int(rng.integers(257, 1201))
+    hi = int(rng.integers(200, 3001))
+    say(f"random large decode seed={seed} d={d} hq={g * hkv} hkv={hkv} B={batch} "
+        f"ctx=[1,{hi}]")
+    w = W.decode_batched(device=gpu, seed=9000 + seed, batch=batch, ctx_lo=1, ctx_hi=hi,
+                         hq=g * hkv, hkv=hkv, d=d, with_write=False)
+    bt = w.block_table.copy()
+    for b in range(0, batch, 5):
+        nb = int(np.count_nonzero(bt[b] >= 0))
+        if nb > 2:
+            bt[b, int(rng.integers(0, nb - 1))] = -1
+    w.block_table = bt
+    _poison_unused(w, gpu)
+    meta = w.device_meta(gpu)
+    got = f32(decode_attention(w.q, w.k_cache, w.v_cache, meta["block_table"],
+                               meta["context_lens"]))
+    assert np.all(np.isfinite(got))
+    rows = np.unique(np.r_[0:16, rng.integers(0, batch, size=48), batch - 8:batch])
+    ref = oracle.decode(u16(w.q)[rows], u16(w.k_cache), u16(w.v_cache), w.block_table[rows],
+                        w.context_lens[rows])
+    assert_attn_close(got[rows], ref, f"large seed {seed}")
