@@ -136,8 +136,13 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(
     if (tid == 0) s_ndec = 0;
     __syncthreads();
 
-    // Per-request tile counts; single-token requests become decode items.
-    for (int b = tid; b < batch_size; b += blockDim.x) {
+    // Per-request tile counts; single-token requests become decode items, listed in request
+    // order (a block-wide compaction per round of blockDim.x requests), so the decode plan
+    // built from the list -- and with it the output bits -- is the same on every run.
+    for (int b0 = 0; b0 < batch_size; b0 += blockDim.x) {
+        const int b = b0 + tid;
+        int isdec = 0;
+        if (b < batch_size) {
         const int qb = qsl[b];
         const int qe_raw = qsl[b + 1];
         const int qlen = qe_raw - qb;
@@ -150,16 +155,29 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(
         }
         int n = 0;
         if (qlen > 0 && prefix >= 0 && qb >= 0 && rows > 0) {
-            if (qlen == 1) {
-                const int slot = atomicAdd(&s_ndec, 1);
-                dec_req[slot] = b;
-            } else {
+            if (qlen == 1)
+                isdec = 1;
+            else
                 n = (rows + tile_tokens - 1) / tile_tokens;
-            }
         }
         s_ntiles[b] = n;
+        }
+        const int wave = tid >> 6;
+        const int incl = wave_inclusive_scan(isdec);
+        if ((tid & 63) == 63) s_part[wave] = incl;
+        __syncthreads();
+        int base = s_ndec;
+        int round = 0;
+        for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) {
+            const int pw = s_part[w];
+            if (w < wave) base += pw;
+            round += pw;
+        }
+        if (isdec) dec_req[base + incl - 1] = b;
+        __syncthreads();  // every thread has read s_ndec and s_part
+        if (tid == 0) s_ndec += round;
+        __syncthreads();
     }
-    __syncthreads();
     for (int b = tid; b < batch_size; b += blockDim.x) s_scan[b] = s_ntiles[b];
     __syncthreads();
     block_inclusive_scan(s_scan, batch_size, s_part);

@@ -359,3 +359,52 @@ def test_mixed_batch_with_600_decode_items(gpu):
     ref = oracle.decode(u16(w.q)[rows], u16(w.k_cache), u16(w.v_cache), w.block_table[nc:],
                         w.context_lens[nc:])
     assert_attn_close(got[rows], ref, "600 decode items")
+
+
+@pytest.mark.parametrize("n_req", [40, 120, 200, 257])
+def test_in_launch_plan_matches_planner(gpu, n_req):
+    """Batches of up to 256 requests and tiles plan inside the tile launch; with a side
+    stream (32+ requests) the planner kernel plans them instead. Both must give the same
+    bits, and every row must match the oracle: ragged prompts, single-token items, empty and
+    malformed (prefix < 0) requests, table holes. 257 requests always take the planner."""
+    from ccinfer_amd import SideStream
+    say(f"prefill in-launch plan vs planner, {n_req} requests")
+    rng = np.random.default_rng(900 + n_req)
+    hq, hkv, d, mbpr = 16, 8, 128, 24
+    qlen = rng.choice([0, 1, 1, 2, 7, 33, 129], size=n_req).astype(np.int32)
+    prefix = rng.integers(0, 200, n_req).astype(np.int32)
+    ctx = np.minimum(qlen + prefix, mbpr * 16).astype(np.int32)
+    ctx[::17] = np.maximum(qlen[::17] - 1, 0)      # prefix < 0: rows left untouched
+    pool = n_req * mbpr
+    bt = rng.permutation(pool).astype(np.int32).reshape(n_req, mbpr)
+    bt[5, 2] = -1                                  # a hole
+    qsl = np.concatenate([[0], np.cumsum(qlen)]).astype(np.int32)
+    total = int(qsl[-1])
+    g = torch.Generator(device=gpu)
+    g.manual_seed(n_req)
+    q = W.randn_bf16((total, hq, d), g, gpu)
+    kc = W.randn_bf16((pool * 16, hkv, d), g, gpu)
+    vc = W.randn_bf16((pool * 16, hkv, d), g, gpu)
+    w = W.PagedWorkload("inplan", hq, hkv, d, ctx, bt, pool, q, kc, vc, query_start_loc=qsl)
+    m = w.device_meta(gpu)
+    outs = []
+    for side in (None, SideStream(gpu)):
+        o = torch.full_like(q, 7.0)
+        prefill_attention(q, kc, vc, m["block_table"], m["query_start_loc"],
+                          m["context_lens"], output=o, overlap=side)
+        torch.cuda.synchronize()
+        outs.append(o)
+    want = oracle_prefill(w, out=np.full((total, hq, d), 7.0, np.float32))
+    if not torch.equal(outs[0], outs[1]):
+        a, b = f32(outs[0]), f32(outs[1])
+        bad = np.nonzero((a != b).any(axis=(1, 2)))[0]
+        req = np.searchsorted(qsl, bad, side="right") - 1
+        for r, rq in list(zip(bad, req))[:12]:
+            ea = np.abs(a[r] - want[r]).max()
+            eb = np.abs(b[r] - want[r]).max()
+            print(f"row {r} req {rq} qlen {qlen[rq]} ctx {ctx[rq]} err serial {ea:.3e} "
+                  f"fork {eb:.3e} heads {np.nonzero((a[r] != b[r]).any(axis=1))[0]}")
+        print("bad rows", len(bad), "requests", np.unique(req))
+    assert_attn_close(f32(outs[1]), want, f"planner {n_req}")
+    assert_attn_close(f32(outs[0]), want, f"inplan {n_req}")
+    assert torch.equal(outs[0], outs[1])
