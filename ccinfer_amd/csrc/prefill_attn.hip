@@ -651,8 +651,7 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
                          const int32_t* __restrict__ block_table,
                          const int32_t* __restrict__ qsl,
                          const int32_t* __restrict__ context_lens, __bf16* __restrict__ out,
-                         int32_t* __restrict__ counts, const TileEntry* __restrict__ tiles,
-                         int32_t* __restrict__ dec_req, int plan_batch,
+                         const int32_t* __restrict__ counts, const TileEntry* __restrict__ tiles,
                          int total_tokens, int mbpr, int hq, int hkv, float scale_log2,
                          int dr) {
     static_assert(!(F8 && kPad), "fp8 runs the native head dims only");
@@ -696,129 +695,28 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
     const int WPH = kPipeWaves / HPW;
     const int U = hkv * (G / HPW);
     const int tile_idx = blockIdx.x / U;
+    if (tile_idx >= counts[0]) return;
     const int u = blockIdx.x % U;
     const int kvh = u / (G / HPW);
     const int hg = u % (G / HPW);
-    const int TT = WPH * kPipeRows;
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const TileEntry te = tiles[tile_idx];
+    const int req = te.req;
+    const int t0 = te.t0;
 
-    int req, t0, qb, qlen, ctx;
-    if (plan_batch > 0) {
-        // In-launch plan (batches of at most kPipeThreads requests and tiles; the host also
-        // keeps the decode items on this stream, after this launch). Every workgroup derives
-        // the planner's tile order itself -- longest visible range first, ties by request
-        // and tile index, so all workgroups agree -- and picks entry tile_idx. This spares
-        // the planner launch and the dependent reads of the tile list and the request's
-        // scalars. Workgroup 0 also writes the tile and decode-item counts and the
-        // decode-item list (in request order) for the decode-item launches that follow.
-        __shared__ int s_scan[kPipeThreads];
-        __shared__ int s_qb[kPipeThreads];
-        __shared__ int s_qlen[kPipeThreads];
-        __shared__ int s_ctx[kPipeThreads];
-        __shared__ __attribute__((aligned(16))) int s_key[kPipeThreads];
-        __shared__ int s_part[2 * kPipeWaves];
-        __shared__ int s_sel;
-        const int tid = threadIdx.x;
-        int n = 0;
-        int isdec = 0;
-        if (tid < plan_batch) {
-            const int b_qb = qsl[tid];
-            const int qe_raw = qsl[tid + 1];
-            const int b_ctx = context_lens[tid];
-            const int b_qlen = qe_raw - b_qb;
-            const int b_rows = min(qe_raw, total_tokens) - max(b_qb, 0);
-            if (b_qlen > 0 && b_ctx - b_qlen >= 0 && b_qb >= 0 && b_rows > 0) {
-                if (b_qlen == 1) isdec = 1;
-                else n = (b_rows + TT - 1) / TT;
-            }
-            s_qb[tid] = b_qb;
-            s_qlen[tid] = b_qlen;
-            s_ctx[tid] = b_ctx;
-        }
-        const int incl = wave_inclusive_scan(n);
-        const int dincl = wave_inclusive_scan(isdec);
-        if (lane == 63) {
-            s_part[wave] = incl;
-            s_part[kPipeWaves + wave] = dincl;
-        }
-        __syncthreads();
-        int base = 0, dbase = 0, total = 0, ndec = 0;
-#pragma unroll
-        for (int w = 0; w < kPipeWaves; ++w) {
-            const int pw = s_part[w];
-            const int dw = s_part[kPipeWaves + w];
-            if (w < wave) { base += pw; dbase += dw; }
-            total += pw;
-            ndec += dw;
-        }
-        s_scan[tid] = base + incl;
-        if (blockIdx.x == 0) {
-            if (isdec) dec_req[dbase + dincl - 1] = tid;
-            if (tid == 0) {
-                counts[0] = total;
-                counts[1] = ndec;
-            }
-        }
-        if (tile_idx >= total) return;  // workgroup-uniform
-        __syncthreads();
-        // Tile t (one per thread): request b = first with inclusive scan > t, tile r of it.
-        int key = 0x7fffffff;
-        if (tid < total) {
-            int lo = 0, hi = plan_batch - 1;
-            while (lo < hi) {
-                const int mid = (lo + hi) >> 1;
-                if (s_scan[mid] > tid) hi = mid; else lo = mid + 1;
-            }
-            const int r = tid - (lo > 0 ? s_scan[lo - 1] : 0);
-            const int b_qlen = s_qlen[lo];
-            const int last = min((r + 1) * TT, b_qlen);
-            const int cost = (s_ctx[lo] - b_qlen + last) >> 6;
-            // (cost bucket, tile index): higher cost first, the same buckets as the planner
-            key = ((kBuckets - 1 - min(cost, kBuckets - 1)) << 10) | tid;
-        }
-        s_key[tid] = key;
-        __syncthreads();
-        if (tid < total) {
-            int rank = 0;
-            const int4* k4 = reinterpret_cast<const int4*>(s_key);
-            for (int j = 0; j < (total + 3) / 4; ++j) {
-                const int4 kk = k4[j];
-                rank += (kk.x < key) + (kk.y < key) + (kk.z < key) + (kk.w < key);
-            }
-            if (rank == tile_idx) s_sel = tid;
-        }
-        __syncthreads();
-        const int sel = s_sel;
-        int lo = 0, hi = plan_batch - 1;
-        while (lo < hi) {
-            const int mid = (lo + hi) >> 1;
-            if (s_scan[mid] > sel) hi = mid; else lo = mid + 1;
-        }
-        req = __builtin_amdgcn_readfirstlane(lo);
-        t0 = __builtin_amdgcn_readfirstlane((sel - (lo > 0 ? s_scan[lo - 1] : 0)) * TT);
-        qb = __builtin_amdgcn_readfirstlane(s_qb[req]);
-        qlen = __builtin_amdgcn_readfirstlane(s_qlen[req]);
-        ctx = __builtin_amdgcn_readfirstlane(s_ctx[req]);
-    } else {
-        // Both reads go out together; entries past the count are never used.
-        const int cnt = counts[0];
-        const TileEntry te = tiles[tile_idx];
-        if (tile_idx >= cnt) return;
-        req = te.req;
-        t0 = te.t0;
-        qb = qsl[req];
-        qlen = qsl[req + 1] - qb;
-        ctx = context_lens[req];
-    }
+    const int qb = qsl[req];
+    const int qlen = qsl[req + 1] - qb;
+    const int ctx = context_lens[req];
     const int prefix = ctx - qlen;
     const int qe = min(qb + qlen, total_tokens);
     const int rows = qe - qb;
+    const int TT = WPH * kPipeRows;
     const int kv_end = prefix + min(t0 + TT, rows);  // keys past it are masked for every row
     // Positions past the table row are invalid: no tile needs to reach them.
     const int kv_lim = min(kv_end, mbpr * kBlock);
     const int ntiles = (kv_lim + kKeysPerTile - 1) / kKeysPerTile;
 
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int head_local = wave / WPH;
     const int tw = t0 + (wave % WPH) * kPipeRows;
     const int q_head = kvh * G + hg * HPW + head_local;
@@ -1507,9 +1405,9 @@ hipError_t launch_tiles(const void* q, const void* k_cache, const void* v_cache,
                         const float* k_scale, const float* v_scale,
                         const int32_t* block_table, const int32_t* qsl,
                         const int32_t* context_lens, void* output, int total_query_tokens,
-                        int mbpr, int hq, int hkv, int block_size, int32_t* counts,
-                        const TileEntry* tiles, int32_t* dec_req, int plan_batch,
-                        const void* zero_row, int max_tiles, hipStream_t stream, int dr) {
+                        int mbpr, int hq, int hkv, int block_size, const int32_t* counts,
+                        const TileEntry* tiles, const void* zero_row, int max_tiles,
+                        hipStream_t stream, int dr) {
     const int G = hq / hkv;
     const int U = hkv * (G / heads_per_wg(G));
     const int64_t grid = static_cast<int64_t>(max_tiles) * U;
@@ -1519,8 +1417,8 @@ hipError_t launch_tiles(const void* q, const void* k_cache, const void* v_cache,
             <<<static_cast<unsigned>(grid), PipeShape<D>::kThreads, 0, stream>>>(
             static_cast<const __bf16*>(q), k_cache, v_cache, k_scale, v_scale, block_table, qsl,
             context_lens,
-            static_cast<__bf16*>(output), counts, tiles, dec_req, plan_batch, total_query_tokens,
-            mbpr, hq, hkv, scale_log2, dr);
+            static_cast<__bf16*>(output), counts, tiles, total_query_tokens, mbpr, hq, hkv,
+            scale_log2, dr);
         return hipGetLastError();
     } else if constexpr (F8) {
         return hipErrorInvalidValue;  // fp8 has the pipelined path only
@@ -1570,9 +1468,6 @@ namespace {
 // prompt batches with no decode items -- keep them after the tiles, where their near-empty
 // launches take no CUs from the tiles.
 constexpr int kOverlapMinRequests = 32;
-// Batches of at most this many requests and possible tiles (one thread of the tile
-// workgroup each) plan inside the tile launch.
-constexpr int kInPlanMax = 256;
 
 }  // namespace
 
@@ -1593,20 +1488,7 @@ hipError_t prefill_impl(const void* q, const void* k_cache, const void* v_cache,
     TileEntry* tiles = reinterpret_cast<TileEntry*>(ws + L.tiles_off);
     int32_t* dec = reinterpret_cast<int32_t*>(ws + L.dec_off);
     uint32_t* zero_row = reinterpret_cast<uint32_t*>(ws + L.zero_off);
-    const bool fork = overlap != nullptr && overlap->side != nullptr &&
-                      batch_size >= kOverlapMinRequests;
-    // Small batches on the pipelined kernels plan inside the tile launch (no planner
-    // launch). Not when the decode items fork to the side stream: they would run before the
-    // tile launch has written their list.
-    const int Dm = decode_mfma_dim(head_dim);
-    const int plan_batch =
-        !fork && pipe_head_dim(Dm) && batch_size > 0 && batch_size <= kInPlanMax &&
-                L.max_tiles <= kInPlanMax
-            ? batch_size
-            : 0;
-    if (plan_batch > 0) {
-        // nothing to launch: the tile kernel writes counts and the decode-item list
-    } else if (batch_size > kMaxPlanRequests) {
+    if (batch_size > kMaxPlanRequests) {
         int* big = reinterpret_cast<int*>(ws + L.big_off);
         prefill_plan_kernel<true><<<1, 1024, 0, stream>>>(
             query_start_loc, context_lens, batch_size, total_query_tokens, L.tile_tokens, counts,
@@ -1642,6 +1524,8 @@ hipError_t prefill_impl(const void* q, const void* k_cache, const void* v_cache,
                                     items, max_blocks_per_req, num_q_heads, num_kv_heads,
                                     head_dim, block_size, L.plan, ws + L.decode_ws_off, s);
     };
+    const bool fork = overlap != nullptr && overlap->side != nullptr &&
+                      batch_size >= kOverlapMinRequests;
     if (fork) {
         err = hipEventRecord(overlap->fork, stream);
         if (err == hipSuccess) err = hipStreamWaitEvent(overlap->side, overlap->fork, 0);
@@ -1654,8 +1538,7 @@ hipError_t prefill_impl(const void* q, const void* k_cache, const void* v_cache,
     launch_tiles<DD, F8, PP>(q, k_cache, v_cache, k_scale, v_scale, block_table,             \
                              query_start_loc, context_lens, output, total_query_tokens,      \
                              max_blocks_per_req, num_q_heads, num_kv_heads, block_size,      \
-                             counts, tiles, dec, plan_batch, zero_row, L.max_tiles, stream, \
-                             head_dim)
+                             counts, tiles, zero_row, L.max_tiles, stream, head_dim)
     if (F8 && pad) {
         err = hipErrorInvalidValue;  // fp8 runs the native head dims only
     } else {
