@@ -1465,8 +1465,9 @@ namespace {
 
 // Mixed batches of at least this many requests run their decode items on the caller's side
 // stream (when one is given) beside the tile kernel; smaller batches -- typically pure
-// prompt batches with no decode items -- keep them after the tiles, where their near-empty
-// launches take no CUs from the tiles.
+// prompt batches with no decode items -- run them on the caller's stream before the tiles,
+// where their near-empty launches take no CUs from the tiles (and, ahead of the tile
+// kernel rather than behind it, cost ~0.7 us less per step).
 constexpr int kOverlapMinRequests = 32;
 
 }  // namespace
@@ -1505,7 +1506,8 @@ hipError_t prefill_impl(const void* q, const void* k_cache, const void* v_cache,
     // or more run them there, concurrently with the tile kernel: they write other output rows
     // and other workspace, and the memory-bound decode work fills CUs the MFMA-bound tiles
     // leave idle. The fork and join are event records and waits only (no host sync), which
-    // is also legal under stream capture.
+    // is also legal under stream capture. Otherwise they run on the caller's stream between
+    // the planner and the tile kernel.
     DecodeItems items;
     items.num_items = batch_size;
     items.item_count = counts + 1;
@@ -1530,6 +1532,9 @@ hipError_t prefill_impl(const void* q, const void* k_cache, const void* v_cache,
         err = hipEventRecord(overlap->fork, stream);
         if (err == hipSuccess) err = hipStreamWaitEvent(overlap->side, overlap->fork, 0);
         if (err == hipSuccess) err = launch_decode_items(overlap->side);
+        if (err != hipSuccess) return err;
+    } else {
+        err = launch_decode_items(stream);
         if (err != hipSuccess) return err;
     }
     const int D = decode_mfma_dim(head_dim);
@@ -1563,8 +1568,7 @@ hipError_t prefill_impl(const void* q, const void* k_cache, const void* v_cache,
         const hipError_t jw = je == hipSuccess ? hipStreamWaitEvent(stream, overlap->join, 0) : je;
         return err != hipSuccess ? err : jw;
     }
-    if (err != hipSuccess) return err;
-    return launch_decode_items(stream);
+    return err;
 }
 
 }  // namespace
