@@ -126,7 +126,7 @@ __device__ __forceinline__ bool resolve_item(const ItemArgs& it, int item, int* 
 // wavefront reads that slot (one split holds each position; other requests do not see a
 // request's newest position).
 template <bool kPad>
-__device__ __forceinline__ void write_new_token(const __bf16* k_cache, const __bf16* v_cache,
+__device__ __forceinline__ void write_new_token(__bf16* k_cache, __bf16* v_cache,
                                                 const ItemArgs& items,
                                                 const int32_t* __restrict__ req_blocks, int req,
                                                 int ctx, int hkv_c, int kvh, int ds, int lane) {
@@ -134,12 +134,10 @@ __device__ __forceinline__ void write_new_token(const __bf16* k_cache, const __b
     const int pb = req_blocks[pos / kBlock];
     const int64_t slot = static_cast<int64_t>(pb) * kBlock + pos % kBlock;
     if (pb >= 0 && slot < items.max_slots) {
-        // Stores through the same (const-qualified) cache pointers the split's loads use, so
-        // the compiler keeps the loads after them.
-        uint32_t* kd = reinterpret_cast<uint32_t*>(
-            const_cast<__bf16*>(k_cache) + (slot * hkv_c + kvh) * ds);
-        uint32_t* vd = reinterpret_cast<uint32_t*>(
-            const_cast<__bf16*>(v_cache) + (slot * hkv_c + kvh) * ds);
+        // Stores through the same cache pointers the split's loads use, so the compiler
+        // keeps the loads after them.
+        uint32_t* kd = reinterpret_cast<uint32_t*>(k_cache + (slot * hkv_c + kvh) * ds);
+        uint32_t* vd = reinterpret_cast<uint32_t*>(v_cache + (slot * hkv_c + kvh) * ds);
         const int64_t src = (static_cast<int64_t>(req) * hkv_c + kvh) * ds;
         const uint32_t* ks = reinterpret_cast<const uint32_t*>(items.new_k + src);
         const uint32_t* vs = reinterpret_cast<const uint32_t*>(items.new_v + src);
@@ -283,7 +281,11 @@ __device__ __forceinline__ bool flat_segment(const int32_t* __restrict__ context
 //   S[0..B]       first partial slot of each request (S[B] = total splits),
 //   V[0..B)       the first range that holds a chunk of the request,
 //   L[0..slots]   the first chunk of each range (L[slots] = C),
-//   F[0..slots)   the request holding chunk L[w].
+//   F[0..slots)   the request holding chunk L[w],
+//   O             1 when the plan needed more than `slots` ranges or partial slots (the host
+//                 bound in plan_decode rules that out; should it ever be under-computed, the
+//                 merge kernel writes NaN to every output row instead of merging partials
+//                 that were never written).
 // Range w is the chunks [L[w], L[w+1]). Equal ranges: L[w] = min(w * T, C), as in
 // flat_segment. Launches of many rounds of wavefronts (snap) reshape them, since the
 // dispatcher evens out unequal ranges there and a request cut in two costs a second
@@ -328,7 +330,7 @@ __device__ int block_exclusive_scan_1024(int v, int* s_part, int* total) {
 }
 
 struct FlatIndex {
-    int32_t *P, *S, *V, *L, *F;
+    int32_t *P, *S, *V, *L, *F, *O;
 };
 
 __device__ __forceinline__ FlatIndex flat_index_arrays(int32_t* idx, int num_items, int slots) {
@@ -338,6 +340,7 @@ __device__ __forceinline__ FlatIndex flat_index_arrays(int32_t* idx, int num_ite
     x.V = x.S + num_items + 1;
     x.L = x.V + num_items;
     x.F = x.L + slots + 1;
+    x.O = x.F + slots;
     return x;
 }
 
@@ -407,6 +410,7 @@ __global__ __launch_bounds__(1024) void decode_flat_index_kernel(
             idx[1] = C;
             x.P[B] = C;
             x.S[B] = NS;
+            *x.O = NS > slots ? 1 : 0;
         }
         return;
     }
@@ -458,6 +462,7 @@ __global__ __launch_bounds__(1024) void decode_flat_index_kernel(
         idx[0] = T;
         idx[1] = C;
         x.S[B] = NS;
+        *x.O = (NS > slots || (C + T - 1) / T > slots) ? 1 : 0;
     }
 }
 
@@ -936,8 +941,8 @@ __device__ __forceinline__ void run_split(
 // kTL: the K/V loads stay in L2 (see kv_load).
 template <int D, bool F8, bool kPad, bool kTL>
 __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
-    const __bf16* __restrict__ q, const void* __restrict__ k_cache_v,
-    const void* __restrict__ v_cache_v, const float* __restrict__ k_scale,
+    const __bf16* __restrict__ q, void* k_cache_v, void* v_cache_v,
+    const float* __restrict__ k_scale,
     const float* __restrict__ v_scale, const int32_t* __restrict__ block_table,
     const int32_t* __restrict__ context_lens, __bf16* __restrict__ out, float* __restrict__ ws_o,
     float* __restrict__ ws_ml, MergeDesc* __restrict__ desc, ItemArgs items, int mbpr, int hq,
@@ -946,8 +951,10 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     const int ds = kPad ? dr : D;  // q / output row stride
     constexpr int NV = DecodeShape<D>::kNV;
     using Cache = std::conditional_t<F8, uint8_t, __bf16>;
-    const Cache* __restrict__ k_cache = static_cast<const Cache*>(k_cache_v);
-    const Cache* __restrict__ v_cache = static_cast<const Cache*>(v_cache_v);
+    // Neither const nor restrict: the fused new-token write (write_new_token) stores
+    // through these pointers before the split's loads read the same rows.
+    Cache* k_cache = static_cast<Cache*>(k_cache_v);
+    Cache* v_cache = static_cast<Cache*>(v_cache_v);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wi = blockIdx.x * kWavesPerGroup + wave;
@@ -1099,8 +1106,8 @@ struct GroupShape {
 
 template <int D, bool F8, bool kPad, bool kTL>
 __global__ __launch_bounds__(64 * GroupShape<D>::kWaves) void decode_group_kernel(
-    const __bf16* __restrict__ q, const void* __restrict__ k_cache_v,
-    const void* __restrict__ v_cache_v, const float* __restrict__ k_scale,
+    const __bf16* __restrict__ q, void* k_cache_v, void* v_cache_v,
+    const float* __restrict__ k_scale,
     const float* __restrict__ v_scale, const int32_t* __restrict__ block_table,
     const int32_t* __restrict__ context_lens, __bf16* __restrict__ out, ItemArgs items,
     int mbpr, int hq, int hkv, float scale_log2, int dr, int rep) {
@@ -1112,8 +1119,10 @@ __global__ __launch_bounds__(64 * GroupShape<D>::kWaves) void decode_group_kerne
     __shared__ float lds_o[W * kMaxG * D];
     __shared__ float lds_m[W * kMaxG];
     __shared__ float lds_l[W * kMaxG];
-    const Cache* __restrict__ k_cache = static_cast<const Cache*>(k_cache_v);
-    const Cache* __restrict__ v_cache = static_cast<const Cache*>(v_cache_v);
+    // Neither const nor restrict: the fused new-token write (write_new_token) stores
+    // through these pointers before the split's loads read the same rows.
+    Cache* k_cache = static_cast<Cache*>(k_cache_v);
+    Cache* v_cache = static_cast<Cache*>(v_cache_v);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int h = blockIdx.x % hkv;
@@ -1202,7 +1211,8 @@ __global__ __launch_bounds__(64 * GroupShape<D>::kWaves) void decode_group_kerne
 template <int D>
 __global__ __launch_bounds__(256) void decode_merge_kernel(
     __bf16* __restrict__ out, const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
-    const MergeDesc* __restrict__ desc, ItemArgs items, int hq, int dr) {
+    const MergeDesc* __restrict__ desc, ItemArgs items, int hq, int dr,
+    const int32_t* __restrict__ flat_idx, int slots) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wi = blockIdx.x * kWavesPerGroup + wave;
@@ -1212,6 +1222,13 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(
     const MergeDesc d = desc[static_cast<int64_t>(item) * hq + head];
     int req, qrow;
     if (!resolve_item(items, item, &req, &qrow)) return;
+    if (flat_idx != nullptr && *flat_index_arrays(const_cast<int32_t*>(flat_idx),
+                                                  items.num_items, slots).O != 0) {
+        // bf16 quiet-NaN bits (the build's -fno-honor-nans makes NaN arithmetic undefined)
+        uint16_t* o = reinterpret_cast<uint16_t*>(out + (static_cast<int64_t>(qrow) * hq + head) * dr);
+        for (int x = lane; x < dr; x += 64) o[x] = 0x7fc0u;
+        return;
+    }
     if (d.ns <= 1) return;  // invalid row, or written directly by the split kernel
     merge_row<D>(ws_o, ws_ml, d.base, static_cast<int>(d.ns), items.eps,
                  out + (static_cast<int64_t>(qrow) * hq + head) * dr, lane, dr);
@@ -1242,8 +1259,8 @@ size_t index_offset(size_t rows, int d, int num_items, int hq) {
 }
 
 size_t index_bytes(int num_items, int slots) {
-    // T, C, P[B + 1], S[B + 1], V[B], L[slots + 1], F[slots]
-    return (2 + 3 * static_cast<size_t>(num_items) + 2 + 2 * static_cast<size_t>(slots) + 1) *
+    // T, C, P[B + 1], S[B + 1], V[B], L[slots + 1], F[slots], O
+    return (2 + 3 * static_cast<size_t>(num_items) + 2 + 2 * static_cast<size_t>(slots) + 2) *
            sizeof(int32_t);
 }
 
@@ -1290,9 +1307,9 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
         auto go = [&](auto tl_tag) {
             decode_group_kernel<D, F8, kPad, decltype(tl_tag)::value>
                 <<<static_cast<unsigned>(groups), 64 * GroupShape<D>::kWaves, 0, stream>>>(
-                    static_cast<const __bf16*>(q), k_cache, v_cache, k_scale, v_scale,
-                    block_table, context_lens, static_cast<__bf16*>(output), it, mbpr, hq, hkv,
-                    scale_log2, dr, rep);
+                    static_cast<const __bf16*>(q), const_cast<void*>(k_cache),
+                    const_cast<void*>(v_cache), k_scale, v_scale, block_table, context_lens,
+                    static_cast<__bf16*>(output), it, mbpr, hq, hkv, scale_log2, dr, rep);
         };
         if (kPad || tl)
             go(std::true_type{});
@@ -1317,8 +1334,9 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
     const int bw = plan.flat ? plan.wave_target : 0;
     auto go = [&](auto tl_tag) {
         decode_split_kernel<D, F8, kPad, decltype(tl_tag)::value><<<grid, 256, 0, stream>>>(
-            static_cast<const __bf16*>(q), k_cache, v_cache, k_scale, v_scale, block_table,
-            context_lens, static_cast<__bf16*>(output), w.o, w.ml, w.desc, it, mbpr, hq, hkv,
+            static_cast<const __bf16*>(q), const_cast<void*>(k_cache), const_cast<void*>(v_cache),
+            k_scale, v_scale, block_table, context_lens, static_cast<__bf16*>(output), w.o, w.ml,
+            w.desc, it, mbpr, hq, hkv,
             plan.splits, plan.split_tokens, bw, plan.slots, scale_log2, dr, rep,
             plan.flat_index ? w.index : nullptr);
     };
@@ -1331,7 +1349,9 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
     const int64_t rows = static_cast<int64_t>(it.num_items) * hq;
     const int mgrid = static_cast<int>((rows + kWavesPerGroup - 1) / kWavesPerGroup);
     decode_merge_kernel<D><<<mgrid, 256, 0, stream>>>(static_cast<__bf16*>(output), w.o, w.ml,
-                                                      w.desc, it, hq, dr);
+                                                      w.desc, it, hq, dr,
+                                                      plan.flat_index ? w.index : nullptr,
+                                                      plan.slots);
     return hipGetLastError();
 }
 

@@ -3,7 +3,11 @@
 // src/backend/cuda/cuda_backend.cpp:162-187). It owns one HIP stream (default priority),
 // a side stream plus fork/join events on which a mixed prefill batch's decode items run
 // beside its prompt tiles, and one device workspace for the split-KV partials and the
-// prefill work list; the workspace grows on demand and is reused across calls.
+// prefill work list. The workspace is reserved once, by reserve_workspace, for the largest
+// shapes the caller will run (the reference's Worker::init_resources sizes its KV cache at
+// the same point, src/worker/worker.cpp:223-294); the ops never allocate, free or
+// synchronise, so they can be captured in a HIP graph. An op whose shape needs more
+// workspace than was reserved returns ErrorCode::InvalidArgument.
 #pragma once
 
 #include <hip/hip_bf16.h>
@@ -13,6 +17,7 @@
 #include <memory>
 
 #include "backend/backend.h"
+#include "kernel/hip_kernels.h"
 
 namespace ccinfer {
 
@@ -28,6 +33,12 @@ public:
     int device_id() const { return device_id_; }
     Result<void> synchronize();
 
+    // Reserves workspace for every decode / prefill op within `lim` (allocates; when a smaller
+    // reservation exists, synchronises the backend's streams and replaces it). Call at
+    // initialisation, outside stream capture.
+    Result<void> reserve_workspace(const AttnWorkspaceLimits& lim);
+    size_t reserved_workspace_bytes() const { return workspace_bytes_; }
+
     template <typename DType>
     Result<void> prefill_attention_impl(const PrefillAttnParams& p);
     template <typename DType>
@@ -37,7 +48,7 @@ public:
 
 private:
     HipBackend() = default;
-    Result<void*> workspace(size_t bytes);
+    Result<void*> workspace(size_t bytes) const;
 
     int device_id_ = 0;
     hipStream_t stream_ = nullptr;

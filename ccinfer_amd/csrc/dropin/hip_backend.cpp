@@ -1,5 +1,5 @@
 // HipBackend implementation: forwards the three hot-path ops to the C ABI on the backend's
-// own stream with its own workspace.
+// own stream with its reserved workspace.
 #include "backend/hip_backend.h"
 
 #include "ccinfer_attn.h"
@@ -56,21 +56,28 @@ HipBackend::~HipBackend() {
 
 Result<void> HipBackend::synchronize() { return check_hip(hipStreamSynchronize(stream_)); }
 
-Result<void*> HipBackend::workspace(size_t bytes) {
-    if (bytes == 0) return static_cast<void*>(nullptr);
-    if (bytes > workspace_bytes_) {
-        if (workspace_ != nullptr) {
-            // The old buffer may still be read by work queued on our streams.
-            if (auto r = check_hip(hipStreamSynchronize(stream_)); !r) return unexpected(r.error());
-            if (auto r = check_hip(hipStreamSynchronize(side_stream_)); !r)
-                return unexpected(r.error());
-            (void)hipFree(workspace_);
-            workspace_ = nullptr;
-            workspace_bytes_ = 0;
-        }
-        if (auto r = check_hip(hipMalloc(&workspace_, bytes)); !r) return unexpected(r.error());
-        workspace_bytes_ = bytes;
+Result<void> HipBackend::reserve_workspace(const AttnWorkspaceLimits& lim) {
+    const size_t bytes = attn_workspace_bytes(lim);
+    if (bytes == 0) return unexpected(ErrorCode::InvalidArgument);
+    if (bytes <= workspace_bytes_) return {};
+    if (auto r = check_hip(hipSetDevice(device_id_)); !r) return r;
+    if (workspace_ != nullptr) {
+        // work queued on our streams may still read the old buffer
+        if (auto r = check_hip(hipStreamSynchronize(stream_)); !r) return r;
+        if (auto r = check_hip(hipStreamSynchronize(side_stream_)); !r) return r;
+        (void)hipFree(workspace_);
+        workspace_ = nullptr;
+        workspace_bytes_ = 0;
     }
+    if (auto r = check_hip(hipMalloc(&workspace_, bytes)); !r) return r;
+    workspace_bytes_ = bytes;
+    return {};
+}
+
+// The reserved workspace when it covers `bytes` (no allocation here).
+Result<void*> HipBackend::workspace(size_t bytes) const {
+    if (bytes == 0) return static_cast<void*>(nullptr);
+    if (bytes > workspace_bytes_) return unexpected(ErrorCode::InvalidArgument);
     return workspace_;
 }
 

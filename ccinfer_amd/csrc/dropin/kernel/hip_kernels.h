@@ -5,8 +5,16 @@
 //
 // These wrappers call the C ABI (include/ccinfer_attn.h). The reference launchers take no
 // workspace, so the split-KV partials and the prefill work list come from a buffer the
-// library keeps per (device, stream); it is allocated on first use and grown when a larger
-// batch shape arrives, never per call at steady state.
+// library keeps per (device, stream), reserved once by reserve_launcher_workspace for the
+// largest shapes the caller will launch (the reference sizes its KV cache the same way, at
+// Worker::init_resources, src/worker/worker.cpp:223-294). The launchers themselves never
+// allocate, free or synchronise: a launch on a stream with no reservation, or whose shape
+// needs more than the reservation, returns ErrorCode::InvalidArgument. They are therefore
+// safe under stream capture.
+//
+// Thread safety: the (device, stream) -> buffer map is guarded by a mutex; reserve and
+// release modify it, launches only read it. Launches on different streams use different
+// buffers and may run concurrently; launches on one stream are ordered by the stream.
 #pragma once
 
 #include <hip/hip_bf16.h>
@@ -17,6 +25,26 @@
 #include "base/result.h"
 
 namespace ccinfer {
+
+// The largest shapes a caller will launch; a reservation covers every shape within them.
+struct AttnWorkspaceLimits {
+    int max_batch_size = 0;          // requests per launch
+    int max_query_tokens = 0;        // prefill: query tokens per launch
+    int max_blocks_per_req = 0;      // block-table row length
+    int num_q_heads = 0;
+    int num_kv_heads = 0;
+    int head_dim = 0;
+    int cache_block_size = 16;
+};
+
+// Bytes of device workspace that cover every decode and prefill launch within `lim` (0 when
+// the limits are invalid).
+size_t attn_workspace_bytes(const AttnWorkspaceLimits& lim);
+
+// Reserves the workspace of (current device, stream) for launches within `lim`: allocates
+// (after synchronising the stream, when a smaller buffer must be replaced) and keeps it until
+// release_launcher_workspaces. Call at initialisation, outside stream capture.
+Result<void> reserve_launcher_workspace(hipStream_t stream, const AttnWorkspaceLimits& lim);
 
 Result<void> launch_prefill_attention(const __hip_bfloat16* q, const __hip_bfloat16* k_cache,
                                       const __hip_bfloat16* v_cache, const int32_t* block_table,

@@ -34,9 +34,11 @@ namespace {
 constexpr int kWaves = 4;
 
 // The row scale: the smallest power of two P >= 2^-126 with amax <= 448 P (448 = 0.875 *
-// 2^9), or 0 for an all-zero row.
+// 2^9), 0 for an all-zero row, and 2^126 for a row holding an infinity (its infinities
+// store as +-448 and dequantise to +-inf again; its finite elements store as zeros).
 __device__ __forceinline__ float fp8_row_scale(float amax) {
     if (!(amax > 0.f)) return 0.f;
+    if (__builtin_isinf(amax)) return 0x1p126f;
     int e;
     const float f = frexpf(amax, &e);  // amax = f * 2^e, f in [0.5, 1)
     int p = e - 9 + (f > 0.875f ? 1 : 0);

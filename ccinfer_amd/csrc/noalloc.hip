@@ -7,7 +7,7 @@
 // kScratchBytes per GPU (each GPU the library runs on holds it until the process ends).
 // Host code never passes the array's name to a kernel: on the first call on a device, with
 // that device current, hipGetSymbolAddress resolves the device's own copy and the address
-// is kept per device. Shapes whose plan needs more than kScratchBytes are rejected with
+// is kept per device (that first call may itself be made under stream capture). Shapes whose plan needs more than kScratchBytes are rejected with
 // CCINFER_ERR_INVALID_ARGUMENT. The partials need no clearing between calls (every launch
 // rewrites what it reads). Calls that overlap on one GPU (concurrent streams) share the
 // array and race.
@@ -32,8 +32,11 @@ static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 std::atomic<void*> g_scratch_ptr[kMaxDevices];
 std::mutex g_scratch_mutex;
 
-// Device address of the current device's `scratch` (resolved once per device).
-hipError_t scratch_address(void** out) {
+// Device address of the current device's `scratch` (resolved once per device). A first
+// call made while `stream` is being captured resolves the address with the thread in relaxed
+// capture mode (the lookup enqueues no work, but the runtime's capture checks would
+// otherwise reject or invalidate the capture).
+hipError_t scratch_address(hipStream_t stream, void** out) {
     int dev = 0;
     hipError_t err = hipGetDevice(&dev);
     if (err != hipSuccess) return err;
@@ -43,7 +46,20 @@ hipError_t scratch_address(void** out) {
         std::lock_guard<std::mutex> lock(g_scratch_mutex);
         p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
         if (p == nullptr) {
+            hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+            err = hipStreamIsCapturing(stream, &status);
+            if (err != hipSuccess) return err;
+            const bool capturing = status != hipStreamCaptureStatusNone;
+            hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+            if (capturing) {
+                err = hipThreadExchangeStreamCaptureMode(&mode);
+                if (err != hipSuccess) return err;
+            }
             err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (capturing) {
+                const hipError_t back = hipThreadExchangeStreamCaptureMode(&mode);
+                if (err == hipSuccess) err = back;
+            }
             if (err != hipSuccess) return err;
             g_scratch_ptr[dev].store(p, std::memory_order_release);
         }
@@ -66,7 +82,7 @@ extern "C" int ccinfer_decode_attention_noalloc(const void* q, const void* k_cac
     if (need > kScratchBytes) return CCINFER_ERR_INVALID_ARGUMENT;
     void* ws = nullptr;
     if (need > 0) {
-        const hipError_t err = scratch_address(&ws);
+        const hipError_t err = scratch_address(static_cast<hipStream_t>(stream), &ws);
         if (err != hipSuccess) return CCINFER_ERR_DEVICE_RUNTIME;
     }
     // The workspace path's validation, plan and kernels, on the static array.

@@ -1528,11 +1528,20 @@ hipError_t prefill_impl(const void* q, const void* k_cache, const void* v_cache,
     };
     const bool fork = overlap != nullptr && overlap->side != nullptr &&
                       batch_size >= kOverlapMinRequests;
+    // Once the side stream has waited on the fork event it is joined back on every path,
+    // errors included (an unjoined fork would invalidate a capture of the caller's stream).
+    auto join = [&](hipError_t first) {
+        const hipError_t je = hipEventRecord(overlap->join, overlap->side);
+        const hipError_t jw = je == hipSuccess ? hipStreamWaitEvent(stream, overlap->join, 0) : je;
+        return first != hipSuccess ? first : jw;
+    };
     if (fork) {
         err = hipEventRecord(overlap->fork, stream);
-        if (err == hipSuccess) err = hipStreamWaitEvent(overlap->side, overlap->fork, 0);
-        if (err == hipSuccess) err = launch_decode_items(overlap->side);
         if (err != hipSuccess) return err;
+        err = hipStreamWaitEvent(overlap->side, overlap->fork, 0);
+        if (err != hipSuccess) return err;
+        err = launch_decode_items(overlap->side);
+        if (err != hipSuccess) return join(err);
     } else {
         err = launch_decode_items(stream);
         if (err != hipSuccess) return err;
@@ -1562,13 +1571,7 @@ hipError_t prefill_impl(const void* q, const void* k_cache, const void* v_cache,
         }
     }
 #undef CCI_TILES
-    if (fork) {
-        // join even when the tile launch failed, so the side stream's work is ordered
-        const hipError_t je = hipEventRecord(overlap->join, overlap->side);
-        const hipError_t jw = je == hipSuccess ? hipStreamWaitEvent(stream, overlap->join, 0) : je;
-        return err != hipSuccess ? err : jw;
-    }
-    return err;
+    return fork ? join(err) : err;
 }
 
 }  // namespace

@@ -19,10 +19,14 @@
  * ccinfer::ErrorCode (src/base/error_code.h:8-45) -- the same codes the reference returns
  * through Result<void>.
  *
- * Thread safety: re-entrant. The library keeps no global state except the per-device scratch
+ * Thread safety: re-entrant. The C ABI keeps no global state except the per-device scratch
  * array of ccinfer_decode_attention_noalloc (and that array's cached device address), so
  * concurrent calls on different streams need only different workspaces -- apart from that
- * entry, whose calls on one GPU share the array.
+ * entry, whose calls on one GPU share the array. The C++ drop-in layer above it
+ * (ccinfer_amd/csrc/dropin) adds one more piece of global state: the reference-signature
+ * launchers' workspaces, one per (device, stream), reserved explicitly by
+ * reserve_launcher_workspace and kept in a map behind a mutex (launches only read it; none
+ * allocates). HipBackend holds its own reserved workspace and needs no global state.
  *
  * Alignment: the reference launchers accept any bf16 (2-byte aligned) view. The MFMA paths
  * move q, output and K/V cache rows in 16-byte pieces, so bf16 decode / prefill calls with

@@ -593,6 +593,9 @@ int64_t orc_fp8_scale_index(int slot, int kv_head, int num_kv_heads, int block_s
 
 float orc_fp8_row_scale(float amax) {
     if (!(amax > 0.0f)) return 0.0f;
+    /* a row holding an infinity: 2^126, so inf * 2^-126 clamps to 448 and finite elements
+       store as zeros (kv_fp8.hip fp8_row_scale) */
+    if (isinf(amax)) return ldexpf(1.0f, 126);
     /* smallest p with amax <= 448 * 2^p, by search (448 * 2^p is exact in float) */
     int p = -126;
     while (p < 127 && amax > ldexpf(448.0f, p)) ++p;

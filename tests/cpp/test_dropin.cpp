@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "backend/hip_backend.h"
+#include "ccinfer_attn.h"
 #include "kernel/hip_kernels.h"
 
 using namespace ccinfer;
@@ -81,6 +82,24 @@ static void cpu_checks() {
                                    nullptr);
     CHECK(!w.has_value() && w.error() == ErrorCode::InvalidArgument);
     CHECK(error_message(ErrorCode::InvalidArgument) == "invalid argument");
+
+    // Workspace reservation sizes (host-only arithmetic over the C ABI size queries).
+    CHECK(attn_workspace_bytes(AttnWorkspaceLimits{}) == 0);
+    CHECK(attn_workspace_bytes(AttnWorkspaceLimits{.max_batch_size = 4, .max_query_tokens = 64,
+                                                    .max_blocks_per_req = 8, .num_q_heads = 6,
+                                                    .num_kv_heads = 4, .head_dim = 64}) == 0);
+    const AttnWorkspaceLimits lim{.max_batch_size = 64, .max_query_tokens = 4096,
+                                  .max_blocks_per_req = 256, .num_q_heads = 16,
+                                  .num_kv_heads = 8, .head_dim = 128};
+    const size_t res = attn_workspace_bytes(lim);
+    CHECK(res > 0);
+    // every shape within the limits fits the reservation
+    for (int b : {1, 2, 3, 4, 5, 8, 9, 31, 64})
+        for (int mb : {1, 16, 255, 256}) {
+            CHECK(ccinfer_decode_workspace_size(b, mb, 16, 8, 128, 16) <= res);
+            for (int t : {b, 1000, 4096})
+                CHECK(ccinfer_prefill_workspace_size(b, t, mb, 16, 8, 128, 16) <= res);
+        }
 }
 
 static uint16_t bf(float x) {
@@ -137,18 +156,79 @@ static void gpu_checks() {
     auto bk = reinterpret_cast<const __hip_bfloat16*>(k);
     auto bv = reinterpret_cast<const __hip_bfloat16*>(v);
 
-    // Decode: backend (own stream + workspace) vs reference-signature launcher.
-    auto r = be.decode_attention<__hip_bfloat16>(DecodeAttnParams{
+    const DecodeAttnParams dp{
         .q_ = q, .k_cache_ = k, .v_cache_ = v, .block_table_ = dbt, .context_lens_ = dctx,
         .output_ = o1, .batch_size_ = B, .max_blocks_per_req_ = MBPR, .num_q_heads_ = HQ,
-        .num_kv_heads_ = HKV, .head_dim_ = D, .cache_block_size_ = BS});
+        .num_kv_heads_ = HKV, .head_dim_ = D, .cache_block_size_ = BS};
+    // No reservation yet: the ops reject instead of allocating.
+    CHECK(ccinfer_decode_workspace_size(B, MBPR, HQ, HKV, D, BS) > 0);
+    auto r = be.decode_attention<__hip_bfloat16>(dp);
+    CHECK(!r.has_value() && r.error() == ErrorCode::InvalidArgument);
+    auto l = launch_decode_attention(bq, bk, bv, dbt, dctx, o2, B, MBPR, HQ, HKV, D, BS, nullptr);
+    CHECK(!l.has_value() && l.error() == ErrorCode::InvalidArgument);
+
+    // Reserve once (initialisation), then run.
+    const AttnWorkspaceLimits lim{.max_batch_size = B, .max_query_tokens = 128,
+                                  .max_blocks_per_req = MBPR, .num_q_heads = HQ,
+                                  .num_kv_heads = HKV, .head_dim = D, .cache_block_size = BS};
+    CHECK(be.reserve_workspace(lim).has_value());
+    CHECK(be.reserved_workspace_bytes() == attn_workspace_bytes(lim));
+    CHECK(reserve_launcher_workspace(nullptr, lim).has_value());
+
+    // A shape beyond the reservation is rejected before any launch (the size check runs
+    // first; the buffers here are far too small for the shape, so a launch would fault).
+    const int BIG_B = 4096, BIG_MBPR = 4096;
+    const size_t big = ccinfer_decode_workspace_size(BIG_B, BIG_MBPR, HQ, HKV, D, BS);
+    CHECK(big > be.reserved_workspace_bytes());
+    if (big > be.reserved_workspace_bytes()) {
+        DecodeAttnParams bp = dp;
+        bp.batch_size_ = BIG_B;
+        bp.max_blocks_per_req_ = BIG_MBPR;
+        r = be.decode_attention<__hip_bfloat16>(bp);
+        CHECK(!r.has_value() && r.error() == ErrorCode::InvalidArgument);
+        l = launch_decode_attention(bq, bk, bv, dbt, dctx, o2, BIG_B, BIG_MBPR, HQ, HKV, D, BS,
+                                    nullptr);
+        CHECK(!l.has_value() && l.error() == ErrorCode::InvalidArgument);
+    }
+
+    // Decode: backend (own stream + workspace) vs reference-signature launcher.
+    r = be.decode_attention<__hip_bfloat16>(dp);
     CHECK(r.has_value());
     CHECK(be.synchronize().has_value());
-    auto l = launch_decode_attention(bq, bk, bv, dbt, dctx, o2, B, MBPR, HQ, HKV, D, BS, nullptr);
+    l = launch_decode_attention(bq, bk, bv, dbt, dctx, o2, B, MBPR, HQ, HKV, D, BS, nullptr);
     CHECK(l.has_value());
     CHECK(hipDeviceSynchronize() == hipSuccess);
     CHECK(dev_download(reinterpret_cast<uint16_t*>(o1), hq.size()) ==
           dev_download(reinterpret_cast<uint16_t*>(o2), hq.size()));
+
+    // The backend decode captured in a HIP graph (its ops allocate nothing): every replay,
+    // with eager work and synchronisations between, equals the eager result bit for bit.
+    {
+        const auto want = dev_download(reinterpret_cast<uint16_t*>(o1), hq.size());
+        __hip_bfloat16* og = nullptr;
+        CHECK(hipMalloc(&og, hq.size() * 2) == hipSuccess);
+        DecodeAttnParams gp = dp;
+        gp.output_ = og;
+        hipGraph_t graph = nullptr;
+        hipGraphExec_t exec = nullptr;
+        CHECK(hipStreamBeginCapture(be.stream(), hipStreamCaptureModeGlobal) == hipSuccess);
+        r = be.decode_attention<__hip_bfloat16>(gp);
+        CHECK(r.has_value());
+        CHECK(hipStreamEndCapture(be.stream(), &graph) == hipSuccess);
+        CHECK(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) == hipSuccess);
+        for (int rep = 0; rep < 3; ++rep) {
+            CHECK(hipMemset(og, 0xff, hq.size() * 2) == hipSuccess);
+            CHECK(hipGraphLaunch(exec, be.stream()) == hipSuccess);
+            CHECK(be.synchronize().has_value());
+            CHECK(dev_download(reinterpret_cast<uint16_t*>(og), hq.size()) == want);
+            // eager work between replays, on the same stream and workspace
+            CHECK(be.decode_attention<__hip_bfloat16>(dp).has_value());
+            CHECK(be.synchronize().has_value());
+        }
+        CHECK(hipGraphExecDestroy(exec) == hipSuccess);
+        CHECK(hipGraphDestroy(graph) == hipSuccess);
+        CHECK(hipFree(og) == hipSuccess);
+    }
 
     // Prefill of 3 requests (qlen 20, 1, 64) both ways.
     std::vector<int32_t> qsl = {0, 20, 21, 85}, pctx = {60, 700, 64};
@@ -209,6 +289,12 @@ static void gpu_checks() {
     auto*ductx = dev_upload(uctx);
     __hip_bfloat16* uo = nullptr;
     CHECK(hipMalloc(&uo, uq.size() * 2) == hipSuccess);
+    // another head shape on the same stream: the reservation grows to cover it
+    CHECK(reserve_launcher_workspace(
+              nullptr, AttnWorkspaceLimits{.max_batch_size = 2, .max_query_tokens = 2,
+                                           .max_blocks_per_req = 2, .num_q_heads = 4,
+                                           .num_kv_heads = 4, .head_dim = 64})
+              .has_value());
     l = launch_decode_attention(reinterpret_cast<const __hip_bfloat16*>(duq),
                                 reinterpret_cast<const __hip_bfloat16*>(duk),
                                 reinterpret_cast<const __hip_bfloat16*>(duv), dubt, ductx, uo, 2,

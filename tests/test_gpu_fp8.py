@@ -15,6 +15,11 @@ pytestmark = pytest.mark.gpu
 BS = 16
 
 
+def bf(x):
+    """One float as a bf16 bit pattern (numpy scalar)."""
+    return oracle.f32_to_bf16(np.array([x], np.float32))[0]
+
+
 def rnd_bf16(rng, shape, scale=1.0):
     return oracle.f32_to_bf16((rng.standard_normal(shape) * scale).astype(np.float32))
 
@@ -27,13 +32,15 @@ def test_write_bit_exact(gpu, hkv, d):
     k = rnd_bf16(rng, (t, hkv, d), 2.0)
     v = rnd_bf16(rng, (t, hkv, d), 1e-3)
     k[4] = 0                                       # all-zero rows: scale 0
-    v[6, 0, 1] = oracle.f32_to_bf16(np.float32(1e30))   # one huge element
+    v[6, 0, 1] = bf(1e30)                          # one huge element
+    v[12, 0, 2] = bf(np.inf)                       # infinities: scale 2^126, code 448
+    v[13, :, 0] = bf(-np.inf)
     # scale boundaries: amax exactly 448 (scale 1), just above (scale 2), tiny (2^-126)
-    k[7] = oracle.f32_to_bf16(np.float32(0.5))
-    k[7, :, 3] = oracle.f32_to_bf16(np.float32(448.0))
-    k[8] = oracle.f32_to_bf16(np.float32(-1.0))
-    k[8, :, 5] = oracle.f32_to_bf16(np.float32(-450.0))
-    k[10] = oracle.f32_to_bf16(np.float32(2e-38))
+    k[7] = bf(0.5)
+    k[7, :, 3] = bf(448.0)
+    k[8] = bf(-1.0)
+    k[8, :, 5] = bf(-450.0)
+    k[10] = bf(2e-38)
     sm = rng.permutation(slots)[:t].astype(np.int32)
     sm[2], sm[9] = -1, slots + 4                   # skipped
     nsc = fp8_scale_numel(slots, hkv)

@@ -200,4 +200,19 @@ def test_row_scale_boundaries():
         ks = np.zeros(16 * hkv, np.float32)
         oracle.write_kv_cache_fp8(k, k, kc, kc.copy(), ks, ks.copy(), np.array([0], np.int32))
         assert ks[0] == want, (amax, ks[0])
-        assert amax_b <= 448 * ks[0] and (amax_b > 224 * ks[0] or ks[0] == 2.0 ** -126)
+        sc = float(ks[0])
+        assert amax_b <= 448 * sc and (amax_b > 224 * sc or sc == 2.0 ** -126)
+
+
+def test_row_with_an_infinity():
+    # scale 2^126: the infinities store as +-448 (codes 0x7e / 0xfe) and dequantise to +-inf
+    # in bf16 (448 * 2^126 is past bf16's largest finite value); finite elements store as 0
+    hkv, d = 1, 4
+    x = np.array([[[np.inf, 3.0, -np.inf, -2.0]]], np.float32)
+    k = oracle.f32_to_bf16(x)
+    kc = np.full((16, hkv, d), 0x55, np.uint8)
+    ks = np.zeros(16 * hkv, np.float32)
+    oracle.write_kv_cache_fp8(k, k, kc, kc.copy(), ks, ks.copy(), np.array([0], np.int32))
+    assert ks[0] == 2.0 ** 126
+    assert kc[0, 0].tolist() == [0x7E, 0x00, 0xFE, 0x80]
+    assert 448.0 * float(ks[0]) > 3.3961e38  # beyond bf16's largest finite value

@@ -87,3 +87,47 @@ def test_no_alloc_decode_under_graph_capture(gpu):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager), rep
+
+
+_FIRST_CALL_IN_CAPTURE = r"""
+import sys, torch
+sys.path.insert(0, sys.argv[1])
+from ccinfer_amd import _lib
+from ccinfer_amd import workloads as W
+from tests.test_zz_no_alloc import _no_alloc, _with_workspace
+dev = torch.device("cuda:0")
+lib = _lib.load()
+w = W.decode_batched(device=dev, seed=54, batch=24, ctx_hi=2500, with_write=False)
+meta = w.device_meta(dev)
+out = torch.full_like(w.q, float("nan"))
+want = torch.full_like(w.q, float("nan"))
+s = torch.cuda.Stream()
+s.wait_stream(torch.cuda.current_stream())
+torch.cuda.synchronize()
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph, stream=s):
+    rc = _no_alloc(lib, w, meta, out, s.cuda_stream)   # the process's first no-alloc call
+assert rc == 0, rc
+_with_workspace(lib, w, meta, want, torch.cuda.current_stream().cuda_stream)
+torch.cuda.synchronize()
+for rep in range(3):
+    out.fill_(float("nan"))
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, want), rep
+print("ok")
+"""
+
+
+def test_no_alloc_first_call_under_capture(gpu):
+    """The scratch address is resolved by the first call; here that call is made while the
+    stream is being captured, in a fresh process (so nothing resolved it earlier)."""
+    import subprocess
+    import sys
+    from pathlib import Path
+    say("no-alloc first call inside graph capture (fresh process)")
+    root = str(Path(__file__).resolve().parent.parent)
+    res = subprocess.run([sys.executable, "-c", _FIRST_CALL_IN_CAPTURE, root],
+                         capture_output=True, text=True, timeout=150, cwd=root)
+    assert res.returncode == 0 and "ok" in res.stdout, res.stdout[-2000:] + res.stderr[-2000:]
