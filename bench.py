@@ -1,6 +1,6 @@
 """Benchmark of the paged-attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5,6,7,8] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5,6,7,8,9] [--no-cpu]
 
 One "step" is one pass of the hot path over one batch of synthetic input already resident in
 HBM. The headline (the JSON `value`) is BASELINE.json's decode metric on configs[1]: batched
@@ -512,6 +512,39 @@ def run(args):
         out["8_fp8_prefill_8x(512+1536)"] = r
         del w, kc, vc, ks, vs
 
+    if 9 in configs:
+        # shared cached prompts: 64 requests on one 2048-token prefix + U[128, 1024] private
+        # tokens (prefix-cache hits), through the shared-prefix entry and through plain
+        # decode; bytes = every request's positions (the plain decode's algorithmic bytes)
+        # and the distinct positions (each prefix once)
+        lib = _lib.load()
+        for key, groups in (("9_decode_shared_b64_1x2048+128-1024", 1),
+                            ("9_decode_shared_b64_4x2048+128-1024", 4)):
+            w = W.decode_shared_prefix(device=dev, groups=groups)
+            meta = w.device_meta(dev)
+            outp = torch.empty_like(w.q)
+            n = lib.ccinfer_decode_shared_workspace_size(w.batch, w.mbpr, w.hq, w.hkv, w.d, 16)
+            ws = torch.zeros(max(1, n), dtype=torch.uint8, device=dev)
+
+            def shared_call(w=w, meta=meta, outp=outp, n=n, ws=ws):
+                rc = lib.ccinfer_decode_attention_shared_prefix(
+                    w.q.data_ptr(), w.k_cache.data_ptr(), w.v_cache.data_ptr(),
+                    meta["block_table"].data_ptr(), meta["context_lens"].data_ptr(),
+                    outp.data_ptr(), w.batch, w.mbpr, w.hq, w.hkv, w.d, 16, ws.data_ptr(), n,
+                    stream.cuda_stream)
+                assert rc == 0, rc
+            ms, host_ms = time_loop(shared_call, args.steps, args.warmup, stream)
+            plain_ms, _ = time_loop(Ops(w, dev, stream).decode, args.steps, args.warmup, stream)
+            uniq = w.info["unique_kv_bytes"]
+            r = {"ms_per_step": ms, "host_ms_per_step": host_ms, "plain_decode_ms": plain_ms,
+                 "kv_bytes": w.kv_bytes(), "unique_kv_bytes": uniq,
+                 "kv_GBps": w.kv_bytes() / (ms * 1e-3) / 1e9,
+                 "unique_GBps": uniq / (ms * 1e-3) / 1e9,
+                 "plain_kv_GBps": w.kv_bytes() / (plain_ms * 1e-3) / 1e9}
+            r["unique_hbm_frac"] = r["unique_GBps"] * 1e9 / HBM_PEAK
+            out[key] = r
+            del w, ws
+
     torch.cuda.synchronize()
     if not args.no_cpu:
         for f in deferred:
@@ -539,6 +572,26 @@ def profile(op: str, iters: int) -> None:
         w = W.decode_batched(device=dev, seed=5, batch=batch, ctx_lo=lo, ctx_hi=hi, hq=32,
                              hkv=8, with_write=False)
         fn = Ops(w, dev, stream).decode
+    elif op in ("decode_shared", "decode_unshared"):
+        # 64 requests on one 2048-token cached prompt + U[128, 1024] private tokens, through
+        # the shared-prefix entry or plain decode
+        w = W.decode_shared_prefix(device=dev)
+        ops = Ops(w, dev, stream)
+        if op == "decode_shared":
+            lib = _lib.load()
+            meta = w.device_meta(dev)
+            n = lib.ccinfer_decode_shared_workspace_size(w.batch, w.mbpr, w.hq, w.hkv, w.d, 16)
+            ws = torch.zeros(max(1, n), dtype=torch.uint8, device=dev)
+
+            def fn():
+                rc = lib.ccinfer_decode_attention_shared_prefix(
+                    w.q.data_ptr(), w.k_cache.data_ptr(), w.v_cache.data_ptr(),
+                    meta["block_table"].data_ptr(), meta["context_lens"].data_ptr(),
+                    ops.out.data_ptr(), w.batch, w.mbpr, w.hq, w.hkv, w.d, 16, ws.data_ptr(),
+                    n, stream.cuda_stream)
+                assert rc == 0, rc
+        else:
+            fn = ops.decode
     elif op in ("shared_prefix", "private_prefix"):
         # 16 sequences x (4096 cached + 256 new): one prefix shared by all, or 16 copies
         share = tuple((i, 0) for i in range(1, 16)) if op == "shared_prefix" else ()
@@ -647,13 +700,14 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--configs", default="1,2,3,4,5,6,7,8")
+    ap.add_argument("--configs", default="1,2,3,4,5,6,7,8,9")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=5.0)
     ap.add_argument("--sweep", choices=("decode", "prefill"),
                     help="print a table of the op across shapes and exit")
     ap.add_argument("--profile-op", choices=["decode", "write", "prefill", "mixed", "long",
                                              "decode_b600", "decode_b2048",
+                                             "decode_shared", "decode_unshared",
                                              "prologue", "shared_prefix", "private_prefix",
                                              "shared_prefix_ragged", "private_prefix_ragged",
                                              "copy"], default=None)

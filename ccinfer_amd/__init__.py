@@ -12,7 +12,9 @@ from .ops import (  # noqa: F401
     build_batch_metadata,
     decode_attention,
     decode_attention_fp8,
+    decode_attention_shared_prefix,
     decode_attention_write_kv,
+    decode_shared_workspace_size,
     decode_workspace_size,
     prefill_attention,
     prefill_attention_fp8,
@@ -31,7 +33,9 @@ __all__ = [
     "build_batch_metadata",
     "decode_attention",
     "decode_attention_fp8",
+    "decode_attention_shared_prefix",
     "decode_attention_write_kv",
+    "decode_shared_workspace_size",
     "decode_workspace_size",
     "prefill_attention",
     "prefill_attention_fp8",

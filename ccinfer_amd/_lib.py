@@ -26,6 +26,11 @@ SIGNATURES = {
         _c_int,
         [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _c_size, _vp],
     ),
+    "ccinfer_decode_shared_workspace_size": (_c_size, [_c_int] * 6),
+    "ccinfer_decode_attention_shared_prefix": (
+        _c_int,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _c_size, _vp],
+    ),
     "ccinfer_decode_attention_write_kv": (
         _c_int, [_vp] * 8 + [_c_int] * 7 + [_vp, _c_size, _vp]),
     "ccinfer_decode_attention_noalloc": (

@@ -325,6 +325,50 @@ int ccinfer_decode_attention(const void* q, const void* k_cache, const void* v_c
                         0);
 }
 
+size_t ccinfer_decode_shared_workspace_size(int batch_size, int max_blocks_per_req,
+                                            int num_q_heads, int num_kv_heads, int head_dim,
+                                            int cache_block_size) {
+    const size_t plain = ccinfer_decode_workspace_size(batch_size, max_blocks_per_req,
+                                                       num_q_heads, num_kv_heads, head_dim,
+                                                       cache_block_size);
+    if (!decode_shape_ok(batch_size, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
+                         cache_block_size) ||
+        !decode_shared_supported(batch_size, num_q_heads, num_kv_heads, head_dim,
+                                 cache_block_size))
+        return plain;
+    return std::max(plain, decode_shared_workspace_bytes(batch_size, max_blocks_per_req,
+                                                         num_q_heads, num_kv_heads, head_dim));
+}
+
+int ccinfer_decode_attention_shared_prefix(const void* q, const void* k_cache,
+                                           const void* v_cache, const int32_t* block_table,
+                                           const int32_t* context_lens, void* output,
+                                           int batch_size, int max_blocks_per_req,
+                                           int num_q_heads, int num_kv_heads, int head_dim,
+                                           int cache_block_size, void* workspace,
+                                           size_t workspace_bytes, void* stream) {
+    if (!q || !k_cache || !v_cache || !block_table || !context_lens || !output)
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    if (!decode_shape_ok(batch_size, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
+                         cache_block_size))
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    const bool shared = decode_shared_supported(batch_size, num_q_heads, num_kv_heads,
+                                                head_dim, cache_block_size) &&
+                        fast_aligned(q, k_cache, v_cache, output);
+    if (!shared)
+        return decode_entry(q, k_cache, v_cache, block_table, context_lens, output, batch_size,
+                            max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
+                            cache_block_size, workspace, workspace_bytes, stream, nullptr,
+                            nullptr, 0);
+    const size_t need = ccinfer_decode_shared_workspace_size(
+        batch_size, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim, cache_block_size);
+    if (workspace == nullptr || workspace_bytes < need) return CCINFER_ERR_INVALID_ARGUMENT;
+    return map_hip_error(decode_attention_shared(q, k_cache, v_cache, block_table, context_lens,
+                                                 output, batch_size, max_blocks_per_req,
+                                                 num_q_heads, num_kv_heads, head_dim, workspace,
+                                                 as_stream(stream)));
+}
+
 int ccinfer_decode_attention_write_kv(const void* q, const void* k_new, const void* v_new,
                                       void* k_cache, void* v_cache, const int32_t* block_table,
                                       const int32_t* context_lens, void* output, int batch_size,

@@ -91,7 +91,20 @@ struct ItemArgs {
     const __bf16* new_k;
     const __bf16* new_v;
     int max_slots;
+    // Shared-prefix decode (decode_attention_shared): the first position each item attends
+    // to here (a multiple of kChunk; nullptr: 0), and the number of partials of the item's
+    // rows that the shared-prefix kernel wrote for positions before it (nullptr: none). Such
+    // rows always go through the merge, which adds those partials.
+    const int32_t* begin;
+    const int32_t* sh_splits;
 };
+
+__device__ __forceinline__ int item_first(const ItemArgs& it, int item) {
+    return it.begin != nullptr ? it.begin[item] : 0;
+}
+__device__ __forceinline__ int item_shared(const ItemArgs& it, int item) {
+    return it.sh_splits != nullptr ? it.sh_splits[item] : 0;
+}
 
 // Per (item, q_head) row: how many splits its partials span and where they start. Written
 // by split 0 of the row's kv_head group on every launch; the merge reads it instead of
@@ -211,18 +224,21 @@ __device__ __forceinline__ bool flat_segment(const int32_t* __restrict__ context
     const int rounds = (B + 63) / 64;  // B <= kFlatMaxItems
     int cr[kFlatMaxItems / 64];
     int ectx[kFlatMaxItems / 64];
+    int bx[kFlatMaxItems / 64];
     int total = 0;
 #pragma unroll
     for (int x = 0; x < kFlatMaxItems / 64; ++x) {
         cr[x] = 0;
         ectx[x] = -1;
+        bx[x] = 0;
         if (x < rounds) {
             const int r = x * 64 + lane;
             if (r < B) {
                 const int req = items.item_req != nullptr ? items.item_req[r] : r;
                 const int ctx = effective_ctx(context_lens[req], mbpr, items.zero_invalid);
                 ectx[x] = ctx;
-                cr[x] = ctx > 0 ? (ctx + kChunk - 1) / kChunk : 0;
+                bx[x] = item_first(items, r);
+                cr[x] = ctx > 0 ? (ctx - bx[x] + kChunk - 1) / kChunk : 0;
             }
             total += cr[x];
         }
@@ -259,9 +275,10 @@ __device__ __forceinline__ bool flat_segment(const int32_t* __restrict__ context
             out->ctx = __builtin_amdgcn_readlane(ectx[x], src);
             out->nsplit = __builtin_amdgcn_readlane(nsr, src);
             out->first_slot = __builtin_amdgcn_readlane(sr, src);
+            const int b0 = __builtin_amdgcn_readlane(bx[x], src);
             out->split = w - ps / T;
-            out->begin = (max(lo, ps) - ps) * kChunk;
-            out->end = min(out->ctx, (min(hi, ps + cs) - ps) * kChunk);
+            out->begin = b0 + (max(lo, ps) - ps) * kChunk;
+            out->end = min(out->ctx, b0 + (min(hi, ps + cs) - ps) * kChunk);
             out->more = ps + cs < hi;
             return true;
         }
@@ -306,7 +323,7 @@ __device__ __forceinline__ int item_chunks(const int32_t* __restrict__ context_l
     const int req = items.item_req != nullptr ? items.item_req[r] : r;
     const int ctx = effective_ctx(context_lens[req], mbpr, items.zero_invalid);
     *ectx = ctx;
-    return ctx > 0 ? (ctx + kChunk - 1) / kChunk : 0;
+    return ctx > 0 ? (ctx - item_first(items, r) + kChunk - 1) / kChunk : 0;
 }
 
 // Exclusive prefix sum of v over the 1024 threads of the block (s_part: 16 ints of LDS);
@@ -497,9 +514,10 @@ __device__ __forceinline__ bool flat_segment_indexed(const int32_t* __restrict__
         out->ctx = __builtin_amdgcn_readfirstlane(e);
         out->nsplit = __builtin_amdgcn_readfirstlane(x.S[r + 1]) - s0;
         out->first_slot = s0;
+        const int b0 = __builtin_amdgcn_readfirstlane(item_first(items, r));
         out->split = w - __builtin_amdgcn_readfirstlane(x.V[r]);
-        out->begin = (max(lo, p) - p) * kChunk;
-        out->end = min(out->ctx, (min(hi, p + c) - p) * kChunk);
+        out->begin = b0 + (max(lo, p) - p) * kChunk;
+        out->end = min(out->ctx, b0 + (min(hi, p + c) - p) * kChunk);
         out->more = p + c < hi;
         return true;
     }
@@ -849,6 +867,68 @@ __device__ void merge_row(const float* __restrict__ ws_o, const float* __restric
         if (lane * kPer + x < dr) o[lane * kPer + x] = static_cast<__bf16>(acc[x] * inv);
 }
 
+// Log-sum-exp merge of a row whose partials sit in two lists: ns split partials at `base`
+// of the workspace and sn shared-prefix partials at `sbase` of the shared area (the rows of
+// decode_attention_shared). A plain loop: these rows are few per launch.
+template <int D>
+__device__ void merge_row_two(const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
+                              int64_t base, int ns, const float* __restrict__ sh_o,
+                              const float* __restrict__ sh_ml, int64_t sbase, int sn,
+                              float eps, __bf16* __restrict__ o, int lane, int dr) {
+    constexpr int kPer = D / 64;
+    constexpr int kBatch = 8;
+    const int n = ns + sn;
+    auto row = [&](int t) {
+        return t < ns ? ws_o + (base + t) * D : sh_o + (sbase + t - ns) * D;
+    };
+    auto ml = [&](int t, int w) {
+        return t < ns ? ws_ml[(base + t) * 2 + w] : sh_ml[(sbase + t - ns) * 2 + w];
+    };
+    float mmax = kNegInf;
+    for (int t = lane; t < n; t += 64) mmax = fmaxf(mmax, ml(t, 0));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, off));
+    float acc[kPer];
+#pragma unroll
+    for (int x = 0; x < kPer; ++x) acc[x] = 0.f;
+    float lsum = 0.f;
+    if (mmax != kNegInf) {
+        for (int tb = 0; tb < n; tb += 64) {
+            // lane t: the weight of partial tb + t
+            const int t = tb + lane;
+            float w = 0.f;
+            if (t < n) {
+                w = __builtin_amdgcn_exp2f(ml(t, 0) - mmax);
+                lsum += ml(t, 1) * w;
+            }
+            const int nt = min(64, n - tb);
+            for (int t0 = 0; t0 < nt; t0 += kBatch) {
+                float v[kBatch][kPer];
+#pragma unroll
+                for (int u = 0; u < kBatch; ++u) {  // clamped: a repeat's weight is 0
+                    const float* po = row(tb + min(t0 + u, nt - 1)) + lane * kPer;
+#pragma unroll
+                    for (int x = 0; x < kPer; ++x) v[u][x] = po[x];
+                }
+#pragma unroll
+                for (int u = 0; u < kBatch; ++u) {
+                    const float wt = t0 + u < nt ? __int_as_float(__builtin_amdgcn_readlane(
+                                                       __float_as_int(w), t0 + u))
+                                                 : 0.f;
+#pragma unroll
+                    for (int x = 0; x < kPer; ++x) acc[x] += v[u][x] * wt;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) lsum += __shfl_xor(lsum, off);
+    const float inv = lsum > 0.f ? 1.f / (lsum + eps) : 0.f;
+#pragma unroll
+    for (int x = 0; x < kPer; ++x)
+        if (lane * kPer + x < dr) o[lane * kPer + x] = static_cast<__bf16>(acc[x] * inv);
+}
+
 // Per-split inputs: the split's block ids, one per lane (two registers cover 128 blocks),
 // and the Q^T operand: lane (head j, grp g) holds dims (kk*4+g)*8 .. +8 of head j (fp8:
 // the permuted order of the fp8 K loads).
@@ -936,10 +1016,266 @@ __device__ __forceinline__ void run_split(
     }
 }
 
+// ---- shared-prefix decode (decode_attention_shared) ----
+// Requests whose block-table rows start with the same block ids hold one cached prompt
+// prefix in common (the reference counts such prefix-cache hits in BlockTable::shared_count,
+// src/cache/block.h:85-97, when KVCacheManager::lookup_prefix_cache reuses the blocks,
+// src/cache/kv_cache_manager.cpp:93-173). A planner groups them on the device by their first
+// block id; a group's common prefix -- the leading block ids all members share, cut to whole
+// 32-token chunks and to before every member's last position -- is attended once per
+// subgroup of up to 16 / G members, whose G query heads each fill the 16 columns of the
+// decode MFMA tile together (one request alone uses G of them), so each K/V byte of the
+// prefix is read once per subgroup instead of once per request. Each member's positions from
+// the end of the prefix on run through the ordinary split plan (items start there), and the
+// merge adds the prefix partials to the row. Requests in no group run as in plain decode.
+constexpr int kSharedSplitTokens = 128;   // prefix positions per shared-kernel wavefront
+constexpr int kSharedMinTokens = 64;      // shorter common prefixes are not worth a subgroup
+constexpr int kSharedMaxItems = 2048;     // the planner's hash table holds 2x this many keys
+constexpr int kSharedHash = 4096;
+constexpr int kSharedCols = 16;           // columns of the 16x16x32 MFMA tile
+#ifndef CCI_SH_SLOTS
+#define CCI_SH_SLOTS 128
+#endif
+#ifndef CCI_SH_W2
+#define CCI_SH_W2 0
+#endif
+constexpr int kSharedSlotsPerHead = CCI_SH_SLOTS;  // shared-kernel wavefronts per kv head
+
+struct SharedPlan {
+    int32_t* nsub;      // [1] subgroups
+    int32_t* sub_len;   // [B] prefix positions of subgroup s
+    int32_t* sub_n;     // [B] members of subgroup s
+    int32_t* sub_mem;   // [B][16] its members (items)
+    int32_t* begin;     // [B] first position item r attends in the split plan
+    int32_t* sh_splits; // [B] prefix partials of item r's rows
+};
+
+__global__ __launch_bounds__(1024) void decode_shared_plan_kernel(
+    const int32_t* __restrict__ block_table, const int32_t* __restrict__ context_lens, int B,
+    int mbpr, int M, SharedPlan sp) {
+    __shared__ int h_key[kSharedHash];
+    __shared__ int h_lead[kSharedHash];
+    __shared__ int h_count[kSharedHash];
+    __shared__ int h_minctx[kSharedHash];
+    __shared__ int h_common[kSharedHash];
+    __shared__ int h_base[kSharedHash];
+    __shared__ int h_slot[kSharedMaxItems];  // each request's hash slot (-1: not grouped)
+    __shared__ int s_nsub;
+    constexpr int kPer = kSharedMaxItems / 1024;
+    const int tid = threadIdx.x;
+    for (int i = tid; i < kSharedHash; i += 1024) {
+        h_key[i] = -1;
+        h_lead[i] = 0x7fffffff;
+        h_count[i] = 0;
+        h_minctx[i] = 0x7fffffff;
+        h_common[i] = 0x7fffffff;
+        h_base[i] = 0;  // the fill counter until the subgroups are numbered
+    }
+    if (tid == 0) s_nsub = 0;
+    __syncthreads();
+    // 1. hash every eligible request on its first block id (decode semantics: a row whose
+    //    context is invalid writes zeros and is never grouped)
+    int slot[kPer];
+#pragma unroll
+    for (int x = 0; x < kPer; ++x) {
+        slot[x] = -1;
+        const int r = tid + 1024 * x;
+        if (r >= B) continue;
+        sp.begin[r] = 0;
+        sp.sh_splits[r] = 0;
+        const int ctx = context_lens[r];
+        const int key = ctx > kSharedMinTokens && (ctx + kBlock - 1) / kBlock <= mbpr
+                            ? block_table[static_cast<int64_t>(r) * mbpr]
+                            : -1;
+        if (key < 0) continue;
+        int h = static_cast<int>((static_cast<uint32_t>(key) * 2654435761u) >> 20) &
+                (kSharedHash - 1);
+        for (;;) {
+            const int prev = atomicCAS(&h_key[h], -1, key);
+            if (prev == -1 || prev == key) break;
+            h = (h + 1) & (kSharedHash - 1);
+        }
+        atomicMin(&h_lead[h], r);
+        atomicAdd(&h_count[h], 1);
+        atomicMin(&h_minctx[h], ctx);
+        slot[x] = h;
+    }
+    __syncthreads();
+    // 2. each member's run of block ids equal to the group leader's, within the blocks that
+    //    lie wholly before the shortest member's last position: one wavefront per request,
+    //    64 ids per step, the first mismatch found by a ballot
+#pragma unroll
+    for (int x = 0; x < kPer; ++x) h_slot[tid + 1024 * x] = slot[x];
+    __syncthreads();
+    {
+        // four requests per wavefront at a time, so their loads are in flight together
+        constexpr int U = 4;
+        const int lane = tid & 63;
+        for (int r0 = (tid >> 6) * U; r0 < B; r0 += 16 * U) {
+            int h[U], nb[U], cb[U], lead[U];
+            int nbmax = 0;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int r = r0 + u;
+                h[u] = r < B ? h_slot[r] : -1;
+                const bool grouped = h[u] >= 0 && h_count[h[u]] >= 2;
+                nb[u] = grouped ? (h_minctx[h[u]] - 1) / kBlock : 0;
+                lead[u] = grouped ? h_lead[h[u]] : 0;
+                cb[u] = nb[u];
+                nbmax = max(nbmax, nb[u]);
+            }
+            // 128 ids per step (two per lane), all loads of a step in flight together
+            for (int j0 = 0; j0 < nbmax; j0 += 128) {
+                bool diff[U][2];
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int32_t* a = block_table + static_cast<int64_t>(r0 + u) * mbpr;
+                    const int32_t* b = block_table + static_cast<int64_t>(lead[u]) * mbpr;
+#pragma unroll
+                    for (int hx = 0; hx < 2; ++hx) {
+                        const int j = j0 + 64 * hx + lane;
+                        const bool in = j < cb[u];
+                        diff[u][hx] = in && a[in ? j : 0] != b[in ? j : 0];
+                    }
+                }
+                bool more = false;
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+#pragma unroll
+                    for (int hx = 1; hx >= 0; --hx) {  // the lower half's mismatch wins
+                        const uint64_t d = __builtin_amdgcn_ballot_w64(diff[u][hx]);
+                        if (d != 0)
+                            cb[u] = min(cb[u], j0 + 64 * hx +
+                                                   __builtin_ffsll(static_cast<long long>(d)) - 1);
+                    }
+                    more = more || cb[u] > j0 + 128;
+                }
+                if (!more) break;  // wave-uniform
+            }
+            if (lane == 0) {
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+                    if (nb[u] > 0) atomicMin(&h_common[h[u]], cb[u]);
+            }
+        }
+    }
+    __syncthreads();
+    // 3. groups with a long enough common prefix get ceil(count / M) subgroups
+    for (int i = tid; i < kSharedHash; i += 1024) {
+        if (h_key[i] < 0 || h_count[i] < 2) continue;
+        const int len = min(h_common[i] * kBlock, h_minctx[i] - 1) / kChunk * kChunk;
+        if (len < kSharedMinTokens) {
+            h_count[i] = 0;
+            continue;
+        }
+        h_common[i] = len;
+        h_lead[i] = atomicAdd(&s_nsub, (h_count[i] + M - 1) / M);  // first subgroup
+    }
+    __syncthreads();
+    // 4. members into subgroups (in arrival order: a member's result does not depend on its
+    //    column or on the other members of its subgroup)
+#pragma unroll
+    for (int x = 0; x < kPer; ++x) {
+        const int r = tid + 1024 * x;
+        const int h = slot[x];
+        if (h < 0 || h_count[h] < 2) continue;
+        const int i = atomicAdd(&h_base[h], 1);
+        const int sub = h_lead[h] + i / M;
+        const int len = h_common[h];
+        sp.sub_mem[sub * kSharedCols + i % M] = r;
+        sp.begin[r] = len;
+        sp.sh_splits[r] = (len + kSharedSplitTokens - 1) / kSharedSplitTokens;
+        if (i % M == 0) {
+            sp.sub_len[sub] = len;
+            sp.sub_n[sub] = min(M, h_count[h] - (i / M) * M);
+        }
+    }
+    if (tid == 0) *sp.nsub = s_nsub;
+}
+
+// Prefix attention of the subgroups: each wavefront takes work items (128-position piece,
+// kv head h, subgroup) in turn. Lane column j holds
+// member j / G's query head h G + j % G; the partial (O, m, l) of each member row goes to
+// the shared area at ((member * Hq + head) * k + piece).
+// Runs in the split kernel's extra workgroups (wg of nwg), beside the split work, which
+// needs the same inputs and nothing from it.
+template <int D, bool kPad>
+__device__ __forceinline__ void shared_prefix_work(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ k_cache,
+    const __bf16* __restrict__ v_cache, const int32_t* __restrict__ block_table,
+    const SharedPlan& sp, float* __restrict__ sh_o, float* __restrict__ sh_ml, int mbpr, int hq,
+    int hkv, int sh_k, float scale_log2, int dr, int wg_raw, int nwg) {
+    constexpr int S = DecodeShape<D>::kSteps;
+    constexpr int NV = DecodeShape<D>::kNV;
+    const int ds = kPad ? dr : D;
+    const int lane = threadIdx.x & 63;
+    // Work item (piece, kv head, subgroup), subgroup fastest: the wavefronts of a workgroup
+    // read the same K/V rows (they hit in the CU's cache), and workgroups are renumbered so
+    // that consecutive ones run on one XCD (workgroups are dealt to the 8 XCDs in turn),
+    // keeping the subgroups of a piece in one L2.
+    // nwg: a multiple of 8; the split workgroups before these are a multiple of 8 too
+    const int wg = (wg_raw % 8) * (nwg / 8) + wg_raw / 8;
+    const int wi = wg * kWavesPerGroup + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int G = hq / hkv;
+    const int j = lane & 15;
+    const int g = lane >> 4;
+    const int nsub = *sp.nsub;
+    const int nwork = nsub * hkv * sh_k;
+    for (int w = wi; w < nwork; w += nwg * kWavesPerGroup) {
+        const int sub = w % nsub;
+        const int h = (w / nsub) % hkv;
+        const int piece = w / (nsub * hkv);
+        const int len = sp.sub_len[sub];
+        const int begin = piece * kSharedSplitTokens;
+        if (begin >= len) continue;  // wave-uniform
+        const int end = min(len, begin + kSharedSplitTokens);
+        const int nmem = sp.sub_n[sub];
+        const int32_t* mem = sp.sub_mem + sub * kSharedCols;
+        const int m = j / G;
+        const bool live = m < nmem;
+        const int r = mem[live ? m : 0];
+        const int head = h * G + j % G;
+        SplitInputs<D> in;
+        // block ids: any member's row (the prefix's ids are the same in all of them)
+        const int32_t* rb = block_table + static_cast<int64_t>(mem[0]) * mbpr;
+        const int lb0 = begin / kBlock;
+        const int nblk = (end - begin + kBlock - 1) / kBlock;
+        in.bt_lo = lane < nblk ? rb[lb0 + lane] : -1;
+        in.bt_hi = lane + 64 < nblk ? rb[lb0 + lane + 64] : -1;
+        const __bf16* qv = q + (static_cast<int64_t>(r) * hq + head) * ds;
+#pragma unroll
+        for (int kk = 0; kk < S; ++kk) {
+            const int dim0 = (kk * 4 + g) * 8;
+            const bool ok = !kPad || dim0 < dr;
+            u32x4 v = load16(qv + (ok ? dim0 : 0));
+            if (!live || !ok) v = u32x4{0, 0, 0, 0};
+            in.qop[kk] = __builtin_bit_cast(bf16x8, v);
+        }
+        SoftmaxState<D> st;
+        // cached loads (kTL): every subgroup of the group reads these blocks
+        run_split<D, false, kPad, true>(k_cache, v_cache, nullptr, nullptr, in, hkv, h, begin,
+                                        end, scale_log2, lane, st, dr);
+        const float l_tot = wave_sum_xor16_32(st.l);
+        if (live) {
+            const int64_t slot = (static_cast<int64_t>(r) * hq + head) * sh_k + piece;
+            float* po = sh_o + slot * D;
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+                for (int n = 0; n < NV; ++n) po[NV * (4 * g + rr) + n] = st.acc[n][rr];
+            if (g == 0) {
+                sh_ml[slot * 2 + 0] = st.m;
+                sh_ml[slot * 2 + 1] = l_tot;
+            }
+        }
+    }
+}
+
 // F8: the cache holds E4M3 bytes with row scales (k_scale / v_scale); else bf16.
 // kPad: head_dim dr < D (see load_chunk); q and output rows hold dr elements.
 // kTL: the K/V loads stay in L2 (see kv_load).
-template <int D, bool F8, bool kPad, bool kTL>
+// kShared: workgroups from split_wgs on run shared_prefix_work (decode_attention_shared).
+template <int D, bool F8, bool kPad, bool kTL, bool kShared = false>
 __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     const __bf16* __restrict__ q, void* k_cache_v, void* v_cache_v,
     const float* __restrict__ k_scale,
@@ -947,7 +1283,18 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     const int32_t* __restrict__ context_lens, __bf16* __restrict__ out, float* __restrict__ ws_o,
     float* __restrict__ ws_ml, MergeDesc* __restrict__ desc, ItemArgs items, int mbpr, int hq,
     int hkv, int splits, int split_tokens, int flat_w, int slots, float scale_log2, int dr,
-    int rep, const int32_t* __restrict__ flat_idx) {
+    int rep, const int32_t* __restrict__ flat_idx, SharedPlan sp, float* __restrict__ sh_o,
+    float* __restrict__ sh_ml, int sh_k, int split_wgs) {
+    if constexpr (kShared && !F8) {
+        if (static_cast<int>(blockIdx.x) >= split_wgs) {
+            shared_prefix_work<D, kPad>(q, static_cast<const __bf16*>(k_cache_v),
+                                        static_cast<const __bf16*>(v_cache_v), block_table, sp,
+                                        sh_o, sh_ml, mbpr, hq, hkv, sh_k, scale_log2, dr,
+                                        static_cast<int>(blockIdx.x) - split_wgs,
+                                        static_cast<int>(gridDim.x) - split_wgs);
+            return;
+        }
+    }
     const int ds = kPad ? dr : D;  // q / output row stride
     constexpr int NV = DecodeShape<D>::kNV;
     using Cache = std::conditional_t<F8, uint8_t, __bf16>;
@@ -1011,7 +1358,7 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     const float l_tot = wave_sum_xor16_32(st.l);
     const bool live = j < G;
     const int head = h * G + j;
-    if (ns == 1) {
+    if (ns == 1 && item_shared(items, item) == 0) {
         if (!live) return;
         const float inv = l_tot > 0.f ? 1.f / (l_tot + items.eps) : 0.f;
         __bf16* o = out + (static_cast<int64_t>(qrow) * hq + head) * ds;
@@ -1088,8 +1435,9 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     int req, qrow;
     if (!resolve_item(items, item, &req, &qrow)) return;
     const int ctx = effective_ctx(context_lens[req], mbpr, items.zero_invalid);
-    const int ns = ctx > 0 ? (ctx + split_tokens - 1) / split_tokens : 0;
-    const int begin = s * split_tokens;
+    const int b0 = item_first(items, item);
+    const int ns = ctx > 0 ? (ctx - b0 + split_tokens - 1) / split_tokens : 0;
+    const int begin = b0 + s * split_tokens;
     process(lane, item, s, ns, 0, ctx, begin, ctx > 0 ? min(ctx, begin + split_tokens) : 0);
 }
 
@@ -1212,7 +1560,8 @@ template <int D>
 __global__ __launch_bounds__(256) void decode_merge_kernel(
     __bf16* __restrict__ out, const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
     const MergeDesc* __restrict__ desc, ItemArgs items, int hq, int dr,
-    const int32_t* __restrict__ flat_idx, int slots) {
+    const int32_t* __restrict__ flat_idx, int slots, const float* __restrict__ sh_o,
+    const float* __restrict__ sh_ml, int sh_k) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wi = blockIdx.x * kWavesPerGroup + wave;
@@ -1227,6 +1576,13 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(
         // bf16 quiet-NaN bits (the build's -fno-honor-nans makes NaN arithmetic undefined)
         uint16_t* o = reinterpret_cast<uint16_t*>(out + (static_cast<int64_t>(qrow) * hq + head) * dr);
         for (int x = lane; x < dr; x += 64) o[x] = 0x7fc0u;
+        return;
+    }
+    const int sn = item_shared(items, item);
+    if (sn > 0) {
+        merge_row_two<D>(ws_o, ws_ml, d.base, static_cast<int>(d.ns), sh_o, sh_ml,
+                         (static_cast<int64_t>(req) * hq + head) * sh_k, sn, items.eps,
+                         out + (static_cast<int64_t>(qrow) * hq + head) * dr, lane, dr);
         return;
     }
     if (d.ns <= 1) return;  // invalid row, or written directly by the split kernel
@@ -1289,12 +1645,22 @@ constexpr int resident_waves() {
     return 1024 * (D <= 64 ? 3 : D <= 128 ? 2 : 1);
 }
 
+// The shared-prefix partials the merge adds to the rows of decode_attention_shared.
+struct SharedParts {
+    float* o = nullptr;   // [B][Hq][k][D]
+    float* ml = nullptr;  // [B][Hq][k][2]
+    int k = 0;            // partial slots per row
+    SharedPlan sp{};      // the planner's output
+    int nwg = 0;          // workgroups of the prefix work (a multiple of 8)
+};
+
 template <int D, bool F8, bool kPad>
 hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache,
                          const float* k_scale, const float* v_scale,
                          const int32_t* block_table, const int32_t* context_lens, void* output,
                          const ItemArgs& it, int mbpr, int hq, int hkv, const DecodePlan& plan,
-                         void* workspace, hipStream_t stream, int dr) {
+                         void* workspace, hipStream_t stream, int dr,
+                         const SharedParts& shared = SharedParts{}) {
     const float scale_log2 = kLog2e / sqrtf(static_cast<float>(dr));
     // Query groups larger than one MFMA N-tile run as `rep` virtual kv heads of hq / hkv /
     // rep query heads each; virtual head v reads cache head v / rep.
@@ -1321,7 +1687,7 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
                               ? static_cast<int64_t>(plan.slots) * hkv
                               : static_cast<int64_t>(it.num_items) * hkv * plan.splits;
     const int grid = static_cast<int>((waves + kWavesPerGroup - 1) / kWavesPerGroup);
-    const bool merge = plan.flat || plan.splits > 1;
+    const bool merge = plan.flat || plan.splits > 1 || shared.o != nullptr;
     DecodeWs w{};
     if (merge) w = carve(workspace, partial_rows(it.num_items, hq, plan), D, it.num_items, hq);
     if (plan.flat_index) {
@@ -1332,18 +1698,33 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
         if (ie != hipSuccess) return ie;
     }
     const int bw = plan.flat ? plan.wave_target : 0;
-    auto go = [&](auto tl_tag) {
-        decode_split_kernel<D, F8, kPad, decltype(tl_tag)::value><<<grid, 256, 0, stream>>>(
+    // Shared-prefix decode: the prefix work runs in extra workgroups of the same launch (the
+    // split part padded to a multiple of 8 workgroups so the prefix part starts on XCD 0).
+    const bool shr = shared.o != nullptr;
+    const int split_wgs = shr ? (grid + 7) / 8 * 8 : grid;
+    const int total_wgs = split_wgs + (shr ? shared.nwg : 0);
+    auto go = [&](auto tl_tag, auto sh_tag) {
+        decode_split_kernel<D, F8, kPad, decltype(tl_tag)::value, decltype(sh_tag)::value>
+            <<<total_wgs, 256, 0, stream>>>(
             static_cast<const __bf16*>(q), const_cast<void*>(k_cache), const_cast<void*>(v_cache),
             k_scale, v_scale, block_table, context_lens, static_cast<__bf16*>(output), w.o, w.ml,
             w.desc, it, mbpr, hq, hkv,
             plan.splits, plan.split_tokens, bw, plan.slots, scale_log2, dr, rep,
-            plan.flat_index ? w.index : nullptr);
+            plan.flat_index ? w.index : nullptr, shared.sp, shared.o, shared.ml, shared.k,
+            split_wgs);
     };
-    if (tl)
-        go(std::true_type{});
-    else if constexpr (!kPad)
-        go(std::false_type{});
+    if (shr) {
+        if constexpr (!F8) {
+            if (tl)
+                go(std::true_type{}, std::true_type{});
+            else if constexpr (!kPad)
+                go(std::false_type{}, std::true_type{});
+        }
+    } else if (tl) {
+        go(std::true_type{}, std::false_type{});
+    } else if constexpr (!kPad) {
+        go(std::false_type{}, std::false_type{});
+    }
     hipError_t err = hipGetLastError();
     if (err != hipSuccess || !merge) return err;
     const int64_t rows = static_cast<int64_t>(it.num_items) * hq;
@@ -1351,20 +1732,21 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
     decode_merge_kernel<D><<<mgrid, 256, 0, stream>>>(static_cast<__bf16*>(output), w.o, w.ml,
                                                       w.desc, it, hq, dr,
                                                       plan.flat_index ? w.index : nullptr,
-                                                      plan.slots);
+                                                      plan.slots, shared.o, shared.ml,
+                                                      shared.k);
     return hipGetLastError();
 }
 
 }  // namespace
 
 DecodePlan plan_decode(int num_items, int num_q_heads, int num_kv_heads, int max_ctx,
-                       bool allow_flat, bool fp8) {
+                       bool allow_flat, bool fp8, bool allow_group) {
     // Query groups above one MFMA N-tile run as several virtual kv heads (launch_decode).
     num_kv_heads *= decode_head_rep(num_q_heads / num_kv_heads);
     DecodePlan p;
     // Tiny batches: one workgroup per (request, kv_head) merges its parts in LDS (a single
     // launch; these batches are latency-bound).
-    if (static_cast<int64_t>(num_items) * num_q_heads <= kGroupMaxRows &&
+    if (allow_group && static_cast<int64_t>(num_items) * num_q_heads <= kGroupMaxRows &&
         max_ctx <= kGroupMaxCtx) {
         p.group = true;
         return p;
@@ -1525,6 +1907,120 @@ hipError_t decode_attention_fp8(const void* q, const void* k_cache, const void* 
         default:
             return hipErrorInvalidValue;
     }
+}
+
+// ---- shared-prefix decode ----
+namespace {
+
+struct SharedLayout {
+    DecodePlan plan;
+    size_t regular, plan_off, o_off, ml_off, total;
+    int k;
+};
+
+SharedLayout shared_layout(int B, int mbpr, int hq, int hkv, int head_dim) {
+    SharedLayout L{};
+    // the suffixes: plain decode's split plan (never the group plan, whose rows do not go
+    // through the merge), with the merge always on
+    L.plan = plan_decode(B, hq, hkv, mbpr * kBlock, true, CCI_SH_W2 != 0, false);
+    const int d = decode_mfma_dim(head_dim);
+    const size_t rows = partial_rows(B, hq, L.plan);
+    L.regular = L.plan.flat_index ? index_offset(rows, d, B, hq) + index_bytes(B, L.plan.slots)
+                                  : desc_offset(rows, d) +
+                                        static_cast<size_t>(B) * hq * sizeof(MergeDesc);
+    L.regular = (L.regular + 255) & ~static_cast<size_t>(255);
+    L.k = (mbpr * kBlock + kSharedSplitTokens - 1) / kSharedSplitTokens;
+    L.plan_off = L.regular;
+    const size_t plan_ints = 1 + static_cast<size_t>(B) * (3 + kSharedCols + 2);
+    L.o_off = (L.plan_off + plan_ints * sizeof(int32_t) + 255) & ~static_cast<size_t>(255);
+    const size_t parts = static_cast<size_t>(B) * hq * L.k;
+    L.ml_off = L.o_off + parts * d * sizeof(float);
+    L.total = L.ml_off + parts * 2 * sizeof(float);
+    return L;
+}
+
+template <int D, bool kPad>
+hipError_t launch_decode_shared(const void* q, const void* k_cache, const void* v_cache,
+                                const int32_t* block_table, const int32_t* context_lens,
+                                void* output, int B, int mbpr, int hq, int hkv, int dr,
+                                const SharedLayout& L, char* ws, hipStream_t stream) {
+    int32_t* pi = reinterpret_cast<int32_t*>(ws + L.plan_off);
+    SharedPlan sp;
+    sp.nsub = pi;
+    sp.sub_len = pi + 1;
+    sp.sub_n = sp.sub_len + B;
+    sp.begin = sp.sub_n + B;
+    sp.sh_splits = sp.begin + B;
+    sp.sub_mem = sp.sh_splits + B;
+    float* sh_o = reinterpret_cast<float*>(ws + L.o_off);
+    float* sh_ml = reinterpret_cast<float*>(ws + L.ml_off);
+    const int G = hq / hkv;
+    decode_shared_plan_kernel<<<1, 1024, 0, stream>>>(block_table, context_lens, B, mbpr,
+                                                      kSharedCols / G, sp);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    const int waves = kSharedSlotsPerHead * hkv;
+    const int nwg = ((waves + kWavesPerGroup - 1) / kWavesPerGroup + 7) / 8 * 8;
+    ItemArgs it{};
+    it.num_items = B;
+    it.eps = 1e-6f;
+    it.zero_invalid = 1;
+    it.begin = sp.begin;
+    it.sh_splits = sp.sh_splits;
+    SharedParts parts;
+    parts.o = sh_o;
+    parts.ml = sh_ml;
+    parts.k = L.k;
+    parts.sp = sp;
+    parts.nwg = nwg;
+    return launch_decode<D, false, kPad>(q, k_cache, v_cache, nullptr, nullptr, block_table,
+                                         context_lens, output, it, mbpr, hq, hkv, L.plan, ws,
+                                         stream, dr, parts);
+}
+
+}  // namespace
+
+bool decode_shared_supported(int batch_size, int num_q_heads, int num_kv_heads, int head_dim,
+                             int block_size) {
+    if (!decode_fast_supported(num_q_heads, num_kv_heads, head_dim, block_size)) return false;
+    const int G = num_q_heads / num_kv_heads;
+    return batch_size >= 1 && batch_size <= kSharedMaxItems && G <= kSharedCols / 2;
+}
+
+size_t decode_shared_workspace_bytes(int batch_size, int max_blocks_per_req, int num_q_heads,
+                                     int num_kv_heads, int head_dim) {
+    return shared_layout(batch_size, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim)
+        .total;
+}
+
+hipError_t decode_attention_shared(const void* q, const void* k_cache, const void* v_cache,
+                                   const int32_t* block_table, const int32_t* context_lens,
+                                   void* output, int batch_size, int max_blocks_per_req,
+                                   int num_q_heads, int num_kv_heads, int head_dim,
+                                   void* workspace, hipStream_t stream) {
+    const SharedLayout L = shared_layout(batch_size, max_blocks_per_req, num_q_heads,
+                                         num_kv_heads, head_dim);
+    char* ws = static_cast<char*>(workspace);
+    const int D = decode_mfma_dim(head_dim);
+    const bool pad = D != head_dim;
+#define CCI_SHARED(DD, PP)                                                                  \
+    return launch_decode_shared<DD, PP>(q, k_cache, v_cache, block_table, context_lens,    \
+                                        output, batch_size, max_blocks_per_req, num_q_heads, \
+                                        num_kv_heads, head_dim, L, ws, stream)
+    switch (D) {
+        case 64:
+            if (pad) CCI_SHARED(64, true);
+            CCI_SHARED(64, false);
+        case 128:
+            if (pad) CCI_SHARED(128, true);
+            CCI_SHARED(128, false);
+        case 256:
+            if (pad) CCI_SHARED(256, true);
+            CCI_SHARED(256, false);
+        default:
+            return hipErrorInvalidValue;
+    }
+#undef CCI_SHARED
 }
 
 }  // namespace ccinfer::hipk

@@ -40,7 +40,7 @@ constexpr int kFlatMaxItems = 256;
 // Returns the plan for a batch whose longest context is max_ctx tokens. allow_flat: the
 // flat mode may be used (it resolves items through DecodeItems like the kernel does).
 DecodePlan plan_decode(int num_items, int num_q_heads, int num_kv_heads, int max_ctx,
-                       bool allow_flat, bool fp8 = false);
+                       bool allow_flat, bool fp8 = false, bool allow_group = true);
 
 // The plan for the single-token items of a prefill batch (at most num_items of them).
 DecodePlan plan_decode_items(int num_items, int num_q_heads, int num_kv_heads, int max_ctx,
@@ -90,6 +90,20 @@ hipError_t decode_attention(const void* q, const void* k_cache, const void* v_ca
                             const DecodeItems& items, int max_blocks_per_req, int num_q_heads,
                             int num_kv_heads, int head_dim, int block_size,
                             const DecodePlan& plan, void* workspace, hipStream_t stream);
+
+// Decode of a batch whose requests may share cached prompt prefixes (leading block ids equal
+// across table rows): each group's common prefix is read once per subgroup of up to 16 / G
+// requests, the rest as in decode_attention. Plain decode semantics (zeros for invalid rows,
+// 1e-6 in the denominator); bf16 cache, head dims of decode_fast_supported, G <= 8.
+bool decode_shared_supported(int batch_size, int num_q_heads, int num_kv_heads, int head_dim,
+                             int block_size);
+size_t decode_shared_workspace_bytes(int batch_size, int max_blocks_per_req, int num_q_heads,
+                                     int num_kv_heads, int head_dim);
+hipError_t decode_attention_shared(const void* q, const void* k_cache, const void* v_cache,
+                                   const int32_t* block_table, const int32_t* context_lens,
+                                   void* output, int batch_size, int max_blocks_per_req,
+                                   int num_q_heads, int num_kv_heads, int head_dim,
+                                   void* workspace, hipStream_t stream);
 
 // ---- prefill --------------------------------------------------------------
 bool prefill_fast_supported(int num_q_heads, int num_kv_heads, int head_dim,

@@ -245,6 +245,44 @@ def decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     return output
 
 
+def decode_shared_workspace_size(batch_size: int, max_blocks_per_req: int, num_q_heads: int,
+                                 num_kv_heads: int, head_dim: int,
+                                 cache_block_size: int = 16) -> int:
+    return int(_lib.load().ccinfer_decode_shared_workspace_size(
+        batch_size, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim, cache_block_size))
+
+
+def decode_attention_shared_prefix(q: torch.Tensor, k_cache: torch.Tensor,
+                                   v_cache: torch.Tensor, block_table: torch.Tensor,
+                                   context_lens: torch.Tensor,
+                                   output: Optional[torch.Tensor] = None,
+                                   cache_block_size: int = 16,
+                                   workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """decode_attention for a batch whose requests may share cached prompt prefixes (equal
+    leading block ids): each group's common prefix is read once per MFMA tile of requests.
+    Same semantics as decode_attention; returns output."""
+    op = "decode_attention_shared_prefix"
+    for t in (q, k_cache, v_cache):
+        _dev_tensor(t, torch.bfloat16, op)
+    _dev_tensor(block_table, torch.int32, op)
+    _dev_tensor(context_lens, torch.int32, op)
+    _require(q.dim() == 3 and block_table.dim() == 2, op)
+    b, hq, d = q.shape
+    _, hkv, dk = _kv_shape(k_cache)
+    _require(dk == d and block_table.shape[0] == b and context_lens.numel() == b, op)
+    if output is None:
+        output = torch.empty_like(q)
+    _dev_tensor(output, torch.bfloat16, op)
+    _require(output.shape == q.shape, op)
+    mbpr = block_table.shape[1]
+    need = decode_shared_workspace_size(b, mbpr, hq, hkv, d, cache_block_size)
+    ws, ws_bytes = _workspace(need, q.device, workspace)
+    _check(_lib.load().ccinfer_decode_attention_shared_prefix(
+        _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(block_table), _ptr(context_lens),
+        _ptr(output), b, mbpr, hq, hkv, d, cache_block_size, _ptr(ws), ws_bytes, _stream()), op)
+    return output
+
+
 def decode_attention_write_kv(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
                               k_cache: torch.Tensor, v_cache: torch.Tensor,
                               block_table: torch.Tensor, context_lens: torch.Tensor,

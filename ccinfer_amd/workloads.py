@@ -152,6 +152,34 @@ def decode_batched(device="cpu", seed: int = 2, batch: int = 64, ctx_lo: int = 1
     return w
 
 
+def decode_shared_prefix(device="cpu", seed: int = 7, batch: int = 64, prefix: int = 2048,
+                         priv_lo: int = 128, priv_hi: int = 1024, groups: int = 1,
+                         hq: int = 16, hkv: int = 8, d: int = 128) -> PagedWorkload:
+    """Decode over shared cached prompts: request b belongs to prefix group b % groups; the
+    group's prefix (`prefix` tokens, whole blocks) sits in blocks every member's table row
+    starts with (prefix-cache hits), followed by U[priv_lo, priv_hi] private tokens."""
+    assert prefix % BLOCK == 0 and 1 <= groups <= batch
+    rng = np.random.default_rng(seed)
+    priv = rng.integers(priv_lo, priv_hi + 1, size=batch)
+    ctx = (prefix + priv).astype(np.int32)
+    nblk = (ctx + BLOCK - 1) // BLOCK
+    pblk = prefix // BLOCK
+    shared = {b: (b % groups, pblk) for b in range(groups, batch)}
+    distinct = int(nblk.sum()) - len(shared) * pblk
+    pool = _pool_size(distinct)
+    bt = _tables(rng, nblk.tolist(), pool, shared)
+    g = _gen(seed, device)
+    q = randn_bf16((batch, hq, d), g, device)
+    k, v = _cache(pool, hkv, d, g, device)
+    w = PagedWorkload(f"decode_b{batch}_shared{groups}x{prefix}+{priv_lo}-{priv_hi}", hq, hkv,
+                      d, ctx, bt, pool, q, k, v)
+    w.info["prefix"] = prefix
+    w.info["groups"] = groups
+    # bytes of distinct K/V positions: each group's prefix once, every private suffix
+    w.info["unique_kv_bytes"] = (groups * prefix + int(priv.sum())) * hkv * d * 2 * 2
+    return w
+
+
 def decode_long(device="cpu", seed: int = 5, batch: int = 32, ctx: int = 32768,
                 hq: int = 32, hkv: int = 8, d: int = 128) -> PagedWorkload:
     """Config 5: every context `ctx` tokens, blocks scattered across a shuffled pool."""

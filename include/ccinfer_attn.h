@@ -153,6 +153,33 @@ int ccinfer_decode_attention_write_kv(const void* q, const void* k_new, const vo
                                       int head_dim, int cache_block_size, int max_slots,
                                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* Workspace bytes ccinfer_decode_attention_shared_prefix needs for this batch shape. */
+size_t ccinfer_decode_shared_workspace_size(int batch_size, int max_blocks_per_req,
+                                            int num_q_heads, int num_kv_heads, int head_dim,
+                                            int cache_block_size);
+
+/* ccinfer_decode_attention for batches whose requests share cached prompt prefixes. No
+ * single counterpart in the reference: its prefix cache hands several requests the same
+ * leading block ids (KVCacheManager::lookup_prefix_cache, src/cache/kv_cache_manager.cpp:
+ * 93-173, counted in BlockTable::shared_count, src/cache/block.h:85-97), and its decode
+ * then reads those blocks once per request. Here the call finds, on the device, the groups
+ * of requests whose table rows start with the same block ids and attends each group's
+ * common prefix (whole 32-token chunks before every member's last position) once per
+ * subgroup of up to 16 / (num_q_heads / num_kv_heads) requests, which fill one MFMA tile
+ * together; positions after the prefix, and requests in no group, run as in
+ * ccinfer_decode_attention, and the parts are combined by the log-sum-exp merge. Same
+ * arguments, semantics and tolerance as ccinfer_decode_attention; a batch in which nothing
+ * is shared gives the same bits. Shapes outside the fast path (query groups above 8 heads,
+ * more than 2048 requests, misaligned views, non-16 blocks) run ccinfer_decode_attention
+ * (the workspace size covers it). */
+int ccinfer_decode_attention_shared_prefix(const void* q, const void* k_cache,
+                                           const void* v_cache, const int32_t* block_table,
+                                           const int32_t* context_lens, void* output,
+                                           int batch_size, int max_blocks_per_req,
+                                           int num_q_heads, int num_kv_heads, int head_dim,
+                                           int cache_block_size, void* workspace,
+                                           size_t workspace_bytes, void* stream);
+
 /* ccinfer_decode_attention without a workspace and without any allocation. No counterpart
  * in the reference: for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc). The split-KV scratch is
