@@ -695,6 +695,106 @@ def sweep(kind: str) -> None:
             torch.cuda.empty_cache()
 
 
+def sweep_generic() -> None:
+    """The generic kernels' cost against the MFMA paths at the configs' shapes: views that are
+    only 2-byte aligned (q / output offset by one element) and cache blocks other than 16."""
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream()
+    lib = _lib.load()
+    print("| case | aligned call (us) | this call (us) | ratio |")
+    print("|---|---|---|---|")
+
+    def misaligned(t):
+        buf = torch.empty(t.numel() + 8, dtype=t.dtype, device=t.device)
+        v = buf[1:1 + t.numel()].view(t.shape)
+        v.copy_(t)
+        return v
+
+    def rebin(w, bs):
+        """The workload's context lengths over a table of bs-token blocks of the same cache."""
+        rng = np.random.default_rng(bs)
+        nslots = w.k_cache.shape[0]
+        nb = (w.context_lens + bs - 1) // bs
+        perm = rng.permutation(nslots // bs).astype(np.int32)
+        bt = np.full((w.batch, int(nb.max())), -1, np.int32)
+        cur = 0
+        for b in range(w.batch):
+            # blocks are reused once the cache runs out (reads only, the timing is the same)
+            bt[b, :nb[b]] = perm[(cur + np.arange(nb[b])) % perm.size]
+            cur += nb[b]
+        return torch.from_numpy(bt).to(dev)
+
+    # decode, configs[1]
+    w = W.decode_batched(device=dev, with_write=False)
+    meta = w.device_meta(dev)
+    out = torch.empty_like(w.q)
+    n = lib.ccinfer_decode_workspace_size(w.batch, w.mbpr, w.hq, w.hkv, w.d, 16)
+    ws = torch.zeros(max(1, n), dtype=torch.uint8, device=dev)
+
+    def dec(q, o, bt, mbpr, bs):  # decode takes 16-token blocks only
+        def f():
+            rc = lib.ccinfer_decode_attention(q.data_ptr(), w.k_cache.data_ptr(),
+                                              w.v_cache.data_ptr(), bt.data_ptr(),
+                                              meta["context_lens"].data_ptr(), o.data_ptr(),
+                                              w.batch, mbpr, w.hq, w.hkv, w.d, bs,
+                                              ws.data_ptr(), n, stream.cuda_stream)
+            assert rc == 0, rc
+        return time_loop(f, 20, 3, stream)[0] * 1e3
+    base = dec(w.q, out, meta["block_table"], w.mbpr, 16)
+    qm, om = misaligned(w.q), misaligned(out)
+    t = dec(qm, om, meta["block_table"], w.mbpr, 16)
+    print(f"| decode configs[1], q and output 2-byte aligned (MFMA on row copies) | {base:.1f} "
+          f"| {t:.1f} | {t / base:.2f}x |", flush=True)
+    kshift = misaligned(w.k_cache)
+    def dec_k():
+        rc = lib.ccinfer_decode_attention(w.q.data_ptr(), kshift.data_ptr(),
+                                          w.v_cache.data_ptr(), meta["block_table"].data_ptr(),
+                                          meta["context_lens"].data_ptr(), out.data_ptr(),
+                                          w.batch, w.mbpr, w.hq, w.hkv, w.d, 16,
+                                          ws.data_ptr(), n, stream.cuda_stream)
+        assert rc == 0, rc
+    t = time_loop(dec_k, 3, 1, stream)[0] * 1e3
+    print(f"| decode configs[1], k_cache 2-byte aligned (generic) | {base:.1f} | {t:.1f} | "
+          f"{t / base:.0f}x |", flush=True)
+    del kshift
+    del w, ws
+    torch.cuda.empty_cache()
+
+    # prefill, configs[2]
+    w = W.prefill_prefix(device=dev)
+    meta = w.device_meta(dev)
+    out = torch.empty_like(w.q)
+    T = w.q.shape[0]
+    n = max(lib.ccinfer_prefill_workspace_size(w.batch, T, w.mbpr, w.hq, w.hkv, w.d, bs)
+            for bs in (16, 32, 64))
+    ws = torch.zeros(max(1, n), dtype=torch.uint8, device=dev)
+
+    def pre(q, o, bt, mbpr, bs, steps=10):
+        def f():
+            rc = lib.ccinfer_prefill_attention(q.data_ptr(), w.k_cache.data_ptr(),
+                                               w.v_cache.data_ptr(), bt.data_ptr(),
+                                               meta["query_start_loc"].data_ptr(),
+                                               meta["context_lens"].data_ptr(), o.data_ptr(),
+                                               w.batch, T, mbpr, w.hq, w.hkv, w.d, bs,
+                                               ws.data_ptr(), n, stream.cuda_stream)
+            assert rc == 0, rc
+        return time_loop(f, steps, 2, stream)[0] * 1e3
+    base = pre(w.q, out, meta["block_table"], w.mbpr, 16)
+    qm, om = misaligned(w.q), misaligned(out)
+    t = pre(qm, om, meta["block_table"], w.mbpr, 16, 3)
+    print(f"| prefill configs[2], q and output 2-byte aligned (MFMA on row copies) | "
+          f"{base:.1f} | {t:.1f} | {t / base:.2f}x |", flush=True)
+    for bs in (32, 64):
+        btb = rebin(w, bs)
+        t = pre(w.q, out, btb, btb.shape[1], bs, 5)
+        print(f"| prefill configs[2], {bs}-token blocks (MFMA, 16-token table) | {base:.1f} | "
+              f"{t:.1f} | {t / base:.2f}x |", flush=True)
+    bt8 = rebin(w, 8)
+    t = pre(w.q, out, bt8, bt8.shape[1], 8, 2)
+    print(f"| prefill configs[2], 8-token blocks (generic) | {base:.1f} | {t:.1f} | "
+          f"{t / base:.0f}x |", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -703,7 +803,7 @@ def main():
     ap.add_argument("--configs", default="1,2,3,4,5,6,7,8,9")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=5.0)
-    ap.add_argument("--sweep", choices=("decode", "prefill"),
+    ap.add_argument("--sweep", choices=("decode", "prefill", "generic"),
                     help="print a table of the op across shapes and exit")
     ap.add_argument("--profile-op", choices=["decode", "write", "prefill", "mixed", "long",
                                              "decode_b600", "decode_b2048",
@@ -718,6 +818,9 @@ def main():
               "(each GPU would own whole sequences or whole kv_heads, with no exchange "
               "inside attention; only the one-GPU share is built).", file=sys.stderr)
         sys.exit(2)
+    if args.sweep == "generic":
+        sweep_generic()
+        return
     if args.sweep:
         sweep(args.sweep)
         return

@@ -65,6 +65,26 @@ bool fast_aligned(const void* q, const void* k_cache, const void* v_cache, const
     return aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && aligned16(output);
 }
 
+// A bf16 call whose caches are 16-byte aligned but whose q or output view is only 2-byte
+// aligned still runs the MFMA kernels: q (and, for prefill, the output rows the call may
+// leave untouched) are copied into 16-byte-aligned workspace regions, the kernels run on
+// those, and the output rows are copied back -- two or three passes over rows that are
+// small next to the cache reads. Only caches that are not 16-byte aligned take the generic
+// kernels. The workspace size queries include these regions; a call checks only the bytes
+// it uses.
+constexpr size_t kWsAlign = 256;
+
+size_t ws_align(size_t v) { return (v + kWsAlign - 1) / kWsAlign * kWsAlign; }
+
+// Bytes of one workspace copy of `rows` x Hq x D bf16.
+size_t row_copy_bytes(int64_t rows, int num_q_heads, int head_dim) {
+    return ws_align(static_cast<size_t>(rows) * num_q_heads * head_dim * 2);
+}
+
+bool caches_aligned(const void* k_cache, const void* v_cache) {
+    return aligned16(k_cache) && aligned16(v_cache);
+}
+
 bool decode_shape_ok(int batch_size, int max_blocks_per_req, int num_q_heads, int num_kv_heads,
                      int head_dim, int cache_block_size) {
     if (batch_size <= 0 || max_blocks_per_req <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 ||
@@ -94,6 +114,39 @@ bool prefill_uses_fast(int batch_size, int max_blocks_per_req, int num_q_heads,
            decode_fast_supported(num_q_heads, num_kv_heads, head_dim, cache_block_size);
 }
 
+// How a bf16 prefill of this shape runs on the MFMA kernels: cache blocks of 16·k tokens are
+// read through a table of 16-token blocks (`expand` = k) built in the workspace; the
+// workspace holds the kernels' region, then that table, then the q / output row copies.
+struct PrefillRoute {
+    bool fast = false;
+    int expand = 1;
+    int mbpr16 = 0;
+    size_t table_off = 0;
+    size_t rows_off = 0;
+    size_t rows_bytes = 0;
+    size_t need(bool staged) const { return rows_off + (staged ? 2 * rows_bytes : 0); }
+};
+
+PrefillRoute prefill_route(int batch_size, int total_query_tokens, int max_blocks_per_req,
+                           int num_q_heads, int num_kv_heads, int head_dim,
+                           int cache_block_size) {
+    PrefillRoute r;
+    if (cache_block_size % 16 != 0) return r;
+    r.expand = cache_block_size / 16;
+    const int64_t mbpr16 = static_cast<int64_t>(max_blocks_per_req) * r.expand;
+    if (!fits_int(mbpr16) || !fits_int(mbpr16 * batch_size)) return r;
+    r.mbpr16 = static_cast<int>(mbpr16);
+    if (!prefill_uses_fast(batch_size, r.mbpr16, num_q_heads, num_kv_heads, head_dim, 16))
+        return r;
+    r.fast = true;
+    r.table_off = ws_align(prefill_workspace_bytes(batch_size, total_query_tokens, r.mbpr16,
+                                                   num_q_heads, num_kv_heads, head_dim, 16));
+    r.rows_off = r.table_off +
+                 (r.expand > 1 ? ws_align(static_cast<size_t>(mbpr16) * batch_size * 4) : 0);
+    r.rows_bytes = row_copy_bytes(total_query_tokens, num_q_heads, head_dim);
+    return r;
+}
+
 // A side stream needs both events; the events may not be NULL with a side stream.
 bool overlap_ok(void* side_stream, void* fork_event, void* join_event) {
     return side_stream == nullptr || (fork_event != nullptr && join_event != nullptr);
@@ -112,23 +165,47 @@ int prefill_entry(const void* q, const void* k_cache, const void* v_cache,
     if (!prefill_shape_ok(batch_size, total_query_tokens, max_blocks_per_req, num_q_heads,
                           num_kv_heads, head_dim, cache_block_size))
         return CCINFER_ERR_INVALID_ARGUMENT;
-    if (!prefill_uses_fast(batch_size, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
-                           cache_block_size) ||
-        !fast_aligned(q, k_cache, v_cache, output)) {
+    const PrefillRoute rt = prefill_route(batch_size, total_query_tokens, max_blocks_per_req,
+                                          num_q_heads, num_kv_heads, head_dim,
+                                          cache_block_size);
+    if (!rt.fast || !caches_aligned(k_cache, v_cache)) {
         return map_hip_error(generic_prefill_attention(
             q, k_cache, v_cache, block_table, query_start_loc, context_lens, output, batch_size,
             total_query_tokens, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
             cache_block_size, as_stream(stream)));
     }
-    const size_t need =
-        prefill_workspace_bytes(batch_size, total_query_tokens, max_blocks_per_req,
-                                num_q_heads, num_kv_heads, head_dim, cache_block_size);
-    if (workspace == nullptr || workspace_bytes < need) return CCINFER_ERR_INVALID_ARGUMENT;
-    return map_hip_error(prefill_attention(q, k_cache, v_cache, block_table, query_start_loc,
-                                           context_lens, output, batch_size, total_query_tokens,
-                                           max_blocks_per_req, num_q_heads, num_kv_heads,
-                                           head_dim, cache_block_size, workspace,
-                                           as_stream(stream), overlap));
+    const bool staged = !(aligned16(q) && aligned16(output));
+    if (workspace == nullptr || workspace_bytes < rt.need(staged))
+        return CCINFER_ERR_INVALID_ARGUMENT;
+    char* ws = static_cast<char*>(workspace);
+    hipStream_t s = as_stream(stream);
+    const int32_t* table = block_table;
+    if (rt.expand > 1) {
+        int32_t* t16 = reinterpret_cast<int32_t*>(ws + rt.table_off);
+        const hipError_t err =
+            expand_block_table(block_table, t16, batch_size, max_blocks_per_req, rt.expand, s);
+        if (err != hipSuccess) return map_hip_error(err);
+        table = t16;
+    }
+    const void* q_run = q;
+    void* out_run = output;
+    const int64_t elems = static_cast<int64_t>(total_query_tokens) * num_q_heads * head_dim;
+    if (staged) {
+        q_run = ws + rt.rows_off;
+        out_run = ws + rt.rows_off + rt.rows_bytes;
+        // the output copy starts as the caller's rows: rows of no request, or of a request
+        // whose context is shorter than its query, are not written and must come back as
+        // they were
+        hipError_t err = gather_rows(q, ws + rt.rows_off, elems, s);
+        if (err == hipSuccess) err = gather_rows(output, out_run, elems, s);
+        if (err != hipSuccess) return map_hip_error(err);
+    }
+    const hipError_t err = prefill_attention(
+        q_run, k_cache, v_cache, table, query_start_loc, context_lens, out_run, batch_size,
+        total_query_tokens, rt.mbpr16, num_q_heads, num_kv_heads, head_dim, 16, workspace, s,
+        overlap);
+    if (err != hipSuccess || !staged) return map_hip_error(err);
+    return map_hip_error(scatter_rows(out_run, output, elems, s));
 }
 
 int prefill_fp8_entry(const void* q, const void* k_cache, const void* v_cache,
@@ -163,6 +240,25 @@ int prefill_fp8_entry(const void* q, const void* k_cache, const void* v_cache,
 }
 
 }  // namespace
+
+namespace ccinfer::hipk {
+
+size_t decode_bytes_for(int batch_size, int max_blocks_per_req, int num_q_heads,
+                        int num_kv_heads, int head_dim, int cache_block_size, bool staged) {
+    // One size serves ccinfer_decode_attention and ccinfer_decode_attention_fp8, whose flat
+    // plans differ in wavefront count.
+    size_t bytes = 0;
+    for (const bool fp8 : {false, true}) {
+        const DecodePlan plan =
+            plan_decode(batch_size, num_q_heads, num_kv_heads,
+                        max_blocks_per_req * cache_block_size, true, fp8);
+        bytes = std::max(bytes, decode_workspace_bytes(batch_size, num_q_heads, head_dim, plan));
+    }
+    if (staged) bytes = ws_align(bytes) + 2 * row_copy_bytes(batch_size, num_q_heads, head_dim);
+    return bytes;
+}
+
+}  // namespace ccinfer::hipk
 
 extern "C" {
 
@@ -241,16 +337,8 @@ size_t ccinfer_decode_workspace_size(int batch_size, int max_blocks_per_req, int
                          cache_block_size))
         return 0;
     if (!decode_fast_supported(num_q_heads, num_kv_heads, head_dim, cache_block_size)) return 0;
-    // One size serves ccinfer_decode_attention and ccinfer_decode_attention_fp8, whose flat
-    // plans differ in wavefront count.
-    size_t bytes = 0;
-    for (const bool fp8 : {false, true}) {
-        const DecodePlan plan =
-            plan_decode(batch_size, num_q_heads, num_kv_heads,
-                        max_blocks_per_req * cache_block_size, true, fp8);
-        bytes = std::max(bytes, decode_workspace_bytes(batch_size, num_q_heads, head_dim, plan));
-    }
-    return bytes;
+    return decode_bytes_for(batch_size, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
+                            cache_block_size, true);
 }
 
 namespace {
@@ -268,15 +356,16 @@ int decode_entry(const void* q, const void* k_cache, const void* v_cache,
         return CCINFER_ERR_INVALID_ARGUMENT;
     const bool fast = decode_fast_supported(num_q_heads, num_kv_heads, head_dim,
                                             cache_block_size) &&
-                      fast_aligned(q, k_cache, v_cache, output);
+                      caches_aligned(k_cache, v_cache);
+    const bool staged = fast && !(aligned16(q) && aligned16(output));
     DecodePlan plan;
     if (fast) {
         plan = plan_decode(batch_size, num_q_heads, num_kv_heads,
                            max_blocks_per_req * cache_block_size, true);
-        // the size the query returns (it covers the fp8 entry's plan too)
-        const size_t need = ccinfer_decode_workspace_size(batch_size, max_blocks_per_req,
-                                                          num_q_heads, num_kv_heads, head_dim,
-                                                          cache_block_size);
+        // the size the query returns without the row copies, which only a call with
+        // unaligned q / output uses (it covers the fp8 entry's plan too)
+        const size_t need = decode_bytes_for(batch_size, max_blocks_per_req, num_q_heads,
+                                             num_kv_heads, head_dim, cache_block_size, staged);
         if (need > 0 && (workspace == nullptr || workspace_bytes < need))
             return CCINFER_ERR_INVALID_ARGUMENT;
     }
@@ -305,10 +394,25 @@ int decode_entry(const void* q, const void* k_cache, const void* v_cache,
         items.new_v = new_v;
         items.max_slots = max_slots;
     }
-    return map_hip_error(decode_attention(q, k_cache, v_cache, block_table, context_lens, output,
-                                          items, max_blocks_per_req, num_q_heads, num_kv_heads,
-                                          head_dim, cache_block_size, plan, workspace,
-                                          as_stream(stream)));
+    const void* q_run = q;
+    void* out_run = output;
+    const int64_t elems = static_cast<int64_t>(batch_size) * num_q_heads * head_dim;
+    if (staged) {
+        char* rows = static_cast<char*>(workspace) +
+                     ws_align(decode_bytes_for(batch_size, max_blocks_per_req, num_q_heads,
+                                               num_kv_heads, head_dim, cache_block_size, false));
+        q_run = rows;
+        out_run = rows + row_copy_bytes(batch_size, num_q_heads, head_dim);
+        const hipError_t err = gather_rows(q, rows, elems, as_stream(stream));
+        if (err != hipSuccess) return map_hip_error(err);
+    }
+    const hipError_t err = decode_attention(q_run, k_cache, v_cache, block_table, context_lens,
+                                            out_run, items, max_blocks_per_req, num_q_heads,
+                                            num_kv_heads, head_dim, cache_block_size, plan,
+                                            workspace, as_stream(stream));
+    if (err != hipSuccess || !staged) return map_hip_error(err);
+    // every output row is written (zeros for rows with no context)
+    return map_hip_error(scatter_rows(out_run, output, elems, as_stream(stream)));
 }
 
 }  // namespace
@@ -436,11 +540,12 @@ size_t ccinfer_prefill_workspace_size(int batch_size, int total_query_tokens,
     if (!prefill_shape_ok(batch_size, total_query_tokens, max_blocks_per_req, num_q_heads,
                           num_kv_heads, head_dim, cache_block_size))
         return 0;
-    if (!prefill_uses_fast(batch_size, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
-                           cache_block_size))
-        return 0;
-    return prefill_workspace_bytes(batch_size, total_query_tokens, max_blocks_per_req,
-                                   num_q_heads, num_kv_heads, head_dim, cache_block_size);
+    const PrefillRoute rt = prefill_route(batch_size, total_query_tokens, max_blocks_per_req,
+                                          num_q_heads, num_kv_heads, head_dim,
+                                          cache_block_size);
+    if (!rt.fast) return 0;
+    // it covers the fp8 entry (16-token blocks, aligned views only) too
+    return rt.need(true);
 }
 
 int ccinfer_prefill_attention(const void* q, const void* k_cache, const void* v_cache,

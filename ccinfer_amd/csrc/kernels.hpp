@@ -198,4 +198,20 @@ hipError_t generic_prefill_attention(const void* q, const void* k_cache, const v
                                      int num_q_heads, int num_kv_heads, int head_dim,
                                      int block_size, hipStream_t stream);
 
+// Workspace bytes of a bf16 / fp8 decode call of this shape on the MFMA kernels; `staged`
+// adds the q and output row copies a call with 2-byte-aligned q / output uses (defined with
+// the C ABI, which lays those copies out).
+size_t decode_bytes_for(int batch_size, int max_blocks_per_req, int num_q_heads,
+                        int num_kv_heads, int head_dim, int cache_block_size, bool staged);
+
+// Copies `elems` bf16 (a multiple of 8) between a 2-byte-aligned view and a 16-byte-aligned
+// buffer: gather reads the view, scatter writes it.
+hipError_t gather_rows(const void* src, void* dst, int64_t elems, hipStream_t stream);
+hipError_t scatter_rows(const void* src, void* dst, int64_t elems, hipStream_t stream);
+
+// Rewrites a [rows, max_blocks_per_req] table of (16·k)-token blocks as a
+// [rows, max_blocks_per_req·k] table of 16-token blocks over the same cache rows.
+hipError_t expand_block_table(const int32_t* block_table, int32_t* out, int rows,
+                              int max_blocks_per_req, int k, hipStream_t stream);
+
 }  // namespace ccinfer::hipk

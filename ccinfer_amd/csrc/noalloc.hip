@@ -76,9 +76,13 @@ extern "C" int ccinfer_decode_attention_noalloc(const void* q, const void* k_cac
                                                 int batch_size, int max_blocks_per_req,
                                                 int num_q_heads, int num_kv_heads, int head_dim,
                                                 int cache_block_size, void* stream) {
-    const size_t need = ccinfer_decode_workspace_size(batch_size, max_blocks_per_req,
-                                                      num_q_heads, num_kv_heads, head_dim,
-                                                      cache_block_size);
+    size_t need = ccinfer_decode_workspace_size(batch_size, max_blocks_per_req, num_q_heads,
+                                                num_kv_heads, head_dim, cache_block_size);
+    // the q / output row copies are needed only for views that are not 16-byte aligned
+    if (need > 0 && ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(output)) &
+                     15u) == 0)
+        need = ccinfer::hipk::decode_bytes_for(batch_size, max_blocks_per_req, num_q_heads,
+                                               num_kv_heads, head_dim, cache_block_size, false);
     if (need > kScratchBytes) return CCINFER_ERR_INVALID_ARGUMENT;
     void* ws = nullptr;
     if (need > 0) {

@@ -29,11 +29,13 @@
  * allocates). HipBackend holds its own reserved workspace and needs no global state.
  *
  * Alignment: the reference launchers accept any bf16 (2-byte aligned) view. The MFMA paths
- * move q, output and K/V cache rows in 16-byte pieces, so bf16 decode / prefill calls with
- * a q, output, k_cache or v_cache pointer that is not 16-byte aligned run on the generic
- * kernels instead (same results, slower); the fp8 calls, which have the MFMA paths only,
- * return CCINFER_ERR_INVALID_ARGUMENT for such pointers (and for k_scale / v_scale not
- * 16-byte aligned).
+ * move q, output and K/V cache rows in 16-byte pieces. A bf16 decode / prefill call whose
+ * q or output view is only 2-byte aligned copies q (and, for prefill, output) into the
+ * workspace, runs the MFMA kernels there and copies the output rows back (same bits as an
+ * aligned call); a k_cache or v_cache pointer that is not 16-byte aligned runs the generic
+ * kernels (same results within the tolerance, much slower). The fp8 calls, which have the
+ * MFMA paths only, return CCINFER_ERR_INVALID_ARGUMENT for any such pointer (and for
+ * k_scale / v_scale not 16-byte aligned).
  */
 #ifndef CCINFER_ATTN_H
 #define CCINFER_ATTN_H
@@ -111,7 +113,10 @@ int ccinfer_build_batch_metadata(const int32_t* item_kv_written, const int32_t* 
                                  int32_t* context_lens, int32_t* logits_indices, int32_t* status,
                                  void* stream);
 
-/* Workspace bytes ccinfer_decode_attention needs for this batch shape (may be 0). */
+/* Workspace bytes ccinfer_decode_attention (and ccinfer_decode_attention_fp8) needs for this
+ * batch shape; 0 for shapes on the generic kernels. The figure includes two copies of the
+ * q rows, which only a call with a 2-byte-aligned q or output uses; an aligned call accepts
+ * a workspace that much smaller. */
 size_t ccinfer_decode_workspace_size(int batch_size, int max_blocks_per_req, int num_q_heads,
                                      int num_kv_heads, int head_dim, int cache_block_size);
 
@@ -224,7 +229,9 @@ int ccinfer_decode_attention_fp8(const void* q, const void* k_cache, const void*
                                  int cache_block_size, void* workspace, size_t workspace_bytes,
                                  void* stream);
 
-/* Workspace bytes ccinfer_prefill_attention needs for this batch shape. */
+/* Workspace bytes ccinfer_prefill_attention (and the fp8 / overlap variants) needs for this
+ * batch shape; 0 for shapes on the generic kernel. As for decode, it includes two copies of
+ * the q rows used only by a call with a 2-byte-aligned q or output. */
 size_t ccinfer_prefill_workspace_size(int batch_size, int total_query_tokens,
                                       int max_blocks_per_req, int num_q_heads,
                                       int num_kv_heads, int head_dim, int cache_block_size);
@@ -238,8 +245,10 @@ size_t ccinfer_prefill_workspace_size(int batch_size, int total_query_tokens,
  * neither the batch size nor the table length is bounded. The MFMA path covers every
  * query group size and head dims that are multiples of 8 up to 128 (at any size; those
  * below 64 / 128 run padded with zeros) or multiples of 16 up to 256 (up to 4096 blocks per
- * table row); other shapes run the generic kernel. A mixed batch's
- * decode items run after the prompt tiles on `stream`. */
+ * table row, counted in 16-token blocks), with cache blocks of any multiple of 16 tokens
+ * (read through a 16-token table the call builds in the workspace); other shapes run the
+ * generic kernel. A mixed batch's decode items run on `stream` ahead of the prompt
+ * tiles. */
 int ccinfer_prefill_attention(const void* q, const void* k_cache, const void* v_cache,
                               const int32_t* block_table, const int32_t* query_start_loc,
                               const int32_t* context_lens, void* output, int batch_size,

@@ -75,7 +75,13 @@ def test_decode_validation(lib):
     need = lib.ccinfer_decode_workspace_size(64, 256, 16, 8, 128, 16)
     assert need > 0
     assert _decode(lib, b=64, mbpr=256, hq=16, hkv=8, ws=None, wsb=0) == INVALID
-    assert _decode(lib, b=64, mbpr=256, hq=16, hkv=8, ws=FAKE, wsb=need - 1) == INVALID
+    # an aligned call needs the size without the q / output row copies, a call with a
+    # 2-byte-aligned q or output the whole size
+    aligned = need - _row_copies(64, 16, 128)
+    assert _decode(lib, b=64, mbpr=256, hq=16, hkv=8, ws=FAKE, wsb=aligned - 1) == INVALID
+    for ptr in ("q", "out"):
+        assert _decode(lib, b=64, mbpr=256, hq=16, hkv=8, ws=FAKE, wsb=need - 1,
+                       **{ptr: FAKE + 2}) == INVALID, ptr
 
 
 def test_decode_write_kv_validation(lib):
@@ -96,8 +102,16 @@ def test_decode_write_kv_validation(lib):
     assert f(*a) == INVALID
 
 
+def _row_copies(b, hq, d):
+    """Two 256-byte-aligned copies of the q rows, at the end of every MFMA-path workspace
+    (used only by calls whose q or output view is 2-byte aligned)."""
+    return 2 * ((b * hq * d * 2 + 255) // 256 * 256)
+
+
 def test_decode_workspace_size(lib):
-    f = lib.ccinfer_decode_workspace_size
+    def f(b, mbpr, hq, hkv, d, bs):
+        n = lib.ccinfer_decode_workspace_size(b, mbpr, hq, hkv, d, bs)
+        return n - _row_copies(b, hq, d) if n else n
     assert f(0, 4, 8, 2, 128, 16) == 0            # invalid shape -> 0
     assert f(1, 1, 8, 2, 128, 16) == 0            # one 16-token block: single split, no scratch
     assert f(7, 2, 8, 2, 128, 16) == 0            # 32 tokens: one chunk per request
@@ -110,6 +124,21 @@ def test_decode_workspace_size(lib):
     # head_dim 80 runs the MFMA kernels at 128 with zero padding: partial rows of 128 floats
     assert f(32, 2048, 32, 8, 80, 16) == f(32, 2048, 32, 8, 128, 16)
     assert f(32, 2048, 32, 8, 72, 16) == 0        # not a decode head dim: invalid shape
+
+
+def test_prefill_workspace_size_for_other_block_sizes(lib):
+    """Blocks of 16·k tokens run the MFMA prefill through a 16-token table built in the
+    workspace: the size is that of the 16-token shape plus the table; other block sizes run
+    the generic kernel (no workspace)."""
+    f = lib.ccinfer_prefill_workspace_size
+    base = f(4, 512, 64, 16, 8, 128, 16)
+    assert base > 0
+    for k in (2, 4, 16):
+        n = f(4, 512, 64 // k, 16, 8, 128, 16 * k)
+        table = (4 * 64 * 4 + 255) // 256 * 256
+        assert n == base + table, k
+    assert f(4, 512, 64, 16, 8, 128, 8) == 0
+    assert f(4, 512, 64, 16, 8, 128, 24) == 0
 
 
 def _prefill(lib, **kw):
@@ -131,7 +160,8 @@ def test_prefill_validation(lib):
     need = lib.ccinfer_prefill_workspace_size(2, 64, 8, 16, 8, 128, 16)
     assert need > 0
     assert _prefill(lib) == INVALID                     # workspace missing
-    assert _prefill(lib, ws=FAKE, wsb=need - 1) == INVALID
+    assert _prefill(lib, ws=FAKE, wsb=need - _row_copies(64, 16, 128) - 1) == INVALID
+    assert _prefill(lib, ws=FAKE, wsb=need - 1, q=FAKE + 2) == INVALID
 
 
 def test_alignment_limits_and_overlap_validation(lib):
@@ -266,7 +296,7 @@ def test_prefill_fp8_validation(lib):
     a[14] = 96                   # a valid bf16 prefill head dim; fp8 is MFMA-only (64 / 128)
     assert pf(*a) == 26          # CCINFER_ERR_UNSUPPORTED
     a = list(ok)
-    a[17] = need - 1
+    a[17] = need - _row_copies(64, 16, 128) - 1   # fp8 views are aligned: no row copies
     assert pf(*a) == INVALID
     a = list(ok)
     a[16] = None

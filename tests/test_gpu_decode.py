@@ -218,8 +218,9 @@ def _offset_view(t: torch.Tensor, elems: int = 1) -> torch.Tensor:
 
 @pytest.mark.parametrize("which", ["q", "k_cache", "v_cache", "output"])
 def test_two_byte_aligned_views(gpu, which):
-    """The reference launchers take any bf16 view: a q, cache or output pointer that is only
-    2-byte aligned runs on the generic kernels (the MFMA path moves 16-byte pieces)."""
+    """The reference launchers take any bf16 view. A q or output view that is only 2-byte
+    aligned runs the MFMA kernels on workspace copies of its rows (bit-equal to the aligned
+    call); a cache that is only 2-byte aligned runs the generic kernels."""
     say(f"decode with a 2-byte aligned {which}")
     w = W.decode_batched(device=gpu, seed=17, batch=6, ctx_lo=20, ctx_hi=600, with_write=False)
     meta = w.device_meta(gpu)
@@ -234,6 +235,37 @@ def test_two_byte_aligned_views(gpu, which):
                            meta["context_lens"], output=out)
     torch.cuda.synchronize()
     assert_attn_close(f32(got), oracle_decode(w), f"misaligned {which}")
+    if which in ("q", "output"):
+        aligned = decode_attention(w.q, w.k_cache, w.v_cache, meta["block_table"],
+                                   meta["context_lens"])
+        torch.cuda.synchronize()
+        assert torch.equal(got, aligned)
+
+
+@pytest.mark.parametrize("batch,ctx_lo,ctx_hi,hq,hkv,d,offset", [
+    (64, 128, 4096, 16, 8, 128, 1),   # configs[1]: split plan with merge
+    (1, 512, 512, 16, 8, 128, 3),     # group plan (one launch)
+    (300, 1, 400, 16, 8, 96, 5),      # flat plan with index kernel, padded head dim
+])
+def test_two_byte_aligned_q_and_output_on_mfma_path(gpu, batch, ctx_lo, ctx_hi, hq, hkv, d,
+                                                    offset):
+    """q and output both 2-byte aligned (offset by an odd number of elements), every decode
+    plan: the staged call equals the aligned call bit for bit and leaves the bytes around
+    the output view alone."""
+    say(f"decode staged rows B={batch} ctx=[{ctx_lo},{ctx_hi}] hq={hq} hkv={hkv} d={d}")
+    w = W.decode_batched(device=gpu, seed=batch + d, batch=batch, ctx_lo=ctx_lo, ctx_hi=ctx_hi,
+                         hq=hq, hkv=hkv, d=d, with_write=False)
+    meta = w.device_meta(gpu)
+    want = decode_attention(w.q, w.k_cache, w.v_cache, meta["block_table"],
+                            meta["context_lens"])
+    qv = _offset_view(w.q, offset)
+    flat = torch.full((w.q.numel() + offset + 8,), 5.0, dtype=torch.bfloat16, device=gpu)
+    ov = flat[offset:offset + w.q.numel()].view(w.q.shape)
+    got = decode_attention(qv, w.k_cache, w.v_cache, meta["block_table"], meta["context_lens"],
+                           output=ov)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert torch.all(flat[:offset] == 5.0) and torch.all(flat[offset + w.q.numel():] == 5.0)
 
 
 def _write_then_decode(w, dev, slot_mapping, k_cache, v_cache):

@@ -286,7 +286,9 @@ def test_concurrent_mixed_prefills_on_two_streams(gpu):
 
 @pytest.mark.parametrize("which", ["q", "k_cache", "output"])
 def test_two_byte_aligned_views(gpu, which):
-    """A q, cache or output view that is only 2-byte aligned runs on the generic kernels."""
+    """A q or output view that is only 2-byte aligned runs the MFMA kernels on workspace
+    copies of its rows (bit-equal to the aligned call); a cache that is only 2-byte aligned
+    runs the generic kernel."""
     say(f"prefill with a 2-byte aligned {which}")
     w = W.prefill_prefix(device=gpu, seed=19, n_seqs=3, prefix=32, new=90, share_pairs=(),
                          hq=8, hkv=4, d=128)
@@ -310,6 +312,77 @@ def test_two_byte_aligned_views(gpu, which):
                             meta["context_lens"], output=out)
     torch.cuda.synchronize()
     assert_attn_close(f32(got), oracle_prefill(w), f"misaligned {which}")
+    if which != "k_cache":
+        assert torch.equal(got, run_prefill(w, gpu))
+
+
+def test_two_byte_aligned_output_keeps_unwritten_rows(gpu):
+    """The staged output starts as a copy of the caller's rows, so rows the kernels do not
+    write (a request whose context is shorter than its query) come back unchanged; a mixed
+    batch's decode items write through the staged rows too."""
+    say("prefill staged output: untouched rows and decode items")
+    rng = np.random.default_rng(31)
+    hq, hkv, d = 16, 8, 128
+    qlen = np.array([70, 1, 3, 1, 5, 200], np.int32)
+    ctx = np.array([90, 300, 2, 17, 40, 200], np.int32)   # request 2: prefix < 0
+    mbpr, pool = 24, 160
+    bt = rng.permutation(pool)[:len(qlen) * mbpr].reshape(len(qlen), mbpr).astype(np.int32)
+    qsl = np.concatenate([[0], np.cumsum(qlen)]).astype(np.int32)
+    total = int(qsl[-1])
+    g = torch.Generator(device=gpu)
+    g.manual_seed(6)
+    q = W.randn_bf16((total, hq, d), g, gpu)
+    kc = W.randn_bf16((pool * 16, hkv, d), g, gpu)
+    vc = W.randn_bf16((pool * 16, hkv, d), g, gpu)
+    w = W.PagedWorkload("staged", hq, hkv, d, ctx, bt, pool, q, kc, vc, query_start_loc=qsl)
+    flat = torch.full((total * hq * d + 9,), 7.0, dtype=torch.bfloat16, device=gpu)
+    ov = flat[3:3 + total * hq * d].view(total, hq, d)
+    meta = w.device_meta(gpu)
+    prefill_attention(q, kc, vc, meta["block_table"], meta["query_start_loc"],
+                      meta["context_lens"], output=ov)
+    torch.cuda.synchronize()
+    got = f32(ov)
+    want = oracle_prefill(w, out=np.full((total, hq, d), 7.0, np.float32))
+    assert np.all(got[qsl[2]:qsl[3]] == 7.0)
+    assert torch.all(flat[:3] == 7.0) and torch.all(flat[3 + total * hq * d:] == 7.0)
+    assert_attn_close(got, want, "staged edge")
+    aligned = run_prefill(w, gpu, out=torch.full_like(q, 7.0))
+    assert torch.equal(ov, aligned)
+
+
+@pytest.mark.parametrize("bs,hq,hkv,d", [(32, 16, 8, 128), (64, 8, 8, 64), (256, 32, 4, 128),
+                                         (48, 16, 8, 96)])
+def test_block_sizes_multiple_of_16_on_mfma_path(gpu, bs, hq, hkv, d):
+    """Cache blocks of 16·k tokens run the MFMA prefill through a 16-token table built in the
+    workspace: bit-equal to the same call with that table written out on the host, and
+    within the tolerance of the oracle at block size bs. The batch mixes prompt chunks over
+    cached prefixes with decode items."""
+    say(f"prefill block size {bs} hq={hq} hkv={hkv} d={d}")
+    rng = np.random.default_rng(bs + d)
+    qlen = np.array([300, 1, 77, 1, 1, 129, 40], np.int32)
+    prefix = np.array([0, 900, 250, 31, 2047, 600, 5], np.int32)
+    ctx = prefix + qlen
+    mbpr = int((ctx.max() + bs - 1) // bs) + 1
+    pool = len(qlen) * mbpr
+    bt = rng.permutation(pool).reshape(len(qlen), mbpr).astype(np.int32)
+    k = bs // 16
+    bt16 = (bt[:, :, None] * k + np.arange(k)[None, None, :]).reshape(len(qlen), mbpr * k)
+    qsl = np.concatenate([[0], np.cumsum(qlen)]).astype(np.int32)
+    total = int(qsl[-1])
+    g = torch.Generator(device=gpu)
+    g.manual_seed(bs)
+    q = W.randn_bf16((total, hq, d), g, gpu)
+    kc = W.randn_bf16((pool * bs, hkv, d), g, gpu)
+    vc = W.randn_bf16((pool * bs, hkv, d), g, gpu)
+    w = W.PagedWorkload(f"bs{bs}", hq, hkv, d, ctx, bt, pool, q, kc, vc, query_start_loc=qsl)
+    w16 = W.PagedWorkload("bs16", hq, hkv, d, ctx, bt16.astype(np.int32), pool * k, q, kc, vc,
+                          query_start_loc=qsl)
+    got = run_prefill(w, gpu, block_size=bs)
+    assert torch.equal(got, run_prefill(w16, gpu))
+    pairs = sample_pairs(w, 400, bs)
+    want = oracle_prefill(w, pairs=pairs, block_size=bs)
+    r, h = pairs[:, 0], pairs[:, 1]
+    assert_attn_close(f32(got)[r, h], want[r, h], f"bs{bs}")
 
 
 def test_more_than_4096_requests(gpu):
