@@ -572,6 +572,16 @@ def profile(op: str, iters: int) -> None:
         w = W.decode_batched(device=dev, seed=5, batch=batch, ctx_lo=lo, ctx_hi=hi, hq=32,
                              hkv=8, with_write=False)
         fn = Ops(w, dev, stream).decode
+    elif op in ("decode_d64", "decode_d80", "decode_d96", "decode_d128", "decode_d192",
+                "decode_g32", "decode_g32_hkv1"):
+        # the sweep's 64 x 4096 decode at other head dims and query-group sizes
+        hq, hkv, d = {"decode_d64": (16, 8, 64), "decode_d80": (16, 8, 80),
+                      "decode_d96": (16, 8, 96), "decode_d128": (16, 8, 128),
+                      "decode_d192": (8, 4, 192), "decode_g32": (64, 2, 128),
+                      "decode_g32_hkv1": (32, 1, 128)}[op]
+        w = W.decode_batched(device=dev, batch=64, ctx_lo=4096, ctx_hi=4096, hq=hq, hkv=hkv,
+                             d=d, with_write=False)
+        fn = Ops(w, dev, stream).decode
     elif op in ("decode_shared", "decode_unshared"):
         # 64 requests on one 2048-token cached prompt + U[128, 1024] private tokens, through
         # the shared-prefix entry or plain decode
@@ -810,7 +820,9 @@ def main():
                                              "decode_shared", "decode_unshared",
                                              "prologue", "shared_prefix", "private_prefix",
                                              "shared_prefix_ragged", "private_prefix_ragged",
-                                             "copy"], default=None)
+                                             "copy", "decode_d64", "decode_d80",
+                                             "decode_d96", "decode_d128", "decode_d192",
+                                             "decode_g32", "decode_g32_hkv1"], default=None)
     ap.add_argument("--profile-iters", type=int, default=5)
     args = ap.parse_args()
     if args.gpus != 1:
