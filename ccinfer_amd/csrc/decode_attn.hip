@@ -543,9 +543,11 @@ __device__ __forceinline__ T kv_load(const T* p) {
         return __builtin_nontemporal_load(p);
 }
 
-template <int D>
+// KS: the K steps a row needs (fewer than D / 32 when the padded dims leave whole steps
+// empty; those steps are neither loaded nor multiplied).
+template <int D, int KS = DecodeShape<D>::kSteps>
 struct ChunkRegs {
-    u32x4 k[2][DecodeShape<D>::kSteps];
+    u32x4 k[2][KS];
     uint32_t v[8][DecodeShape<D>::kVWords];
 };
 
@@ -555,11 +557,12 @@ struct ChunkRegs {
 // the batch (d=80 151.5 -> 139.7 us, d=120 191.4 -> 183.4 us at 64 x 4096). At D = 64 and
 // 256 such loads read a valid piece of the row instead and are replaced by zeros: masking
 // measured 11-23 % slower at d=32, and spills 137 VGPRs at D = 256.
-template <int D, bool kPad = false, bool kTL = false>
-__device__ __forceinline__ void load_chunk(ChunkRegs<D>& c, const __bf16* __restrict__ k_cache,
+template <int D, bool kPad = false, bool kTL = false, int KS = DecodeShape<D>::kSteps>
+__device__ __forceinline__ void load_chunk(ChunkRegs<D, KS>& c,
+                                           const __bf16* __restrict__ k_cache,
                                            const __bf16* __restrict__ v_cache, int pb0, int pb1,
                                            int kv_head, int hkv, int lane, int dr = D) {
-    constexpr int S = DecodeShape<D>::kSteps;
+    constexpr int S = KS;
     constexpr int NV = DecodeShape<D>::kNV;
     const int rs = kPad ? dr : D;  // row stride (elements)
     constexpr bool kMasked = kPad && D == 128;
@@ -687,14 +690,14 @@ struct SoftmaxState {
 
 // kScaled: K/V came from the fp8 cache; ks[e] / vs[e] are the row scales of token T(g, e),
 // applied to its score (K) and to its probability in the PV product (V).
-template <int D, bool kScaled = false>
-__device__ __forceinline__ void consume_chunk(SoftmaxState<D>& st, ChunkRegs<D>& c,
+template <int D, bool kScaled = false, int KS = DecodeShape<D>::kSteps>
+__device__ __forceinline__ void consume_chunk(SoftmaxState<D>& st, ChunkRegs<D, KS>& c,
                                               const bf16x8 (&qop)[DecodeShape<D>::kSteps],
                                               int cb, int end, int pb0, int pb1,
                                               float scale_log2, int g,
                                               const float* ks = nullptr,
                                               const float* vs = nullptr) {
-    constexpr int S = DecodeShape<D>::kSteps;
+    constexpr int S = KS;
     constexpr int NV = DecodeShape<D>::kNV;
     float sc[8];
 #pragma unroll
@@ -969,15 +972,21 @@ __device__ __forceinline__ void load_split_inputs(const __bf16* __restrict__ q,
 
 // Attention of the G query heads of kv_head h over context positions [begin, end) (at most
 // 2048) with the split's inputs: the online-softmax state of one wavefront.
-template <int D, bool F8, bool kPad = false, bool kTL = false>
+// KS: K steps per row (bf16); NBUF: chunks in flight (two, or three, which the kernels
+// have the registers for at no head dim today: three padded chunks at head dim 80 / 192
+// spill 521 / 619 VGPRs).
+template <int D, bool F8, bool kPad = false, bool kTL = false,
+          int KS = DecodeShape<D>::kSteps, int NBUF = 2>
 __device__ __forceinline__ void run_split(
     const std::conditional_t<F8, uint8_t, __bf16>* __restrict__ k_cache,
     const std::conditional_t<F8, uint8_t, __bf16>* __restrict__ v_cache,
     const float* __restrict__ k_scale, const float* __restrict__ v_scale,
     const SplitInputs<D>& in, int hkv, int h, int begin, int end, float scale_log2, int lane,
     SoftmaxState<D>& st, int dr = D) {
+    static_assert(NBUF == 2 || NBUF == 3, "two or three chunks in flight");
+    static_assert(!F8 || (KS == DecodeShape<D>::kSteps && NBUF == 2), "fp8: the full chunk");
     constexpr int NV = DecodeShape<D>::kNV;
-    using Regs = std::conditional_t<F8, ChunkRegsF8<D>, ChunkRegs<D>>;
+    using Regs = std::conditional_t<F8, ChunkRegsF8<D>, ChunkRegs<D, KS>>;
     const int g = lane >> 4;
     const int nblk = (end - begin + kBlock - 1) / kBlock;
     auto block_id = [&](int jb) -> int {  // jb: wave-uniform block index within the split
@@ -995,24 +1004,51 @@ __device__ __forceinline__ void run_split(
         *p0 = block_id(2 * c);
         *p1 = (2 * c + 1 < nblk) ? block_id(2 * c + 1) : -1;
     };
-    Regs ra, rb;
     auto load = [&](Regs& r, int p0, int p1) {
         if constexpr (F8)
             load_chunk<D, kTL>(r, k_cache, v_cache, k_scale, v_scale, p0, p1, h, hkv, lane);
         else
-            load_chunk<D, kPad, kTL>(r, k_cache, v_cache, p0, p1, h, hkv, lane, dr);
+            load_chunk<D, kPad, kTL, KS>(r, k_cache, v_cache, p0, p1, h, hkv, lane, dr);
     };
+    auto consume = [&](Regs& r, int c, int p0, int p1) {
+        if constexpr (F8)
+            consume_chunk<D>(st, r, in.qop, begin + c * kChunk, end, p0, p1, scale_log2, g);
+        else
+            consume_chunk<D, false, KS>(st, r, in.qop, begin + c * kChunk, end, p0, p1,
+                                        scale_log2, g);
+    };
+    Regs ra, rb;
     int a0, a1, b0, b1;
     chunk_blocks(0, &a0, &a1);
     load(ra, a0, a1);
-    for (int c = 0; c < nchunks; c += 2) {
-        chunk_blocks(c + 1, &b0, &b1);
+    if constexpr (NBUF == 2) {
+        for (int c = 0; c < nchunks; c += 2) {
+            chunk_blocks(c + 1, &b0, &b1);
+            load(rb, b0, b1);
+            consume(ra, c, a0, a1);
+            if (c + 1 >= nchunks) break;
+            chunk_blocks(c + 2, &a0, &a1);
+            load(ra, a0, a1);
+            consume(rb, c + 1, b0, b1);
+        }
+    } else {
+        Regs rc;
+        int c0, c1;
+        chunk_blocks(1, &b0, &b1);
         load(rb, b0, b1);
-        consume_chunk<D>(st, ra, in.qop, begin + c * kChunk, end, a0, a1, scale_log2, g);
-        if (c + 1 >= nchunks) break;
-        chunk_blocks(c + 2, &a0, &a1);
-        load(ra, a0, a1);
-        consume_chunk<D>(st, rb, in.qop, begin + (c + 1) * kChunk, end, b0, b1, scale_log2, g);
+        for (int c = 0; c < nchunks; c += 3) {
+            chunk_blocks(c + 2, &c0, &c1);
+            load(rc, c0, c1);
+            consume(ra, c, a0, a1);
+            if (c + 1 >= nchunks) break;
+            chunk_blocks(c + 3, &a0, &a1);
+            load(ra, a0, a1);
+            consume(rb, c + 1, b0, b1);
+            if (c + 2 >= nchunks) break;
+            chunk_blocks(c + 4, &b0, &b1);
+            load(rb, b0, b1);
+            consume(rc, c + 2, c0, c1);
+        }
     }
 }
 
@@ -1275,7 +1311,8 @@ __device__ __forceinline__ void shared_prefix_work(
 // kPad: head_dim dr < D (see load_chunk); q and output rows hold dr elements.
 // kTL: the K/V loads stay in L2 (see kv_load).
 // kShared: workgroups from split_wgs on run shared_prefix_work (decode_attention_shared).
-template <int D, bool F8, bool kPad, bool kTL, bool kShared = false>
+template <int D, bool F8, bool kPad, bool kTL, bool kShared = false,
+          int KS = DecodeShape<D>::kSteps, int NBUF = 2>
 __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     const __bf16* __restrict__ q, void* k_cache_v, void* v_cache_v,
     const float* __restrict__ k_scale,
@@ -1353,8 +1390,8 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     load_split_inputs<D, F8, kPad>(q, block_table + static_cast<int64_t>(req) * mbpr, mbpr, qrow,
                                    hq, h, G, begin, end, lane, in, dr);
     SoftmaxState<D> st;
-    run_split<D, F8, kPad, kTL>(k_cache, v_cache, k_scale, v_scale, in, hkv / rep, h / rep,
-                                begin, end, scale_log2, lane, st, dr);
+    run_split<D, F8, kPad, kTL, KS, NBUF>(k_cache, v_cache, k_scale, v_scale, in, hkv / rep,
+                                          h / rep, begin, end, scale_log2, lane, st, dr);
     const float l_tot = wave_sum_xor16_32(st.l);
     const bool live = j < G;
     const int head = h * G + j;
@@ -1704,8 +1741,18 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
     const int split_wgs = shr ? (grid + 7) / 8 * 8 : grid;
     const int total_wgs = split_wgs + (shr ? shared.nwg : 0);
     auto go = [&](auto tl_tag, auto sh_tag) {
-        decode_split_kernel<D, F8, kPad, decltype(tl_tag)::value, decltype(sh_tag)::value>
-            <<<total_wgs, 256, 0, stream>>>(
+        constexpr bool kTLv = decltype(tl_tag)::value;
+        constexpr bool kShv = decltype(sh_tag)::value;
+        // Padded rows that leave whole K steps empty (head dims 80 / 96 at D = 128, 192 at
+        // D = 256): those steps are compiled out -- no loads, no MFMAs, 5-16 fewer VGPRs
+        // (the D = 128 kernel's spills go away). Bit-identical; 64 x 4096 positions: d=80
+        // 139.4 -> 137.6 us, d=96 154.8 -> 152.3, d=192 195.0 -> 175.8.
+        constexpr int KSp = D == 128 ? 3 : D == 256 ? 6 : DecodeShape<D>::kSteps;
+        auto kernel = decode_split_kernel<D, F8, kPad, kTLv, kShv>;
+        if constexpr (!F8 && kPad && !kShv && KSp < DecodeShape<D>::kSteps) {
+            if (dr <= KSp * 32) kernel = decode_split_kernel<D, F8, kPad, kTLv, kShv, KSp, 2>;
+        }
+        kernel<<<total_wgs, 256, 0, stream>>>(
             static_cast<const __bf16*>(q), const_cast<void*>(k_cache), const_cast<void*>(v_cache),
             k_scale, v_scale, block_table, context_lens, static_cast<__bf16*>(output), w.o, w.ml,
             w.desc, it, mbpr, hq, hkv,
