@@ -354,24 +354,22 @@ int decode_entry(const void* q, const void* k_cache, const void* v_cache,
     if (!decode_shape_ok(batch_size, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
                          cache_block_size))
         return CCINFER_ERR_INVALID_ARGUMENT;
-    const bool fast = decode_fast_supported(num_q_heads, num_kv_heads, head_dim,
-                                            cache_block_size) &&
-                      caches_aligned(k_cache, v_cache);
-    const bool staged = fast && !(aligned16(q) && aligned16(output));
-    DecodePlan plan;
-    if (fast) {
-        plan = plan_decode(batch_size, num_q_heads, num_kv_heads,
-                           max_blocks_per_req * cache_block_size, true);
-        // the size the query returns without the row copies, which only a call with
-        // unaligned q / output uses (it covers the fp8 entry's plan too)
-        const size_t need = decode_bytes_for(batch_size, max_blocks_per_req, num_q_heads,
-                                             num_kv_heads, head_dim, cache_block_size, staged);
-        if (need > 0 && (workspace == nullptr || workspace_bytes < need))
-            return CCINFER_ERR_INVALID_ARGUMENT;
-    }
+    // Every decode shape the validation admits runs the MFMA kernels (caches that are only
+    // 2-byte aligned with 2-byte piece loads).
+    if (!decode_fast_supported(num_q_heads, num_kv_heads, head_dim, cache_block_size))
+        return CCINFER_ERR_INTERNAL;
+    const bool staged = !(aligned16(q) && aligned16(output));
+    const DecodePlan plan = plan_decode(batch_size, num_q_heads, num_kv_heads,
+                                        max_blocks_per_req * cache_block_size, true);
+    // the size the query returns without the row copies, which only a call with unaligned
+    // q / output uses (it covers the fp8 entry's plan too)
+    const size_t need = decode_bytes_for(batch_size, max_blocks_per_req, num_q_heads,
+                                         num_kv_heads, head_dim, cache_block_size, staged);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+        return CCINFER_ERR_INVALID_ARGUMENT;
     // The new tokens go in with the decode launch when its kernels can write them (4-byte
-    // aligned rows), else by a separate launch before it.
-    const bool fused = new_k != nullptr && fast &&
+    // aligned new rows, 16-byte aligned cache rows), else by a separate launch before it.
+    const bool fused = new_k != nullptr && caches_aligned(k_cache, v_cache) &&
                        ((reinterpret_cast<uintptr_t>(new_k) | reinterpret_cast<uintptr_t>(new_v)) &
                         3u) == 0;
     if (new_k != nullptr && !fused) {
@@ -380,12 +378,6 @@ int decode_entry(const void* q, const void* k_cache, const void* v_cache,
             context_lens, batch_size, max_blocks_per_req, num_kv_heads, head_dim, max_slots,
             as_stream(stream));
         if (err != hipSuccess) return map_hip_error(err);
-    }
-    if (!fast) {
-        return map_hip_error(generic_decode_attention(
-            q, k_cache, v_cache, block_table, context_lens, output, batch_size,
-            max_blocks_per_req, num_q_heads, num_kv_heads, head_dim, cache_block_size,
-            as_stream(stream)));
     }
     DecodeItems items;
     items.num_items = batch_size;

@@ -543,6 +543,25 @@ __device__ __forceinline__ T kv_load(const T* p) {
         return __builtin_nontemporal_load(p);
 }
 
+// kU: the cache rows are only 2-byte aligned (a cache pointer offset by an odd number of
+// elements; the reference kernels read bf16 scalars, so they accept one). Each piece is
+// then assembled from 2-byte loads -- neighbouring lanes read neighbouring elements, so a
+// wavefront still touches whole lines -- and the rest of the kernel is unchanged.
+template <bool kTL, bool kU, typename T>
+__device__ __forceinline__ T kv_piece(const __bf16* p) {
+    if constexpr (!kU) {
+        return kv_load<kTL>(reinterpret_cast<const T*>(p));
+    } else {
+        constexpr int kWords = sizeof(T) / 4;
+        const uint16_t* e = reinterpret_cast<const uint16_t*>(p);
+        T w;
+#pragma unroll
+        for (int i = 0; i < kWords; ++i)
+            w[i] = static_cast<uint32_t>(e[2 * i]) | (static_cast<uint32_t>(e[2 * i + 1]) << 16);
+        return w;
+    }
+}
+
 // KS: the K steps a row needs (fewer than D / 32 when the padded dims leave whole steps
 // empty; those steps are neither loaded nor multiplied).
 template <int D, int KS = DecodeShape<D>::kSteps>
@@ -557,7 +576,8 @@ struct ChunkRegs {
 // the batch (d=80 151.5 -> 139.7 us, d=120 191.4 -> 183.4 us at 64 x 4096). At D = 64 and
 // 256 such loads read a valid piece of the row instead and are replaced by zeros: masking
 // measured 11-23 % slower at d=32, and spills 137 VGPRs at D = 256.
-template <int D, bool kPad = false, bool kTL = false, int KS = DecodeShape<D>::kSteps>
+template <int D, bool kPad = false, bool kTL = false, int KS = DecodeShape<D>::kSteps,
+          bool kU = false>
 __device__ __forceinline__ void load_chunk(ChunkRegs<D, KS>& c,
                                            const __bf16* __restrict__ k_cache,
                                            const __bf16* __restrict__ v_cache, int pb0, int pb1,
@@ -579,9 +599,9 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<D, KS>& c,
             const bool ok = !kPad || dim0 < dr;
             if constexpr (kMasked) {
                 c.k[kb][kk] = u32x4{0, 0, 0, 0};
-                if (ok) c.k[kb][kk] = kv_load<kTL>(reinterpret_cast<const u32x4*>(row + dim0));
+                if (ok) c.k[kb][kk] = kv_piece<kTL, kU, u32x4>(row + dim0);
             } else {
-                c.k[kb][kk] = kv_load<kTL>(reinterpret_cast<const u32x4*>(row + (ok ? dim0 : 0)));
+                c.k[kb][kk] = kv_piece<kTL, kU, u32x4>(row + (ok ? dim0 : 0));
                 if (!ok) c.k[kb][kk] = u32x4{0, 0, 0, 0};
             }
         }
@@ -596,17 +616,17 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<D, KS>& c,
             (vok ? i * NV : 0);
         if constexpr (NV == 8) {
             u32x4 w = u32x4{0, 0, 0, 0};
-            if (!kMasked || vok) w = kv_load<kTL>(reinterpret_cast<const u32x4*>(row));
+            if (!kMasked || vok) w = kv_piece<kTL, kU, u32x4>(row);
 #pragma unroll
             for (int x = 0; x < 4; ++x) c.v[e][x] = vok ? w[x] : 0u;
         } else if constexpr (NV == 4) {
             u32x2 w = u32x2{0, 0};
-            if (!kMasked || vok) w = kv_load<kTL>(reinterpret_cast<const u32x2*>(row));
+            if (!kMasked || vok) w = kv_piece<kTL, kU, u32x2>(row);
             c.v[e][0] = vok ? w[0] : 0u;
             c.v[e][1] = vok ? w[1] : 0u;
         } else {
-            const u32x4 w0 = kv_load<kTL>(reinterpret_cast<const u32x4*>(row));
-            const u32x4 w1 = kv_load<kTL>(reinterpret_cast<const u32x4*>(row + 8));
+            const u32x4 w0 = kv_piece<kTL, kU, u32x4>(row);
+            const u32x4 w1 = kv_piece<kTL, kU, u32x4>(row + 8);
 #pragma unroll
             for (int x = 0; x < 4; ++x) {
                 c.v[e][x] = vok ? w0[x] : 0u;
@@ -976,7 +996,7 @@ __device__ __forceinline__ void load_split_inputs(const __bf16* __restrict__ q,
 // have the registers for at no head dim today: three padded chunks at head dim 80 / 192
 // spill 521 / 619 VGPRs).
 template <int D, bool F8, bool kPad = false, bool kTL = false,
-          int KS = DecodeShape<D>::kSteps, int NBUF = 2>
+          int KS = DecodeShape<D>::kSteps, int NBUF = 2, bool kU = false>
 __device__ __forceinline__ void run_split(
     const std::conditional_t<F8, uint8_t, __bf16>* __restrict__ k_cache,
     const std::conditional_t<F8, uint8_t, __bf16>* __restrict__ v_cache,
@@ -984,7 +1004,8 @@ __device__ __forceinline__ void run_split(
     const SplitInputs<D>& in, int hkv, int h, int begin, int end, float scale_log2, int lane,
     SoftmaxState<D>& st, int dr = D) {
     static_assert(NBUF == 2 || NBUF == 3, "two or three chunks in flight");
-    static_assert(!F8 || (KS == DecodeShape<D>::kSteps && NBUF == 2), "fp8: the full chunk");
+    static_assert(!F8 || (KS == DecodeShape<D>::kSteps && NBUF == 2 && !kU),
+                  "fp8: the full chunk, 16-byte aligned");
     constexpr int NV = DecodeShape<D>::kNV;
     using Regs = std::conditional_t<F8, ChunkRegsF8<D>, ChunkRegs<D, KS>>;
     const int g = lane >> 4;
@@ -1008,7 +1029,7 @@ __device__ __forceinline__ void run_split(
         if constexpr (F8)
             load_chunk<D, kTL>(r, k_cache, v_cache, k_scale, v_scale, p0, p1, h, hkv, lane);
         else
-            load_chunk<D, kPad, kTL, KS>(r, k_cache, v_cache, p0, p1, h, hkv, lane, dr);
+            load_chunk<D, kPad, kTL, KS, kU>(r, k_cache, v_cache, p0, p1, h, hkv, lane, dr);
     };
     auto consume = [&](Regs& r, int c, int p0, int p1) {
         if constexpr (F8)
@@ -1312,7 +1333,7 @@ __device__ __forceinline__ void shared_prefix_work(
 // kTL: the K/V loads stay in L2 (see kv_load).
 // kShared: workgroups from split_wgs on run shared_prefix_work (decode_attention_shared).
 template <int D, bool F8, bool kPad, bool kTL, bool kShared = false,
-          int KS = DecodeShape<D>::kSteps, int NBUF = 2>
+          int KS = DecodeShape<D>::kSteps, int NBUF = 2, bool kU = false>
 __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     const __bf16* __restrict__ q, void* k_cache_v, void* v_cache_v,
     const float* __restrict__ k_scale,
@@ -1390,8 +1411,9 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     load_split_inputs<D, F8, kPad>(q, block_table + static_cast<int64_t>(req) * mbpr, mbpr, qrow,
                                    hq, h, G, begin, end, lane, in, dr);
     SoftmaxState<D> st;
-    run_split<D, F8, kPad, kTL, KS, NBUF>(k_cache, v_cache, k_scale, v_scale, in, hkv / rep,
-                                          h / rep, begin, end, scale_log2, lane, st, dr);
+    run_split<D, F8, kPad, kTL, KS, NBUF, kU>(k_cache, v_cache, k_scale, v_scale, in,
+                                              hkv / rep, h / rep, begin, end, scale_log2, lane,
+                                              st, dr);
     const float l_tot = wave_sum_xor16_32(st.l);
     const bool live = j < G;
     const int head = h * G + j;
@@ -1489,7 +1511,7 @@ struct GroupShape {
     static constexpr int kMaxG = 16;                 // LDS: kWaves * 16 * D floats = 64 KiB
 };
 
-template <int D, bool F8, bool kPad, bool kTL>
+template <int D, bool F8, bool kPad, bool kTL, bool kU = false>
 __global__ __launch_bounds__(64 * GroupShape<D>::kWaves) void decode_group_kernel(
     const __bf16* __restrict__ q, void* k_cache_v, void* v_cache_v,
     const float* __restrict__ k_scale,
@@ -1541,8 +1563,9 @@ __global__ __launch_bounds__(64 * GroupShape<D>::kWaves) void decode_group_kerne
     }
     SoftmaxState<D> st;
     if (begin < end) {
-        run_split<D, F8, kPad, kTL>(k_cache, v_cache, k_scale, v_scale, in, hkv / rep, h / rep,
-                                    begin, end, scale_log2, lane, st, dr);
+        run_split<D, F8, kPad, kTL, DecodeShape<D>::kSteps, 2, kU>(
+            k_cache, v_cache, k_scale, v_scale, in, hkv / rep, h / rep, begin, end, scale_log2,
+            lane, st, dr);
     } else {
 #pragma unroll
         for (int n = 0; n < NV; ++n) st.acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1691,7 +1714,7 @@ struct SharedParts {
     int nwg = 0;          // workgroups of the prefix work (a multiple of 8)
 };
 
-template <int D, bool F8, bool kPad>
+template <int D, bool F8, bool kPad, bool kU = false>
 hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache,
                          const float* k_scale, const float* v_scale,
                          const int32_t* block_table, const int32_t* context_lens, void* output,
@@ -1703,12 +1726,13 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
     // rep query heads each; virtual head v reads cache head v / rep.
     const int rep = decode_head_rep(hq / hkv);
     hkv *= rep;
-    // Padded rows and virtual heads read lines twice: those loads stay in L2.
-    const bool tl = kPad || rep > 1;
+    // Padded rows, virtual heads and 2-byte pieces read lines more than once: those loads
+    // stay in L2.
+    const bool tl = kPad || rep > 1 || kU;
     if (plan.group) {
         const int64_t groups = static_cast<int64_t>(it.num_items) * hkv;
         auto go = [&](auto tl_tag) {
-            decode_group_kernel<D, F8, kPad, decltype(tl_tag)::value>
+            decode_group_kernel<D, F8, kPad, decltype(tl_tag)::value, kU>
                 <<<static_cast<unsigned>(groups), 64 * GroupShape<D>::kWaves, 0, stream>>>(
                     static_cast<const __bf16*>(q), const_cast<void*>(k_cache),
                     const_cast<void*>(v_cache), k_scale, v_scale, block_table, context_lens,
@@ -1749,7 +1773,10 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
         // 139.4 -> 137.6 us, d=96 154.8 -> 152.3, d=192 195.0 -> 175.8.
         constexpr int KSp = D == 128 ? 3 : D == 256 ? 6 : DecodeShape<D>::kSteps;
         auto kernel = decode_split_kernel<D, F8, kPad, kTLv, kShv>;
-        if constexpr (!F8 && kPad && !kShv && KSp < DecodeShape<D>::kSteps) {
+        if constexpr (kU) {
+            kernel = decode_split_kernel<D, F8, kPad, kTLv, kShv, DecodeShape<D>::kSteps, 2,
+                                         true>;
+        } else if constexpr (!F8 && kPad && !kShv && KSp < DecodeShape<D>::kSteps) {
             if (dr <= KSp * 32) kernel = decode_split_kernel<D, F8, kPad, kTLv, kShv, KSp, 2>;
         }
         kernel<<<total_wgs, 256, 0, stream>>>(
@@ -1761,7 +1788,7 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
             split_wgs);
     };
     if (shr) {
-        if constexpr (!F8) {
+        if constexpr (!F8 && !kU) {
             if (tl)
                 go(std::true_type{}, std::true_type{});
             else if constexpr (!kPad)
@@ -1907,11 +1934,20 @@ hipError_t decode_attention(const void* q, const void* k_cache, const void* v_ca
                 items.max_slots};
     const int D = decode_mfma_dim(head_dim);
     const bool pad = D != head_dim;
+    // Caches whose rows are not 16-byte aligned run the kernels with 2-byte piece loads.
+    const bool unaligned =
+        ((reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) & 15u) != 0;
 #define CCI_DECODE(DD, PP)                                                                   \
-    return launch_decode<DD, false, PP>(q, k_cache, v_cache, nullptr, nullptr, block_table, \
-                                        context_lens, output, it, max_blocks_per_req,        \
-                                        num_q_heads, num_kv_heads, plan, workspace, stream,  \
-                                        head_dim)
+    return unaligned                                                                          \
+               ? launch_decode<DD, false, PP, true>(q, k_cache, v_cache, nullptr, nullptr,    \
+                                                    block_table, context_lens, output, it,    \
+                                                    max_blocks_per_req, num_q_heads,          \
+                                                    num_kv_heads, plan, workspace, stream,    \
+                                                    head_dim)                                 \
+               : launch_decode<DD, false, PP>(q, k_cache, v_cache, nullptr, nullptr,          \
+                                              block_table, context_lens, output, it,          \
+                                              max_blocks_per_req, num_q_heads, num_kv_heads,  \
+                                              plan, workspace, stream, head_dim)
     switch (D) {
         case 64:
             if (pad) CCI_DECODE(64, true);

@@ -1,11 +1,14 @@
-// Generic paged attention (any head_dim <= 256, any GQA ratio, any cache block size).
+// Generic paged prefill attention (any head_dim <= 256, any GQA ratio, any cache block
+// size, any 2-byte-aligned view).
 //
-// Coverage path for the shapes the MFMA kernels do not specialise (head_dim 32/80/96/
-// 112/120/192, GQA groups above 16, non-16 cache blocks for prefill). Same semantics as the
-// reference launchers (decode_attn.cu:364-473, prefill_attn.cu:43-242): one wavefront per
-// (query row, q_head); 64 positions per step, one per lane, scores reduced with
-// cross-lane max/sum; each lane accumulates up to 4 output dims over the step's positions
-// with an online softmax. Scalar fp32, not tuned.
+// Coverage path for the prefill shapes the MFMA kernels do not take (head dims that are not
+// a multiple of 8, block sizes that are not a multiple of 16, caches that are only 2-byte
+// aligned, head_dim 256 past 4096 table blocks). Same semantics as the reference launcher
+// (prefill_attn.cu:43-242): one wavefront per (query row, q_head); 64 positions per step,
+// one per lane, scores reduced with cross-lane max/sum; each lane accumulates up to 4
+// output dims over the step's positions with an online softmax. Scalar fp32, not tuned.
+// Also the row copies and the table expansion that put unaligned q / output views and
+// blocks of 16k tokens on the MFMA paths.
 #include <algorithm>
 
 #include "attn_common.hpp"
@@ -78,25 +81,6 @@ __device__ void attend_row(const __bf16* __restrict__ q_vec, const __bf16* __res
         const int d = lane + x * kWave;
         if (d < head_dim) out_vec[d] = static_cast<__bf16>(acc[x] * inv);
     }
-}
-
-__global__ __launch_bounds__(64) void generic_decode_kernel(
-    const __bf16* __restrict__ q, const __bf16* __restrict__ k_cache,
-    const __bf16* __restrict__ v_cache, const int32_t* __restrict__ block_table,
-    const int32_t* __restrict__ context_lens, __bf16* __restrict__ out, int mbpr, int hq,
-    int hkv, int head_dim, int block_size, float scale_log2) {
-    const int b = blockIdx.x / hq;
-    const int qh = blockIdx.x % hq;
-    __bf16* o = out + (static_cast<int64_t>(b) * hq + qh) * head_dim;
-    const int ctx = context_lens[b];
-    if (ctx <= 0 || (ctx + block_size - 1) / block_size > mbpr) {
-        for (int d = threadIdx.x; d < head_dim; d += kWave) o[d] = static_cast<__bf16>(0.f);
-        return;
-    }
-    const int kvh = qh / (hq / hkv);
-    attend_row(q + (static_cast<int64_t>(b) * hq + qh) * head_dim, k_cache, v_cache,
-               block_table + static_cast<int64_t>(b) * mbpr, ctx, kvh, head_dim, hkv,
-               block_size, mbpr, scale_log2, 1e-6f, o);
 }
 
 __global__ __launch_bounds__(64) void generic_prefill_kernel(
@@ -198,21 +182,6 @@ hipError_t expand_block_table(const int32_t* block_table, int32_t* out, int rows
                               int max_blocks_per_req, int k, hipStream_t stream) {
     const int64_t entries = static_cast<int64_t>(rows) * max_blocks_per_req * k;
     expand_table_kernel<<<copy_grid(entries), 256, 0, stream>>>(block_table, out, entries, k);
-    return hipGetLastError();
-}
-
-hipError_t generic_decode_attention(const void* q, const void* k_cache, const void* v_cache,
-                                    const int32_t* block_table, const int32_t* context_lens,
-                                    void* output, int batch_size, int max_blocks_per_req,
-                                    int num_q_heads, int num_kv_heads, int head_dim,
-                                    int block_size, hipStream_t stream) {
-    const float scale_log2 = kLog2e / sqrtf(static_cast<float>(head_dim));
-    const int64_t grid = static_cast<int64_t>(batch_size) * num_q_heads;
-    generic_decode_kernel<<<static_cast<unsigned>(grid), kWave, 0, stream>>>(
-        static_cast<const __bf16*>(q), static_cast<const __bf16*>(k_cache),
-        static_cast<const __bf16*>(v_cache), block_table, context_lens,
-        static_cast<__bf16*>(output), max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
-        block_size, scale_log2);
     return hipGetLastError();
 }
 

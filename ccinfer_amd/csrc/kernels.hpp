@@ -183,13 +183,7 @@ hipError_t qkv_prologue(const void* qkv, const void* q_norm_w, const void* k_nor
                         int rope_cache_max_position, int max_slots, float eps,
                         hipStream_t stream);
 
-// ---- generic (any head_dim / GQA ratio / block size) ----------------------
-hipError_t generic_decode_attention(const void* q, const void* k_cache, const void* v_cache,
-                                    const int32_t* block_table, const int32_t* context_lens,
-                                    void* output, int batch_size, int max_blocks_per_req,
-                                    int num_q_heads, int num_kv_heads, int head_dim,
-                                    int block_size, hipStream_t stream);
-
+// ---- generic prefill (any head_dim / GQA ratio / block size / alignment) ----
 hipError_t generic_prefill_attention(const void* q, const void* k_cache, const void* v_cache,
                                      const int32_t* block_table,
                                      const int32_t* query_start_loc,

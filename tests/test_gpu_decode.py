@@ -219,8 +219,9 @@ def _offset_view(t: torch.Tensor, elems: int = 1) -> torch.Tensor:
 @pytest.mark.parametrize("which", ["q", "k_cache", "v_cache", "output"])
 def test_two_byte_aligned_views(gpu, which):
     """The reference launchers take any bf16 view. A q or output view that is only 2-byte
-    aligned runs the MFMA kernels on workspace copies of its rows (bit-equal to the aligned
-    call); a cache that is only 2-byte aligned runs the generic kernels."""
+    aligned runs the MFMA kernels on workspace copies of its rows; a cache that is only
+    2-byte aligned runs them with 2-byte piece loads. Either way bit-equal to the aligned
+    call."""
     say(f"decode with a 2-byte aligned {which}")
     w = W.decode_batched(device=gpu, seed=17, batch=6, ctx_lo=20, ctx_hi=600, with_write=False)
     meta = w.device_meta(gpu)
@@ -235,11 +236,45 @@ def test_two_byte_aligned_views(gpu, which):
                            meta["context_lens"], output=out)
     torch.cuda.synchronize()
     assert_attn_close(f32(got), oracle_decode(w), f"misaligned {which}")
-    if which in ("q", "output"):
-        aligned = decode_attention(w.q, w.k_cache, w.v_cache, meta["block_table"],
-                                   meta["context_lens"])
-        torch.cuda.synchronize()
-        assert torch.equal(got, aligned)
+    aligned = decode_attention(w.q, w.k_cache, w.v_cache, meta["block_table"],
+                               meta["context_lens"])
+    torch.cuda.synchronize()
+    assert torch.equal(got, aligned)
+
+
+@pytest.mark.parametrize("batch,ctx_lo,ctx_hi,hq,hkv,d,offset", [
+    (64, 128, 4096, 16, 8, 128, 1),   # configs[1]: flat plan with merge
+    (1, 512, 512, 16, 8, 128, 3),     # group plan
+    (2, 100, 3000, 16, 8, 256, 1),    # fixed split plan, head dim 256
+    (300, 1, 400, 16, 8, 96, 5),      # indexed flat plan, padded head dim
+    (40, 50, 900, 64, 2, 64, 7),      # 32 query heads per kv head (virtual heads)
+])
+def test_two_byte_aligned_caches_on_mfma_path(gpu, batch, ctx_lo, ctx_hi, hq, hkv, d, offset):
+    """K and V caches offset by an odd number of elements (only 2-byte aligned): the MFMA
+    kernels with 2-byte piece loads, bit-equal to the same call on aligned copies, every
+    decode plan; the fused KV write falls back to its own launch and still writes the same
+    rows."""
+    from ccinfer_amd import decode_attention_write_kv
+    say(f"decode 2-byte aligned caches B={batch} ctx=[{ctx_lo},{ctx_hi}] hq={hq} hkv={hkv} "
+        f"d={d}")
+    w = W.decode_batched(device=gpu, seed=batch + d + 1, batch=batch, ctx_lo=ctx_lo,
+                         ctx_hi=ctx_hi, hq=hq, hkv=hkv, d=d, with_write=True)
+    meta = w.device_meta(gpu)
+    want = decode_attention(w.q, w.k_cache, w.v_cache, meta["block_table"],
+                            meta["context_lens"])
+    kc, vc = _offset_view(w.k_cache, offset), _offset_view(w.v_cache, offset)
+    got = decode_attention(w.q, kc, vc, meta["block_table"], meta["context_lens"])
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    # with the new token's write: same output and same cache rows as on the aligned caches
+    ka, va = w.k_cache.clone(), w.v_cache.clone()
+    want_w = decode_attention_write_kv(w.q, w.k_new, w.v_new, ka, va, meta["block_table"],
+                                       meta["context_lens"])
+    got_w = decode_attention_write_kv(w.q, w.k_new, w.v_new, kc, vc, meta["block_table"],
+                                      meta["context_lens"])
+    torch.cuda.synchronize()
+    assert torch.equal(got_w, want_w)
+    assert torch.equal(kc, ka) and torch.equal(vc, va)
 
 
 @pytest.mark.parametrize("batch,ctx_lo,ctx_hi,hq,hkv,d,offset", [
