@@ -32,10 +32,11 @@
  * move q, output and K/V cache rows in 16-byte pieces. A bf16 decode / prefill call whose
  * q or output view is only 2-byte aligned copies q (and, for prefill, output) into the
  * workspace, runs the MFMA kernels there and copies the output rows back (same bits as an
- * aligned call); a k_cache or v_cache pointer that is not 16-byte aligned runs the generic
- * kernels (same results within the tolerance, much slower). The fp8 calls, which have the
- * MFMA paths only, return CCINFER_ERR_INVALID_ARGUMENT for any such pointer (and for
- * k_scale / v_scale not 16-byte aligned).
+ * aligned call). A k_cache or v_cache pointer that is not 16-byte aligned runs the decode
+ * MFMA kernels with 2-byte loads (same bits, ~1.7x the time) and the generic prefill kernel
+ * (same results within the tolerance, much slower). The fp8 calls, which have the MFMA
+ * paths only, return CCINFER_ERR_INVALID_ARGUMENT for any such pointer (and for k_scale /
+ * v_scale not 16-byte aligned).
  */
 #ifndef CCINFER_ATTN_H
 #define CCINFER_ATTN_H
