@@ -1090,13 +1090,7 @@ constexpr int kSharedMinTokens = 64;      // shorter common prefixes are not wor
 constexpr int kSharedMaxItems = 2048;     // the planner's hash table holds 2x this many keys
 constexpr int kSharedHash = 4096;
 constexpr int kSharedCols = 16;           // columns of the 16x16x32 MFMA tile
-#ifndef CCI_SH_SLOTS
-#define CCI_SH_SLOTS 128
-#endif
-#ifndef CCI_SH_W2
-#define CCI_SH_W2 0
-#endif
-constexpr int kSharedSlotsPerHead = CCI_SH_SLOTS;  // shared-kernel wavefronts per kv head
+constexpr int kSharedSlotsPerHead = 128;  // shared-kernel wavefronts per kv head
 
 struct SharedPlan {
     int32_t* nsub;      // [1] subgroups
@@ -2005,7 +1999,7 @@ SharedLayout shared_layout(int B, int mbpr, int hq, int hkv, int head_dim) {
     SharedLayout L{};
     // the suffixes: plain decode's split plan (never the group plan, whose rows do not go
     // through the merge), with the merge always on
-    L.plan = plan_decode(B, hq, hkv, mbpr * kBlock, true, CCI_SH_W2 != 0, false);
+    L.plan = plan_decode(B, hq, hkv, mbpr * kBlock, true, false, false);
     const int d = decode_mfma_dim(head_dim);
     const size_t rows = partial_rows(B, hq, L.plan);
     L.regular = L.plan.flat_index ? index_offset(rows, d, B, hq) + index_bytes(B, L.plan.slots)
