@@ -800,9 +800,22 @@ def sweep_generic() -> None:
         print(f"| prefill configs[2], {bs}-token blocks (MFMA, 16-token table) | {base:.1f} | "
               f"{t:.1f} | {t / base:.2f}x |", flush=True)
     bt8 = rebin(w, 8)
-    t = pre(w.q, out, bt8, bt8.shape[1], 8, 2)
-    print(f"| prefill configs[2], 8-token blocks (generic) | {base:.1f} | {t:.1f} | "
-          f"{t / base:.0f}x |", flush=True)
+    t = pre(w.q, out, bt8, bt8.shape[1], 8, 5)
+    print(f"| prefill configs[2], 8-token blocks (MFMA tile kernel, register staging) | "
+          f"{base:.1f} | {t:.1f} | {t / base:.2f}x |", flush=True)
+    kshift, vshift = misaligned(w.k_cache), misaligned(w.v_cache)
+
+    def pre_k():
+        rc = lib.ccinfer_prefill_attention(w.q.data_ptr(), kshift.data_ptr(), vshift.data_ptr(),
+                                           meta["block_table"].data_ptr(),
+                                           meta["query_start_loc"].data_ptr(),
+                                           meta["context_lens"].data_ptr(), out.data_ptr(),
+                                           w.batch, T, w.mbpr, w.hq, w.hkv, w.d, 16,
+                                           ws.data_ptr(), n, stream.cuda_stream)
+        assert rc == 0, rc
+    t = time_loop(pre_k, 5, 2, stream)[0] * 1e3
+    print(f"| prefill configs[2], k / v caches 2-byte aligned (MFMA tile kernel, shifted "
+          f"16-byte loads) | {base:.1f} | {t:.1f} | {t / base:.2f}x |", flush=True)
 
 
 def main():

@@ -90,6 +90,39 @@ __device__ __forceinline__ uint32_t e4m3x2_to_bf16x2(uint32_t w, float pow2 = 1.
                                             static_cast<int>(w), pow2, kHi));
 }
 
+// The N (2 or 4) 32-bit words at p, a 2-byte-aligned address `a` bytes past a 16-byte
+// boundary (a per lane): the aligned 16-byte granules that hold those bytes are loaded --
+// the second one only by lanes whose piece reaches into it, so no granule without one of
+// the piece's bytes is touched (nothing outside the pages the data occupies) -- and the
+// words are shifted into place. Two 16-byte loads per piece instead of eight 2-byte ones.
+template <int N, typename T>
+__device__ __forceinline__ T load_shifted(const void* p) {
+    const uintptr_t u = reinterpret_cast<uintptr_t>(p);
+    const int a = static_cast<int>(u & 15u);
+    const u32x4* g = reinterpret_cast<const u32x4*>(u - static_cast<uintptr_t>(a));
+    T out;
+    const u32x4 lo = g[0];
+    const bool two = a + 4 * N > 16;  // the piece reaches into the next granule
+    const u32x4 hi = two ? g[1] : u32x4{0u, 0u, 0u, 0u};
+    const uint32_t w[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    const int q = a >> 2;          // whole words
+    const bool half = (a & 2) != 0;  // plus one 16-bit half
+    auto word = [&](int j) -> uint32_t {
+        uint32_t x0 = 0, x1 = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            if (q == k) {
+                x0 = w[(j + k) & 7];
+                x1 = w[(j + k + 1) & 7];
+            }
+        }
+        return half ? __builtin_amdgcn_alignbyte(x1, x0, 2) : x0;
+    };
+#pragma unroll
+    for (int j = 0; j < N; ++j) out[j] = word(j);
+    return out;
+}
+
 __device__ __forceinline__ u32x4 load16(const void* p) {
     return *reinterpret_cast<const u32x4*>(p);
 }

@@ -169,6 +169,18 @@ int prefill_entry(const void* q, const void* k_cache, const void* v_cache,
                                           num_q_heads, num_kv_heads, head_dim,
                                           cache_block_size);
     if (!rt.fast || !caches_aligned(k_cache, v_cache)) {
+        // Other block sizes, head dims and cache alignments: the MFMA tile kernel with
+        // element-wise staging where its table row fits LDS, else the scalar kernel.
+        if (prefill_any_supported(num_q_heads, num_kv_heads, head_dim, max_blocks_per_req)) {
+            const size_t need_any = prefill_any_workspace_bytes(
+                batch_size, total_query_tokens, num_q_heads, num_kv_heads, head_dim);
+            if (workspace == nullptr || workspace_bytes < need_any)
+                return CCINFER_ERR_INVALID_ARGUMENT;
+            return map_hip_error(prefill_attention_any(
+                q, k_cache, v_cache, block_table, query_start_loc, context_lens, output,
+                batch_size, total_query_tokens, max_blocks_per_req, num_q_heads, num_kv_heads,
+                head_dim, cache_block_size, workspace, as_stream(stream)));
+        }
         return map_hip_error(generic_prefill_attention(
             q, k_cache, v_cache, block_table, query_start_loc, context_lens, output, batch_size,
             total_query_tokens, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
@@ -535,9 +547,16 @@ size_t ccinfer_prefill_workspace_size(int batch_size, int total_query_tokens,
     const PrefillRoute rt = prefill_route(batch_size, total_query_tokens, max_blocks_per_req,
                                           num_q_heads, num_kv_heads, head_dim,
                                           cache_block_size);
-    if (!rt.fast) return 0;
-    // it covers the fp8 entry (16-token blocks, aligned views only) too
-    return rt.need(true);
+    // the MFMA-kernel route (it covers the fp8 entry too: 16-token blocks, aligned views)
+    // and the any-layout route, which a call takes for caches that are not 16-byte aligned
+    // or shapes the first does not take
+    const size_t fast = rt.fast ? rt.need(true) : 0;
+    const size_t any = prefill_any_supported(num_q_heads, num_kv_heads, head_dim,
+                                             max_blocks_per_req)
+                           ? prefill_any_workspace_bytes(batch_size, total_query_tokens,
+                                                         num_q_heads, num_kv_heads, head_dim)
+                           : 0;
+    return std::max(fast, any);
 }
 
 int ccinfer_prefill_attention(const void* q, const void* k_cache, const void* v_cache,

@@ -546,7 +546,9 @@ __device__ __forceinline__ T kv_load(const T* p) {
 // kU: the cache rows are only 2-byte aligned (a cache pointer offset by an odd number of
 // elements; the reference kernels read bf16 scalars, so they accept one). Each piece is
 // then assembled from 2-byte loads -- neighbouring lanes read neighbouring elements, so a
-// wavefront still touches whole lines -- and the rest of the kernel is unchanged.
+// wavefront still touches whole lines -- and the rest of the kernel is unchanged. (Two
+// aligned 16-byte loads shifted into place, as the prefill staging does, hold twice the
+// registers per piece in flight: 48-1198 spilled VGPRs here, 7.6x instead of 1.7x.)
 template <bool kTL, bool kU, typename T>
 __device__ __forceinline__ T kv_piece(const __bf16* p) {
     if constexpr (!kU) {

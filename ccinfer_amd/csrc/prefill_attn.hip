@@ -108,6 +108,7 @@ __device__ void block_inclusive_scan(int* a, int n, int* part) {
 // ---------------------------------------------------------------------------
 // Planner: one workgroup of 1024 threads.
 // ws layout: counts[0] = #tiles, counts[1] = #decode items; tiles[max_tiles]; dec[B].
+// split_dec: single-token requests become decode items (else one-row tiles).
 // kBig: more than kMaxPlanRequests requests; the per-request arrays then live in the
 // workspace (big_ntiles / big_scan, B ints each) instead of LDS.
 // ---------------------------------------------------------------------------
@@ -116,7 +117,7 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(
     const int32_t* __restrict__ qsl, const int32_t* __restrict__ context_lens, int batch_size,
     int total_tokens, int tile_tokens, int32_t* __restrict__ counts,
     TileEntry* __restrict__ tiles, int32_t* __restrict__ dec_req, uint32_t* __restrict__ zero_row,
-    int zero_words, int* __restrict__ big_ntiles, int* __restrict__ big_scan) {
+    int zero_words, int* __restrict__ big_ntiles, int* __restrict__ big_scan, int split_dec) {
     __shared__ int lds_ntiles[kBig ? 1 : kMaxPlanRequests];
     __shared__ int lds_scan[kBig ? 1 : kMaxPlanRequests];
     // Each request's query length and cached prefix, read once (the bucket pass and the
@@ -155,7 +156,7 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(
         }
         int n = 0;
         if (qlen > 0 && prefix >= 0 && qb >= 0 && rows > 0) {
-            if (qlen == 1)
+            if (qlen == 1 && split_dec)
                 isdec = 1;
             else
                 n = (rows + tile_tokens - 1) / tile_tokens;
@@ -292,6 +293,83 @@ __device__ __forceinline__ void stage_issue(__bf16* lk, __bf16* lv, uint8_t* lva
     }
 }
 
+// Any-layout staging (cache rows of any 2-byte alignment, blocks of any size `bs`, any
+// head dim dr <= D): the same tile layout as stage_issue, built in two steps so the loads'
+// latency overlaps the attention of the current tile -- stage_any_load reads each lane's
+// 16-byte chunk element by element (elements past dr, rows past the context or in
+// unmapped blocks read as zeros; 16-byte loads when `vec`: rows 16-byte aligned; two
+// shifted 16-byte loads when only the alignment is off) and records the rows' validity;
+// stage_any_write stores the chunks into the tile.
+template <int D>
+struct AnyStage {
+    u32x4 k[PrefillShape<D>::kLoadsPerThread];
+    u32x4 v[PrefillShape<D>::kLoadsPerThread];
+};
+
+template <int D>
+__device__ __forceinline__ void stage_any_load(AnyStage<D>& r, uint8_t* lvalid,
+                                               const __bf16* k_cache, const __bf16* v_cache,
+                                               const int32_t* lbt, int key_base, int ctx,
+                                               int nblk, int kv_head, int hkv, int dr, int bs,
+                                               bool vec) {
+    const bool shifted = !vec && dr % 8 == 0;
+    constexpr int CPR = PrefillShape<D>::kCPR;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int x = 0; x < PrefillShape<D>::kLoadsPerThread; ++x) {
+        const int p = (x * kWaves + wave) * 64 + lane;
+        const int row = p / CPR;
+        const int lchunk = (p % CPR) ^ (chunk_swizzle<D>(row) & (CPR - 1));
+        const int key = key_base + row;
+        const int lb = key / bs;
+        int pb = -1;
+        if (key < ctx && lb < nblk) pb = lbt[lb];
+        const int64_t base =
+            ((static_cast<int64_t>(pb < 0 ? 0 : pb) * bs + key % bs) * hkv + kv_head) * dr;
+        const uint16_t* ks = reinterpret_cast<const uint16_t*>(k_cache) + base;
+        const uint16_t* vs = reinterpret_cast<const uint16_t*>(v_cache) + base;
+        u32x4 kw{0u, 0u, 0u, 0u}, vw{0u, 0u, 0u, 0u};
+        if (vec || shifted) {
+            // rows of a multiple of 8 elements: a chunk lies wholly inside its row; one
+            // 16-byte load when the rows are 16-byte aligned, else two shifted (load_shifted)
+            if (pb >= 0 && lchunk * 8 < dr) {
+                if (vec) {
+                    kw = *reinterpret_cast<const u32x4*>(ks + lchunk * 8);
+                    vw = *reinterpret_cast<const u32x4*>(vs + lchunk * 8);
+                } else {
+                    kw = load_shifted<4, u32x4>(ks + lchunk * 8);
+                    vw = load_shifted<4, u32x4>(vs + lchunk * 8);
+                }
+            }
+        } else if (pb >= 0) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int e = lchunk * 8 + i;
+                if (e < dr) {
+                    kw[i >> 1] |= static_cast<uint32_t>(ks[e]) << (16 * (i & 1));
+                    vw[i >> 1] |= static_cast<uint32_t>(vs[e]) << (16 * (i & 1));
+                }
+            }
+        }
+        r.k[x] = kw;
+        r.v[x] = vw;
+        if ((p % CPR) == 0) lvalid[row] = static_cast<uint8_t>(pb >= 0);
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void stage_any_write(const AnyStage<D>& r, __bf16* lk, __bf16* lv) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int x = 0; x < PrefillShape<D>::kLoadsPerThread; ++x) {
+        const int p = (x * kWaves + wave) * 64 + lane;
+        *reinterpret_cast<u32x4*>(lk + p * 8) = r.k[x];
+        *reinterpret_cast<u32x4*>(lv + p * 8) = r.v[x];
+    }
+}
+
 // V^T MFMA operand for dim tile n of a 32-key half, read transposed straight out of the
 // row-major [key][dim] LDS tile with ds_read_b64_tr_b16 (gfx950). Within a 16-lane group g,
 // result lane i gets element e from the lane (4e + i/4) of the group, 16-bit word i%4.
@@ -326,8 +404,10 @@ constexpr float kRescaleSlack = 8.0f;
 constexpr float kMaxInit = -1.0e30f;
 
 // kPad: q / cache / output rows hold dr < D dims; the kernel runs at D with the missing dims
-// zero.
-template <int D, bool kPad = false>
+// zero. kAny: any layout -- rows of any head dim dr <= D and any 2-byte alignment, cache
+// blocks of `block_size` tokens -- through element-wise staging (stage_any_*), Q loads and
+// output stores.
+template <int D, bool kPad = false, bool kAny = false>
 __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ k_cache,
     const __bf16* __restrict__ v_cache, const int32_t* __restrict__ block_table,
@@ -335,8 +415,12 @@ __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
     __bf16* __restrict__ out, const int32_t* __restrict__ counts,
     const TileEntry* __restrict__ tiles, const __bf16* __restrict__ zero_row, int total_tokens,
     int mbpr, int hq, int hkv, int block_size, float scale_log2, int dr) {
-    (void)block_size;  // the fast path is specialised for 16-token blocks
-    const int ds = kPad ? dr : D;  // row stride of q / cache / output (elements)
+    if constexpr (!kAny) block_size = kBlock;  // the fast path is specialised for 16-token blocks
+    // kAny: rows 16-byte aligned (cache pointers aligned, dr a multiple of 8) load whole chunks
+    [[maybe_unused]] const bool any_vec =
+        kAny && dr % 8 == 0 &&
+        ((reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) & 15u) == 0;
+    const int ds = (kPad || kAny) ? dr : D;  // row stride of q / cache / output (elements)
     using Sh = PrefillShape<D>;
     constexpr int QT = Sh::kQT;
     constexpr int QW = Sh::kQW;
@@ -397,9 +481,20 @@ __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
         const __bf16* qv = q + (static_cast<int64_t>(qb + (live ? tq : 0)) * hq + q_head) * ds;
 #pragma unroll
         for (int kk = 0; kk < S; ++kk) {
-            const bool ok = !kPad || (kk * 4 + g) * 8 < dr;
-            u32x4 w = load16(qv + (ok ? (kk * 4 + g) * 8 : 0));
-            if (!live || !ok) w = u32x4{0, 0, 0, 0};
+            u32x4 w = u32x4{0, 0, 0, 0};
+            if constexpr (kAny) {
+                const uint16_t* qe = reinterpret_cast<const uint16_t*>(qv);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const int e = (kk * 4 + g) * 8 + i;
+                    if (e < dr) w[i >> 1] |= static_cast<uint32_t>(qe[e]) << (16 * (i & 1));
+                }
+            } else {
+                const bool ok = !kPad || (kk * 4 + g) * 8 < dr;
+                w = load16(qv + (ok ? (kk * 4 + g) * 8 : 0));
+                if (!ok) w = u32x4{0, 0, 0, 0};
+            }
+            if (!live) w = u32x4{0, 0, 0, 0};
             qop[qt][kk] = __builtin_bit_cast(bf16x8, w);
         }
     }
@@ -428,7 +523,7 @@ __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
     __syncthreads();
     // Positions past the table row are invalid, so only min(visible, mbpr) entries matter;
     // the host routes tables longer than kMaxTableLds to the generic kernel.
-    const int nblk_vis = (kv_end + kBlock - 1) / kBlock;
+    const int nblk_vis = (kv_end + block_size - 1) / block_size;
     const int nblk = min(nblk_vis, mbpr);
     for (int lb = threadIdx.x; lb < nblk; lb += kThreads) {
         const int pb = req_blocks[lb];
@@ -438,9 +533,16 @@ __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
     __syncthreads();
     const bool holes = s_holes != 0 || nblk_vis > mbpr;
 
-    stage_issue<D, kPad>(lds_k0, lds_v0, lds_valid0, k_cache, v_cache, zero_row, lds_bt, 0, ctx,
-                         nblk, kvh, hkv, dr);
-    __builtin_amdgcn_s_waitcnt(0);  // this wavefront's direct-to-LDS loads have landed
+    if constexpr (kAny) {
+        AnyStage<D> r0;
+        stage_any_load<D>(r0, lds_valid0, k_cache, v_cache, lds_bt, 0, ctx, nblk, kvh, hkv, dr,
+                          block_size, any_vec);
+        stage_any_write<D>(r0, lds_k0, lds_v0);
+    } else {
+        stage_issue<D, kPad>(lds_k0, lds_v0, lds_valid0, k_cache, v_cache, zero_row, lds_bt, 0,
+                             ctx, nblk, kvh, hkv, dr);
+        __builtin_amdgcn_s_waitcnt(0);  // this wavefront's direct-to-LDS loads have landed
+    }
     __syncthreads();
 
     // Attention over one staged 64-key tile, straight-line so the scheduler can overlap the
@@ -551,9 +653,14 @@ __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
         __bf16* nv = B == 0 ? lds_v1 : lds_v0;
         uint8_t* nvalid = B == 0 ? lds_valid1 : lds_valid0;
         const bool more = t + 1 < ntiles;
+        [[maybe_unused]] AnyStage<D> rn;
         if (more) {
-            stage_issue<D, kPad>(nk, nv, nvalid, k_cache, v_cache, zero_row, lds_bt,
-                                 (t + 1) * kKeysPerTile, ctx, nblk, kvh, hkv, dr);
+            if constexpr (kAny)
+                stage_any_load<D>(rn, nvalid, k_cache, v_cache, lds_bt, (t + 1) * kKeysPerTile,
+                                  ctx, nblk, kvh, hkv, dr, block_size, any_vec);
+            else
+                stage_issue<D, kPad>(nk, nv, nvalid, k_cache, v_cache, zero_row, lds_bt,
+                                     (t + 1) * kKeysPerTile, ctx, nblk, kvh, hkv, dr);
         }
         const int key0 = t * kKeysPerTile;
         if (key0 <= wave_max_key) {
@@ -562,7 +669,11 @@ __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
                                        : ~0ull;
             attend_tile(ck, cv, vmask, key0, mask_tag);
         }
-        if (more) __builtin_amdgcn_s_waitcnt(0);  // next tile resident before the barrier
+        if constexpr (kAny) {
+            if (more) stage_any_write<D>(rn, nk, nv);
+        } else {
+            if (more) __builtin_amdgcn_s_waitcnt(0);  // next tile resident before the barrier
+        }
         __syncthreads();
     };
     using B0 = std::integral_constant<int, 0>;
@@ -594,6 +705,14 @@ __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
         __bf16* o = out + (static_cast<int64_t>(qb + tq) * hq + q_head) * ds;
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
+            if constexpr (kAny) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (16 * n + 4 * g + r < dr)
+                        reinterpret_cast<uint16_t*>(o)[16 * n + 4 * g + r] =
+                            static_cast<uint16_t>(pack_bf16x2(acc[qt][n][r] * inv, 0.f));
+                continue;
+            }
             if (kPad && 16 * n + 4 * g >= dr) continue;  // padded dims
             u32x2 w;
             w[0] = pack_bf16x2(acc[qt][n][0] * inv, acc[qt][n][1] * inv);
@@ -1493,11 +1612,11 @@ hipError_t prefill_impl(const void* q, const void* k_cache, const void* v_cache,
         int* big = reinterpret_cast<int*>(ws + L.big_off);
         prefill_plan_kernel<true><<<1, 1024, 0, stream>>>(
             query_start_loc, context_lens, batch_size, total_query_tokens, L.tile_tokens, counts,
-            tiles, dec, zero_row, decode_mfma_dim(head_dim) / 2, big, big + batch_size);
+            tiles, dec, zero_row, decode_mfma_dim(head_dim) / 2, big, big + batch_size, 1);
     } else {
         prefill_plan_kernel<false><<<1, 1024, 0, stream>>>(
             query_start_loc, context_lens, batch_size, total_query_tokens, L.tile_tokens, counts,
-            tiles, dec, zero_row, decode_mfma_dim(head_dim) / 2, nullptr, nullptr);
+            tiles, dec, zero_row, decode_mfma_dim(head_dim) / 2, nullptr, nullptr, 1);
     }
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
@@ -1586,6 +1705,95 @@ hipError_t prefill_attention(const void* q, const void* k_cache, const void* v_c
                                query_start_loc, context_lens, output, batch_size,
                                total_query_tokens, max_blocks_per_req, num_q_heads, num_kv_heads,
                                head_dim, block_size, workspace, stream, overlap);
+}
+
+// ---- any-layout prefill (the tile kernel with kAny) ----
+namespace {
+
+int any_dim(int dr) { return dr <= 64 ? 64 : dr <= 128 ? 128 : 256; }
+
+struct AnyLayout {
+    size_t counts_off, tiles_off, dec_off, big_off, total;
+    int max_tiles, tile_tokens;
+};
+
+AnyLayout any_layout(int batch_size, int total_query_tokens, int num_q_heads, int num_kv_heads,
+                     int head_dim) {
+    AnyLayout L{};
+    const int G = num_q_heads / num_kv_heads;
+    L.tile_tokens = (kWaves / heads_per_wg(G)) *
+                    (any_dim(head_dim) <= 128 ? PrefillShape<128>::kQW : PrefillShape<256>::kQW);
+    // every request may be a one-row tile here (single-token requests are tiles too)
+    L.max_tiles = total_query_tokens / L.tile_tokens + batch_size;
+    size_t off = 0;
+    L.counts_off = off;
+    off = align256(off + 2 * sizeof(int32_t));
+    L.tiles_off = off;
+    off = align256(off + static_cast<size_t>(L.max_tiles) * sizeof(TileEntry));
+    L.dec_off = off;
+    off = align256(off + static_cast<size_t>(batch_size) * sizeof(int32_t));
+    L.big_off = off;
+    if (batch_size > kMaxPlanRequests)
+        off = align256(off + 2 * static_cast<size_t>(batch_size) * sizeof(int32_t));
+    L.total = off;
+    return L;
+}
+
+}  // namespace
+
+bool prefill_any_supported(int num_q_heads, int num_kv_heads, int head_dim,
+                           int max_blocks_per_req) {
+    return num_kv_heads > 0 && num_q_heads % num_kv_heads == 0 && head_dim > 0 &&
+           head_dim <= 256 && max_blocks_per_req <= kMaxTableLds;
+}
+
+size_t prefill_any_workspace_bytes(int batch_size, int total_query_tokens, int num_q_heads,
+                                   int num_kv_heads, int head_dim) {
+    return any_layout(batch_size, total_query_tokens, num_q_heads, num_kv_heads, head_dim).total;
+}
+
+hipError_t prefill_attention_any(const void* q, const void* k_cache, const void* v_cache,
+                                 const int32_t* block_table, const int32_t* query_start_loc,
+                                 const int32_t* context_lens, void* output, int batch_size,
+                                 int total_query_tokens, int max_blocks_per_req, int num_q_heads,
+                                 int num_kv_heads, int head_dim, int block_size,
+                                 void* workspace, hipStream_t stream) {
+    const AnyLayout L =
+        any_layout(batch_size, total_query_tokens, num_q_heads, num_kv_heads, head_dim);
+    char* ws = static_cast<char*>(workspace);
+    int32_t* counts = reinterpret_cast<int32_t*>(ws + L.counts_off);
+    TileEntry* tiles = reinterpret_cast<TileEntry*>(ws + L.tiles_off);
+    int32_t* dec = reinterpret_cast<int32_t*>(ws + L.dec_off);
+    // single-token requests run as one-row tiles (the decode kernels take 16-token blocks)
+    if (batch_size > kMaxPlanRequests) {
+        int* big = reinterpret_cast<int*>(ws + L.big_off);
+        prefill_plan_kernel<true><<<1, 1024, 0, stream>>>(
+            query_start_loc, context_lens, batch_size, total_query_tokens, L.tile_tokens, counts,
+            tiles, dec, nullptr, 0, big, big + batch_size, 0);
+    } else {
+        prefill_plan_kernel<false><<<1, 1024, 0, stream>>>(
+            query_start_loc, context_lens, batch_size, total_query_tokens, L.tile_tokens, counts,
+            tiles, dec, nullptr, 0, nullptr, nullptr, 0);
+    }
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    const int G = num_q_heads / num_kv_heads;
+    const int U = num_kv_heads * (G / heads_per_wg(G));
+    const int64_t grid = static_cast<int64_t>(L.max_tiles) * U;
+    const float scale_log2 = kLog2e / sqrtf(static_cast<float>(head_dim));
+    auto go = [&](auto kernel) {
+        kernel<<<static_cast<unsigned>(grid), kThreads, 0, stream>>>(
+            static_cast<const __bf16*>(q), static_cast<const __bf16*>(k_cache),
+            static_cast<const __bf16*>(v_cache), block_table, query_start_loc, context_lens,
+            static_cast<__bf16*>(output), counts, tiles, nullptr, total_query_tokens,
+            max_blocks_per_req, num_q_heads, num_kv_heads, block_size, scale_log2, head_dim);
+        return hipGetLastError();
+    };
+    switch (any_dim(head_dim)) {
+        case 64: return go(prefill_tile_kernel<64, false, true>);
+        case 128: return go(prefill_tile_kernel<128, false, true>);
+        default: return go(prefill_tile_kernel<256, false, true>);
+    }
 }
 
 hipError_t prefill_attention_fp8(const void* q, const void* k_cache, const void* v_cache,

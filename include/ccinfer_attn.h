@@ -33,10 +33,10 @@
  * q or output view is only 2-byte aligned copies q (and, for prefill, output) into the
  * workspace, runs the MFMA kernels there and copies the output rows back (same bits as an
  * aligned call). A k_cache or v_cache pointer that is not 16-byte aligned runs the decode
- * MFMA kernels with 2-byte loads (same bits, ~1.7x the time) and the generic prefill kernel
- * (same results within the tolerance, much slower). The fp8 calls, which have the MFMA
- * paths only, return CCINFER_ERR_INVALID_ARGUMENT for any such pointer (and for k_scale /
- * v_scale not 16-byte aligned).
+ * MFMA kernels with 2-byte loads (same bits, ~1.7x the time) and the any-layout prefill
+ * tile kernel (~2.2x). The fp8 calls, which have the MFMA paths only, return
+ * CCINFER_ERR_INVALID_ARGUMENT for any such pointer (and for k_scale / v_scale not 16-byte
+ * aligned).
  */
 #ifndef CCINFER_ATTN_H
 #define CCINFER_ATTN_H
@@ -247,9 +247,10 @@ size_t ccinfer_prefill_workspace_size(int batch_size, int total_query_tokens,
  * query group size and head dims that are multiples of 8 up to 128 (at any size; those
  * below 64 / 128 run padded with zeros) or multiples of 16 up to 256 (up to 4096 blocks per
  * table row, counted in 16-token blocks), with cache blocks of any multiple of 16 tokens
- * (read through a 16-token table the call builds in the workspace); other shapes run the
- * generic kernel. A mixed batch's decode items run on `stream` ahead of the prompt
- * tiles. */
+ * (read through a 16-token table the call builds in the workspace). Other block sizes and
+ * head dims up to 256 run an MFMA tile kernel that stages rows element-wise (tables of up
+ * to 4096 blocks per row; beyond that a scalar kernel). A mixed batch's decode items run
+ * on `stream` ahead of the prompt tiles. */
 int ccinfer_prefill_attention(const void* q, const void* k_cache, const void* v_cache,
                               const int32_t* block_table, const int32_t* query_start_loc,
                               const int32_t* context_lens, void* output, int batch_size,

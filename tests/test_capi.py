@@ -128,8 +128,9 @@ def test_decode_workspace_size(lib):
 
 def test_prefill_workspace_size_for_other_block_sizes(lib):
     """Blocks of 16·k tokens run the MFMA prefill through a 16-token table built in the
-    workspace: the size is that of the 16-token shape plus the table; other block sizes run
-    the generic kernel (no workspace)."""
+    workspace: the size is that of the 16-token shape plus the table. Other block sizes run
+    the any-layout tile kernel: the planner's tile list only, the same for every block size;
+    past 4096 table blocks, the scalar kernel (no workspace)."""
     f = lib.ccinfer_prefill_workspace_size
     base = f(4, 512, 64, 16, 8, 128, 16)
     assert base > 0
@@ -137,8 +138,11 @@ def test_prefill_workspace_size_for_other_block_sizes(lib):
         n = f(4, 512, 64 // k, 16, 8, 128, 16 * k)
         table = (4 * 64 * 4 + 255) // 256 * 256
         assert n == base + table, k
-    assert f(4, 512, 64, 16, 8, 128, 8) == 0
-    assert f(4, 512, 64, 16, 8, 128, 24) == 0
+    any8 = f(4, 512, 64, 16, 8, 128, 8)
+    assert 0 < any8 < base
+    assert f(4, 512, 64, 16, 8, 128, 24) == any8
+    assert f(4, 512, 64, 16, 8, 100, 16) > 0       # head dim 100: any-layout kernel
+    assert f(4, 512, 5000, 16, 8, 128, 8) == 0     # 5000 blocks per row: scalar kernel
 
 
 def _prefill(lib, **kw):
