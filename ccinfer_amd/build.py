@@ -42,7 +42,7 @@ SOURCES = [
     CSRC / "write_kv_cache.hip",
     CSRC / "decode_attn.hip",
     CSRC / "prefill_attn.hip",
-    CSRC / "generic_attn.hip",
+    CSRC / "layout.hip",
     CSRC / "qkv_prologue.hip",
     CSRC / "batch_meta.hip",
     CSRC / "kv_fp8.hip",

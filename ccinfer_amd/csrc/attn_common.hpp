@@ -22,21 +22,13 @@ constexpr int kWave = 64;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_inff();
 
-// Token-to-cache-row mapping of the reference (attn_common.cuh:7-27): returns the
-// element offset of (ctx_pos, kv_head) or -1 when the logical block is outside the
-// table row or the table entry is negative.
-__device__ __forceinline__ int64_t kv_row_offset(int ctx_pos, int kv_head, int head_dim,
-                                                 int num_kv_heads, int block_size,
-                                                 int max_blocks_per_req,
-                                                 const int32_t* __restrict__ req_blocks) {
-    const int lb = ctx_pos / block_size;
-    const int off = ctx_pos - lb * block_size;
-    if (lb < 0 || lb >= max_blocks_per_req) return -1;
-    const int pb = req_blocks[lb];
-    if (pb < 0) return -1;
-    const int64_t slot = static_cast<int64_t>(pb) * block_size + off;
-    return (slot * num_kv_heads + kv_head) * static_cast<int64_t>(head_dim);
-}
+// Token-to-cache-row mapping of the reference (attn_common.cuh:7-27): position p of a
+// request lives in slot table[p / block_size] * block_size + p % block_size, at element
+// (slot * num_kv_heads + kv_head) * head_dim; a negative table entry, or a block past the
+// table row, holds no position. Every kernel computes it inline in the form its staging
+// needs (a wave-uniform block base plus a per-lane row offset in the pipelined prefill,
+// a readlane of the split's block ids in decode, a per-lane block lookup in the
+// any-layout staging).
 
 // Round-to-nearest-even fp32 -> bf16 pair (gfx950 has a native packed convert).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {

@@ -169,22 +169,18 @@ int prefill_entry(const void* q, const void* k_cache, const void* v_cache,
                                           num_q_heads, num_kv_heads, head_dim,
                                           cache_block_size);
     if (!rt.fast || !caches_aligned(k_cache, v_cache)) {
-        // Other block sizes, head dims and cache alignments: the MFMA tile kernel with
-        // element-wise staging where its table row fits LDS, else the scalar kernel.
-        if (prefill_any_supported(num_q_heads, num_kv_heads, head_dim, max_blocks_per_req)) {
-            const size_t need_any = prefill_any_workspace_bytes(
-                batch_size, total_query_tokens, num_q_heads, num_kv_heads, head_dim);
-            if (workspace == nullptr || workspace_bytes < need_any)
-                return CCINFER_ERR_INVALID_ARGUMENT;
-            return map_hip_error(prefill_attention_any(
-                q, k_cache, v_cache, block_table, query_start_loc, context_lens, output,
-                batch_size, total_query_tokens, max_blocks_per_req, num_q_heads, num_kv_heads,
-                head_dim, cache_block_size, workspace, as_stream(stream)));
-        }
-        return map_hip_error(generic_prefill_attention(
-            q, k_cache, v_cache, block_table, query_start_loc, context_lens, output, batch_size,
-            total_query_tokens, max_blocks_per_req, num_q_heads, num_kv_heads, head_dim,
-            cache_block_size, as_stream(stream)));
+        // Other block sizes, head dims, cache alignments, and head dims above 128 past 4096
+        // table blocks: the MFMA tile kernel with element-wise staging.
+        if (!prefill_any_supported(num_q_heads, num_kv_heads, head_dim, max_blocks_per_req))
+            return CCINFER_ERR_INTERNAL;  // the shape check above admits no other shape
+        const size_t need_any = prefill_any_workspace_bytes(
+            batch_size, total_query_tokens, num_q_heads, num_kv_heads, head_dim);
+        if (workspace == nullptr || workspace_bytes < need_any)
+            return CCINFER_ERR_INVALID_ARGUMENT;
+        return map_hip_error(prefill_attention_any(
+            q, k_cache, v_cache, block_table, query_start_loc, context_lens, output,
+            batch_size, total_query_tokens, max_blocks_per_req, num_q_heads, num_kv_heads,
+            head_dim, cache_block_size, workspace, as_stream(stream)));
     }
     const bool staged = !(aligned16(q) && aligned16(output));
     if (workspace == nullptr || workspace_bytes < rt.need(staged))

@@ -184,8 +184,7 @@ hipError_t qkv_prologue(const void* qkv, const void* q_norm_w, const void* k_nor
                         hipStream_t stream);
 
 // ---- any-layout prefill on the MFMA tile kernel: head dims <= 256, any block size, any
-// 2-byte alignment; single-token requests run as one-row tiles; table rows of at most 4096
-// blocks ----
+// 2-byte alignment, any table length; single-token requests run as one-row tiles ----
 bool prefill_any_supported(int num_q_heads, int num_kv_heads, int head_dim,
                            int max_blocks_per_req);
 size_t prefill_any_workspace_bytes(int batch_size, int total_query_tokens, int num_q_heads,
@@ -196,15 +195,6 @@ hipError_t prefill_attention_any(const void* q, const void* k_cache, const void*
                                  int total_query_tokens, int max_blocks_per_req, int num_q_heads,
                                  int num_kv_heads, int head_dim, int block_size,
                                  void* workspace, hipStream_t stream);
-
-// ---- generic prefill (any head_dim / GQA ratio / block size / alignment) ----
-hipError_t generic_prefill_attention(const void* q, const void* k_cache, const void* v_cache,
-                                     const int32_t* block_table,
-                                     const int32_t* query_start_loc,
-                                     const int32_t* context_lens, void* output, int batch_size,
-                                     int total_query_tokens, int max_blocks_per_req,
-                                     int num_q_heads, int num_kv_heads, int head_dim,
-                                     int block_size, hipStream_t stream);
 
 // Workspace bytes of a bf16 / fp8 decode call of this shape on the MFMA kernels; `staged`
 // adds the q and output row copies a call with 2-byte-aligned q / output uses (defined with

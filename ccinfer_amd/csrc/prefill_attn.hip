@@ -525,17 +525,21 @@ __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
     // the host routes tables longer than kMaxTableLds to the generic kernel.
     const int nblk_vis = (kv_end + block_size - 1) / block_size;
     const int nblk = min(nblk_vis, mbpr);
+    // kAny with more visible blocks than the LDS table holds: the staging reads the ids
+    // from the table row in global memory instead (cached; one read per staged chunk).
+    const bool bt_global = kAny && nblk > kMaxTableLds;
     for (int lb = threadIdx.x; lb < nblk; lb += kThreads) {
         const int pb = req_blocks[lb];
-        lds_bt[lb] = pb;
+        if (!bt_global) lds_bt[lb] = pb;
         if (pb < 0) s_holes = 1;
     }
     __syncthreads();
     const bool holes = s_holes != 0 || nblk_vis > mbpr;
+    [[maybe_unused]] const int32_t* stage_bt = bt_global ? req_blocks : lds_bt;
 
     if constexpr (kAny) {
         AnyStage<D> r0;
-        stage_any_load<D>(r0, lds_valid0, k_cache, v_cache, lds_bt, 0, ctx, nblk, kvh, hkv, dr,
+        stage_any_load<D>(r0, lds_valid0, k_cache, v_cache, stage_bt, 0, ctx, nblk, kvh, hkv, dr,
                           block_size, any_vec);
         stage_any_write<D>(r0, lds_k0, lds_v0);
     } else {
@@ -656,7 +660,7 @@ __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
         [[maybe_unused]] AnyStage<D> rn;
         if (more) {
             if constexpr (kAny)
-                stage_any_load<D>(rn, nvalid, k_cache, v_cache, lds_bt, (t + 1) * kKeysPerTile,
+                stage_any_load<D>(rn, nvalid, k_cache, v_cache, stage_bt, (t + 1) * kKeysPerTile,
                                   ctx, nblk, kvh, hkv, dr, block_size, any_vec);
             else
                 stage_issue<D, kPad>(nk, nv, nvalid, k_cache, v_cache, zero_row, lds_bt,
@@ -1743,8 +1747,9 @@ AnyLayout any_layout(int batch_size, int total_query_tokens, int num_q_heads, in
 
 bool prefill_any_supported(int num_q_heads, int num_kv_heads, int head_dim,
                            int max_blocks_per_req) {
+    (void)max_blocks_per_req;  // longer table rows are read from global memory
     return num_kv_heads > 0 && num_q_heads % num_kv_heads == 0 && head_dim > 0 &&
-           head_dim <= 256 && max_blocks_per_req <= kMaxTableLds;
+           head_dim <= 256;
 }
 
 size_t prefill_any_workspace_bytes(int batch_size, int total_query_tokens, int num_q_heads,

@@ -247,10 +247,9 @@ size_t ccinfer_prefill_workspace_size(int batch_size, int total_query_tokens,
  * query group size and head dims that are multiples of 8 up to 128 (at any size; those
  * below 64 / 128 run padded with zeros) or multiples of 16 up to 256 (up to 4096 blocks per
  * table row, counted in 16-token blocks), with cache blocks of any multiple of 16 tokens
- * (read through a 16-token table the call builds in the workspace). Other block sizes and
- * head dims up to 256 run an MFMA tile kernel that stages rows element-wise (tables of up
- * to 4096 blocks per row; beyond that a scalar kernel). A mixed batch's decode items run
- * on `stream` ahead of the prompt tiles. */
+ * (read through a 16-token table the call builds in the workspace). Other block sizes,
+ * head dims up to 256 and table lengths run an MFMA tile kernel that stages rows
+ * element-wise. A mixed batch's decode items run on `stream` ahead of the prompt tiles. */
 int ccinfer_prefill_attention(const void* q, const void* k_cache, const void* v_cache,
                               const int32_t* block_table, const int32_t* query_start_loc,
                               const int32_t* context_lens, void* output, int batch_size,

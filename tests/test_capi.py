@@ -129,8 +129,8 @@ def test_decode_workspace_size(lib):
 def test_prefill_workspace_size_for_other_block_sizes(lib):
     """Blocks of 16·k tokens run the MFMA prefill through a 16-token table built in the
     workspace: the size is that of the 16-token shape plus the table. Other block sizes run
-    the any-layout tile kernel: the planner's tile list only, the same for every block size;
-    past 4096 table blocks, the scalar kernel (no workspace)."""
+    the any-layout tile kernel: the planner's tile list only, the same for every block size
+    and table length."""
     f = lib.ccinfer_prefill_workspace_size
     base = f(4, 512, 64, 16, 8, 128, 16)
     assert base > 0
@@ -142,7 +142,7 @@ def test_prefill_workspace_size_for_other_block_sizes(lib):
     assert 0 < any8 < base
     assert f(4, 512, 64, 16, 8, 128, 24) == any8
     assert f(4, 512, 64, 16, 8, 100, 16) > 0       # head dim 100: any-layout kernel
-    assert f(4, 512, 5000, 16, 8, 128, 8) == 0     # 5000 blocks per row: scalar kernel
+    assert f(4, 512, 5000, 16, 8, 128, 8) == any8  # any table length
 
 
 def _prefill(lib, **kw):
@@ -191,7 +191,9 @@ def test_alignment_limits_and_overlap_validation(lib):
     assert p8(*a) == UNSUPPORTED
     assert lib.ccinfer_prefill_workspace_size(6000, 6000, 8, 16, 8, 128, 16) > 0
     assert lib.ccinfer_prefill_workspace_size(2, 64, 8192, 16, 8, 128, 16) > 0
-    assert lib.ccinfer_prefill_workspace_size(2, 64, 8192, 16, 8, 256, 16) == 0  # generic
+    # head dim 256 past 4096 table blocks: the any-layout tile kernel (ids read from the
+    # table row in global memory)
+    assert lib.ccinfer_prefill_workspace_size(2, 64, 8192, 16, 8, 256, 16) > 0
     ov = lib.ccinfer_prefill_attention_overlap
     base = [FAKE] * 7 + [2, 64, 8, 16, 8, 128, 16, FAKE, 1 << 30, None]
     assert ov(*base, FAKE, None, FAKE) == INVALID
