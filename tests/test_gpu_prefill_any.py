@@ -117,3 +117,31 @@ def test_any_layout_workspace_size(gpu):
     assert lib.ccinfer_prefill_attention(*args, n - 1, s) == 6
     assert lib.ccinfer_prefill_attention(*args, n, s) == 0
     torch.cuda.synchronize()
+
+
+def test_any_layout_under_graph_capture(gpu):
+    """The any-layout route (planner + tile kernel, no host work between them) captures into
+    a HIP graph; every replay, with eager work and synchronisations between, equals the
+    eager call."""
+    say("any-layout prefill captured in a graph")
+    q, k, v, bt, qsl, ctx = _case(gpu, 9, 8, 16, 8, 128, [200, 1, 5, 1, 64, 1, 33, 7],
+                                  [0, 700, 0, 30, 100, 1500, 64, 3])
+    m = [torch.from_numpy(a).to(gpu) for a in (bt, qsl, ctx)]
+    eager = prefill_attention(q, k, v, *m, output=torch.full_like(q, 3.0),
+                              cache_block_size=8).clone()
+    from ccinfer_amd import prefill_workspace_size
+    n = prefill_workspace_size(len(ctx), q.shape[0], bt.shape[1], 16, 8, 128, 8)
+    ws = torch.zeros(max(1, n), dtype=torch.uint8, device=gpu)
+    out = torch.full_like(q, 3.0)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        prefill_attention(q, k, v, *m, output=out, cache_block_size=8, workspace=ws)
+    for _ in range(3):
+        out.fill_(3.0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
