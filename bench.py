@@ -706,7 +706,7 @@ def sweep(kind: str) -> None:
 
 
 def sweep_generic() -> None:
-    """The generic kernels' cost against the MFMA paths at the configs' shapes: views that are
+    """The cost of layouts beyond the native kernels at the configs' shapes: views that are
     only 2-byte aligned (q / output offset by one element) and cache blocks other than 16."""
     dev = torch.device("cuda:0")
     stream = torch.cuda.Stream()

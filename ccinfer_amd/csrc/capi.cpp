@@ -56,9 +56,9 @@ bool fits_int(int64_t v) { return v >= 0 && v <= INT_MAX; }
 
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
-// The MFMA paths move q, output and cache rows in 16-byte pieces; the reference launchers
-// take any bf16 (2-byte aligned) view, so bf16 calls with a less aligned pointer run the
-// generic kernels, and fp8 calls (MFMA only) are rejected.
+// The native MFMA paths move q, output and cache rows in 16-byte pieces; the reference
+// launchers take any bf16 (2-byte aligned) view, so bf16 calls with a less aligned pointer
+// take the routes below, and fp8 calls are rejected.
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 bool fast_aligned(const void* q, const void* k_cache, const void* v_cache, const void* output) {
@@ -69,9 +69,9 @@ bool fast_aligned(const void* q, const void* k_cache, const void* v_cache, const
 // aligned still runs the MFMA kernels: q (and, for prefill, the output rows the call may
 // leave untouched) are copied into 16-byte-aligned workspace regions, the kernels run on
 // those, and the output rows are copied back -- two or three passes over rows that are
-// small next to the cache reads. Only caches that are not 16-byte aligned take the generic
-// kernels. The workspace size queries include these regions; a call checks only the bytes
-// it uses.
+// small next to the cache reads. Caches that are not 16-byte aligned run decode with 2-byte
+// piece loads and prefill on the any-layout tile kernel. The workspace size queries
+// include these regions; a call checks only the bytes it uses.
 constexpr size_t kWsAlign = 256;
 
 size_t ws_align(size_t v) { return (v + kWsAlign - 1) / kWsAlign * kWsAlign; }

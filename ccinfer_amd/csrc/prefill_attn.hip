@@ -522,7 +522,7 @@ __global__ __launch_bounds__(kThreads) void prefill_tile_kernel(
     if (threadIdx.x == 0) s_holes = 0;
     __syncthreads();
     // Positions past the table row are invalid, so only min(visible, mbpr) entries matter;
-    // the host routes tables longer than kMaxTableLds to the generic kernel.
+    // the host sends the native tile kernel table rows of at most kMaxTableLds blocks.
     const int nblk_vis = (kv_end + block_size - 1) / block_size;
     const int nblk = min(nblk_vis, mbpr);
     // kAny with more visible blocks than the LDS table holds: the staging reads the ids

@@ -115,7 +115,7 @@ int ccinfer_build_batch_metadata(const int32_t* item_kv_written, const int32_t* 
                                  void* stream);
 
 /* Workspace bytes ccinfer_decode_attention (and ccinfer_decode_attention_fp8) needs for this
- * batch shape; 0 for shapes on the generic kernels. The figure includes two copies of the
+ * batch shape; 0 for invalid shapes. The figure includes two copies of the
  * q rows, which only a call with a 2-byte-aligned q or output uses; an aligned call accepts
  * a workspace that much smaller. */
 size_t ccinfer_decode_workspace_size(int batch_size, int max_blocks_per_req, int num_q_heads,
@@ -231,7 +231,7 @@ int ccinfer_decode_attention_fp8(const void* q, const void* k_cache, const void*
                                  void* stream);
 
 /* Workspace bytes ccinfer_prefill_attention (and the fp8 / overlap variants) needs for this
- * batch shape; 0 for shapes on the generic kernel. As for decode, it includes two copies of
+ * batch shape; 0 for invalid shapes. As for decode, it includes two copies of
  * the q rows used only by a call with a 2-byte-aligned q or output. */
 size_t ccinfer_prefill_workspace_size(int batch_size, int total_query_tokens,
                                       int max_blocks_per_req, int num_q_heads,

@@ -170,7 +170,7 @@ def test_prefill_validation(lib):
 
 def test_alignment_limits_and_overlap_validation(lib):
     """fp8 calls (MFMA path only) reject q / output / cache / scale pointers that are not
-    16-byte aligned; bf16 calls route them to the generic kernels (GPU tests). Large batches
+    16-byte aligned; bf16 calls take them on other routes (GPU tests). Large batches
     and long tables stay on the MFMA prefill (nonzero workspace); the fp8 prefill keeps its
     4096-block table limit; a side stream without its events is rejected."""
     UNSUPPORTED = 26

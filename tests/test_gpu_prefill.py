@@ -200,8 +200,9 @@ def test_rows_past_total_tokens_not_processed(gpu):
     assert_attn_close(got, want, "clipped")
 
 
-def test_generic_block_size(gpu):
-    """Non-16 cache blocks (accepted by the reference prefill launcher) on the generic path."""
+def test_block_size_8(gpu):
+    """Non-16 cache blocks (accepted by the reference prefill launcher) on the any-layout
+    tile kernel."""
     say("prefill block_size 8")
     rng = np.random.default_rng(3)
     hq, hkv, d, bs = 8, 4, 128, 8
@@ -288,7 +289,7 @@ def test_concurrent_mixed_prefills_on_two_streams(gpu):
 def test_two_byte_aligned_views(gpu, which):
     """A q or output view that is only 2-byte aligned runs the MFMA kernels on workspace
     copies of its rows (bit-equal to the aligned call); a cache that is only 2-byte aligned
-    runs the generic kernel."""
+    runs the any-layout tile kernel."""
     say(f"prefill with a 2-byte aligned {which}")
     w = W.prefill_prefix(device=gpu, seed=19, n_seqs=3, prefix=32, new=90, share_pairs=(),
                          hq=8, hkv=4, d=128)
