@@ -816,6 +816,28 @@ def sweep_generic() -> None:
     t = time_loop(pre_k, 5, 2, stream)[0] * 1e3
     print(f"| prefill configs[2], k / v caches 2-byte aligned (MFMA tile kernel, shifted "
           f"16-byte loads) | {base:.1f} | {t:.1f} | {t / base:.2f}x |", flush=True)
+    del kshift, vshift, w, ws
+    torch.cuda.empty_cache()
+
+    def pre_shape(d, prefix, new, n_seqs, hq=16, hkv=8, steps=5):
+        w2 = W.prefill_prefix(device=dev, n_seqs=n_seqs, prefix=prefix, new=new, hq=hq,
+                              hkv=hkv, d=d, share_pairs=())
+        ops = Ops(w2, dev, stream)
+        ms = time_loop(ops.prefill, steps, 2, stream)[0] * 1e3
+        del w2, ops
+        torch.cuda.empty_cache()
+        return ms
+    # a head dim that is not a multiple of 8 (element-wise staging) against the next one
+    # that is (padded native kernel)
+    a, b = pre_shape(96, 512, 1536, 8), pre_shape(100, 512, 1536, 8)
+    print(f"| prefill configs[2] shape, d=100 (MFMA tile kernel, shifted loads) vs "
+          f"d=96 | {a:.1f} | {b:.1f} | {b / a:.2f}x |", flush=True)
+    # head dim 256 past 4096 table blocks (ids read from global memory) against 4096 blocks
+    a = pre_shape(256, 65536 - 2048, 2048, 1, hq=8, hkv=4, steps=3)
+    b = pre_shape(256, 65536 + 2048, 2048, 1, hq=8, hkv=4, steps=3)
+    print(f"| prefill d=256, 1 x (63488 / 67584 cached + 2048 new): 4,096 blocks (native "
+          f"tile kernel) vs 4,352 (any-layout, table in global memory) | {a:.1f} | {b:.1f} | "
+          f"{b / a:.2f}x |", flush=True)
 
 
 def main():

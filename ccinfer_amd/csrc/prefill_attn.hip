@@ -297,9 +297,10 @@ __device__ __forceinline__ void stage_issue(__bf16* lk, __bf16* lv, uint8_t* lva
 // head dim dr <= D): the same tile layout as stage_issue, built in two steps so the loads'
 // latency overlaps the attention of the current tile -- stage_any_load reads each lane's
 // 16-byte chunk element by element (elements past dr, rows past the context or in
-// unmapped blocks read as zeros; 16-byte loads when `vec`: rows 16-byte aligned; two
-// shifted 16-byte loads when only the alignment is off) and records the rows' validity;
-// stage_any_write stores the chunks into the tile.
+// unmapped blocks read as zeros; one 16-byte load when `vec`: rows 16-byte aligned; two
+// shifted 16-byte loads for other chunks that lie wholly inside their row; 2-byte elements
+// for a row's last, partial chunk) and records the rows' validity; stage_any_write stores
+// the chunks into the tile.
 template <int D>
 struct AnyStage {
     u32x4 k[PrefillShape<D>::kLoadsPerThread];
@@ -312,7 +313,6 @@ __device__ __forceinline__ void stage_any_load(AnyStage<D>& r, uint8_t* lvalid,
                                                const int32_t* lbt, int key_base, int ctx,
                                                int nblk, int kv_head, int hkv, int dr, int bs,
                                                bool vec) {
-    const bool shifted = !vec && dr % 8 == 0;
     constexpr int CPR = PrefillShape<D>::kCPR;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -330,19 +330,18 @@ __device__ __forceinline__ void stage_any_load(AnyStage<D>& r, uint8_t* lvalid,
         const uint16_t* ks = reinterpret_cast<const uint16_t*>(k_cache) + base;
         const uint16_t* vs = reinterpret_cast<const uint16_t*>(v_cache) + base;
         u32x4 kw{0u, 0u, 0u, 0u}, vw{0u, 0u, 0u, 0u};
-        if (vec || shifted) {
-            // rows of a multiple of 8 elements: a chunk lies wholly inside its row; one
-            // 16-byte load when the rows are 16-byte aligned, else two shifted (load_shifted)
+        if (vec) {
+            // 16-byte aligned rows of a multiple of 8 elements: one load per chunk
             if (pb >= 0 && lchunk * 8 < dr) {
-                if (vec) {
-                    kw = *reinterpret_cast<const u32x4*>(ks + lchunk * 8);
-                    vw = *reinterpret_cast<const u32x4*>(vs + lchunk * 8);
-                } else {
-                    kw = load_shifted<4, u32x4>(ks + lchunk * 8);
-                    vw = load_shifted<4, u32x4>(vs + lchunk * 8);
-                }
+                kw = *reinterpret_cast<const u32x4*>(ks + lchunk * 8);
+                vw = *reinterpret_cast<const u32x4*>(vs + lchunk * 8);
             }
+        } else if (pb >= 0 && lchunk * 8 + 8 <= dr) {
+            // a chunk wholly inside its row: two aligned loads shifted into place
+            kw = load_shifted<4, u32x4>(ks + lchunk * 8);
+            vw = load_shifted<4, u32x4>(vs + lchunk * 8);
         } else if (pb >= 0) {
+            // the row's last, partial chunk: element by element
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const int e = lchunk * 8 + i;
