@@ -714,9 +714,9 @@ def sweep_generic() -> None:
     print("| case | aligned call (us) | this call (us) | ratio |")
     print("|---|---|---|---|")
 
-    def misaligned(t):
+    def misaligned(t, elems=1):
         buf = torch.empty(t.numel() + 8, dtype=t.dtype, device=t.device)
-        v = buf[1:1 + t.numel()].view(t.shape)
+        v = buf[elems:elems + t.numel()].view(t.shape)
         v.copy_(t)
         return v
 
@@ -765,6 +765,10 @@ def sweep_generic() -> None:
         assert rc == 0, rc
     t = time_loop(dec_k, 20, 3, stream)[0] * 1e3
     print(f"| decode configs[1], k_cache 2-byte aligned (MFMA, 2-byte pieces) | {base:.1f} | "
+          f"{t:.1f} | {t / base:.2f}x |", flush=True)
+    kshift = misaligned(w.k_cache, 2)
+    t = time_loop(dec_k, 20, 3, stream)[0] * 1e3
+    print(f"| decode configs[1], k_cache 4-byte aligned (MFMA, 4-byte pieces) | {base:.1f} | "
           f"{t:.1f} | {t / base:.2f}x |", flush=True)
     del kshift
     del w, ws

@@ -543,18 +543,26 @@ __device__ __forceinline__ T kv_load(const T* p) {
         return __builtin_nontemporal_load(p);
 }
 
-// kU: the cache rows are only 2-byte aligned (a cache pointer offset by an odd number of
-// elements; the reference kernels read bf16 scalars, so they accept one). Each piece is
-// then assembled from 2-byte loads -- neighbouring lanes read neighbouring elements, so a
-// wavefront still touches whole lines -- and the rest of the kernel is unchanged. (Two
+// kU: the alignment of cache rows that are not 16-byte aligned (a cache pointer offset by a
+// number of elements that is not a multiple of 8; the reference kernels read bf16 scalars,
+// so they accept one): 4 or 2 bytes, 0 for aligned rows. Each piece is then assembled from
+// 4-byte or 2-byte loads -- neighbouring lanes read neighbouring elements, so a wavefront
+// still touches whole lines -- and the rest of the kernel is unchanged. (The choice is per
+// kernel: a branch per piece keeps both paths' registers live.) (Two
 // aligned 16-byte loads shifted into place, as the prefill staging does, hold twice the
 // registers per piece in flight: 48-1198 spilled VGPRs here, 7.6x instead of 1.7x.)
-template <bool kTL, bool kU, typename T>
+template <bool kTL, int kU, typename T>
 __device__ __forceinline__ T kv_piece(const __bf16* p) {
-    if constexpr (!kU) {
+    constexpr int kWords = sizeof(T) / 4;
+    if constexpr (kU == 0) {
         return kv_load<kTL>(reinterpret_cast<const T*>(p));
+    } else if constexpr (kU == 4) {
+        const uint32_t* e = reinterpret_cast<const uint32_t*>(p);
+        T w;
+#pragma unroll
+        for (int i = 0; i < kWords; ++i) w[i] = e[i];
+        return w;
     } else {
-        constexpr int kWords = sizeof(T) / 4;
         const uint16_t* e = reinterpret_cast<const uint16_t*>(p);
         T w;
 #pragma unroll
@@ -579,7 +587,7 @@ struct ChunkRegs {
 // 256 such loads read a valid piece of the row instead and are replaced by zeros: masking
 // measured 11-23 % slower at d=32, and spills 137 VGPRs at D = 256.
 template <int D, bool kPad = false, bool kTL = false, int KS = DecodeShape<D>::kSteps,
-          bool kU = false>
+          int kU = 0>
 __device__ __forceinline__ void load_chunk(ChunkRegs<D, KS>& c,
                                            const __bf16* __restrict__ k_cache,
                                            const __bf16* __restrict__ v_cache, int pb0, int pb1,
@@ -998,7 +1006,7 @@ __device__ __forceinline__ void load_split_inputs(const __bf16* __restrict__ q,
 // have the registers for at no head dim today: three padded chunks at head dim 80 / 192
 // spill 521 / 619 VGPRs).
 template <int D, bool F8, bool kPad = false, bool kTL = false,
-          int KS = DecodeShape<D>::kSteps, int NBUF = 2, bool kU = false>
+          int KS = DecodeShape<D>::kSteps, int NBUF = 2, int kU = 0>
 __device__ __forceinline__ void run_split(
     const std::conditional_t<F8, uint8_t, __bf16>* __restrict__ k_cache,
     const std::conditional_t<F8, uint8_t, __bf16>* __restrict__ v_cache,
@@ -1006,7 +1014,7 @@ __device__ __forceinline__ void run_split(
     const SplitInputs<D>& in, int hkv, int h, int begin, int end, float scale_log2, int lane,
     SoftmaxState<D>& st, int dr = D) {
     static_assert(NBUF == 2 || NBUF == 3, "two or three chunks in flight");
-    static_assert(!F8 || (KS == DecodeShape<D>::kSteps && NBUF == 2 && !kU),
+    static_assert(!F8 || (KS == DecodeShape<D>::kSteps && NBUF == 2 && kU == 0),
                   "fp8: the full chunk, 16-byte aligned");
     constexpr int NV = DecodeShape<D>::kNV;
     using Regs = std::conditional_t<F8, ChunkRegsF8<D>, ChunkRegs<D, KS>>;
@@ -1329,7 +1337,7 @@ __device__ __forceinline__ void shared_prefix_work(
 // kTL: the K/V loads stay in L2 (see kv_load).
 // kShared: workgroups from split_wgs on run shared_prefix_work (decode_attention_shared).
 template <int D, bool F8, bool kPad, bool kTL, bool kShared = false,
-          int KS = DecodeShape<D>::kSteps, int NBUF = 2, bool kU = false>
+          int KS = DecodeShape<D>::kSteps, int NBUF = 2, int kU = 0>
 __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     const __bf16* __restrict__ q, void* k_cache_v, void* v_cache_v,
     const float* __restrict__ k_scale,
@@ -1507,7 +1515,7 @@ struct GroupShape {
     static constexpr int kMaxG = 16;                 // LDS: kWaves * 16 * D floats = 64 KiB
 };
 
-template <int D, bool F8, bool kPad, bool kTL, bool kU = false>
+template <int D, bool F8, bool kPad, bool kTL, int kU = 0>
 __global__ __launch_bounds__(64 * GroupShape<D>::kWaves) void decode_group_kernel(
     const __bf16* __restrict__ q, void* k_cache_v, void* v_cache_v,
     const float* __restrict__ k_scale,
@@ -1710,7 +1718,7 @@ struct SharedParts {
     int nwg = 0;          // workgroups of the prefix work (a multiple of 8)
 };
 
-template <int D, bool F8, bool kPad, bool kU = false>
+template <int D, bool F8, bool kPad, int kU = 0>
 hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache,
                          const float* k_scale, const float* v_scale,
                          const int32_t* block_table, const int32_t* context_lens, void* output,
@@ -1724,7 +1732,7 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
     hkv *= rep;
     // Padded rows, virtual heads and 2-byte pieces read lines more than once: those loads
     // stay in L2.
-    const bool tl = kPad || rep > 1 || kU;
+    const bool tl = kPad || rep > 1 || kU != 0;
     if (plan.group) {
         const int64_t groups = static_cast<int64_t>(it.num_items) * hkv;
         auto go = [&](auto tl_tag) {
@@ -1769,9 +1777,9 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
         // 139.4 -> 137.6 us, d=96 154.8 -> 152.3, d=192 195.0 -> 175.8.
         constexpr int KSp = D == 128 ? 3 : D == 256 ? 6 : DecodeShape<D>::kSteps;
         auto kernel = decode_split_kernel<D, F8, kPad, kTLv, kShv>;
-        if constexpr (kU) {
+        if constexpr (kU != 0) {
             kernel = decode_split_kernel<D, F8, kPad, kTLv, kShv, DecodeShape<D>::kSteps, 2,
-                                         true>;
+                                         kU>;
         } else if constexpr (!F8 && kPad && !kShv && KSp < DecodeShape<D>::kSteps) {
             if (dr <= KSp * 32) kernel = decode_split_kernel<D, F8, kPad, kTLv, kShv, KSp, 2>;
         }
@@ -1784,7 +1792,7 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
             split_wgs);
     };
     if (shr) {
-        if constexpr (!F8 && !kU) {
+        if constexpr (!F8 && kU == 0) {
             if (tl)
                 go(std::true_type{}, std::true_type{});
             else if constexpr (!kPad)
@@ -1930,20 +1938,19 @@ hipError_t decode_attention(const void* q, const void* k_cache, const void* v_ca
                 items.max_slots};
     const int D = decode_mfma_dim(head_dim);
     const bool pad = D != head_dim;
-    // Caches whose rows are not 16-byte aligned run the kernels with 2-byte piece loads.
-    const bool unaligned =
-        ((reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) & 15u) != 0;
+    // Caches whose rows are not 16-byte aligned run the kernels with 4-byte or 2-byte piece
+    // loads.
+    const uintptr_t cache_bits =
+        reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache);
+    const int unaligned = (cache_bits & 15u) == 0 ? 0 : (cache_bits & 3u) == 0 ? 4 : 2;
+#define CCI_DECODE_U(DD, PP, UU)                                                              \
+    launch_decode<DD, false, PP, UU>(q, k_cache, v_cache, nullptr, nullptr, block_table,      \
+                                     context_lens, output, it, max_blocks_per_req,            \
+                                     num_q_heads, num_kv_heads, plan, workspace, stream,      \
+                                     head_dim)
 #define CCI_DECODE(DD, PP)                                                                   \
-    return unaligned                                                                          \
-               ? launch_decode<DD, false, PP, true>(q, k_cache, v_cache, nullptr, nullptr,    \
-                                                    block_table, context_lens, output, it,    \
-                                                    max_blocks_per_req, num_q_heads,          \
-                                                    num_kv_heads, plan, workspace, stream,    \
-                                                    head_dim)                                 \
-               : launch_decode<DD, false, PP>(q, k_cache, v_cache, nullptr, nullptr,          \
-                                              block_table, context_lens, output, it,          \
-                                              max_blocks_per_req, num_q_heads, num_kv_heads,  \
-                                              plan, workspace, stream, head_dim)
+    return unaligned == 0 ? CCI_DECODE_U(DD, PP, 0)                                           \
+                          : unaligned == 4 ? CCI_DECODE_U(DD, PP, 4) : CCI_DECODE_U(DD, PP, 2)
     switch (D) {
         case 64:
             if (pad) CCI_DECODE(64, true);
@@ -1958,6 +1965,7 @@ hipError_t decode_attention(const void* q, const void* k_cache, const void* v_ca
             return hipErrorInvalidValue;
     }
 #undef CCI_DECODE
+#undef CCI_DECODE_U
 }
 
 hipError_t decode_attention_fp8(const void* q, const void* k_cache, const void* v_cache,

@@ -33,8 +33,8 @@
  * q or output view is only 2-byte aligned copies q (and, for prefill, output) into the
  * workspace, runs the MFMA kernels there and copies the output rows back (same bits as an
  * aligned call). A k_cache or v_cache pointer that is not 16-byte aligned runs the decode
- * MFMA kernels with 2-byte loads (same bits, ~1.7x the time) and the any-layout prefill
- * tile kernel (~2.2x). The fp8 calls, which have the MFMA paths only, return
+ * MFMA kernels with 4-byte or 2-byte loads (same bits, ~1.1x / ~1.7x the time) and the
+ * any-layout prefill tile kernel (~2.2x). The fp8 calls, which have the MFMA paths only, return
  * CCINFER_ERR_INVALID_ARGUMENT for any such pointer (and for k_scale / v_scale not 16-byte
  * aligned).
  */

@@ -248,6 +248,8 @@ def test_two_byte_aligned_views(gpu, which):
     (2, 100, 3000, 16, 8, 256, 1),    # fixed split plan, head dim 256
     (300, 1, 400, 16, 8, 96, 5),      # indexed flat plan, padded head dim
     (40, 50, 900, 64, 2, 64, 7),      # 32 query heads per kv head (virtual heads)
+    (64, 128, 4096, 16, 8, 128, 2),   # 4-byte aligned: word loads
+    (1, 512, 512, 16, 8, 96, 6),      # 4-byte aligned, group plan, padded head dim
 ])
 def test_two_byte_aligned_caches_on_mfma_path(gpu, batch, ctx_lo, ctx_hi, hq, hkv, d, offset):
     """K and V caches offset by an odd number of elements (only 2-byte aligned): the MFMA
