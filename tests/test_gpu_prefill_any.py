@@ -145,3 +145,42 @@ def test_any_layout_under_graph_capture(gpu):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
+
+
+def test_any_layout_rows_past_total_tokens(gpu):
+    """total_query_tokens below query_start_loc[B]: rows past it are neither read nor
+    written (src/kernel/attention/prefill_attn.cu launches total_query_tokens rows)."""
+    say("any-layout prefill with total_query_tokens < query_start_loc[B]")
+    q, k, v, bt, qsl, ctx = _case(gpu, 11, 8, 16, 8, 100, [40, 1, 5, 1, 90, 1, 60, 30],
+                                  [10, 300, 0, 20, 50, 700, 0, 9])
+    total = int(qsl[5]) + 17                  # stops inside request 6
+    out = torch.full_like(q, 3.0)
+    got = prefill_attention(q[:total], k, v, torch.from_numpy(bt).to(gpu),
+                            torch.from_numpy(qsl).to(gpu), torch.from_numpy(ctx).to(gpu),
+                            output=out[:total], cache_block_size=8)
+    torch.cuda.synchronize()
+    want = oracle.prefill(u16(q[:total]), u16(k), u16(v), bt, qsl, ctx, block_size=8,
+                          out=np.full((total,) + tuple(q.shape[1:]), 3.0, np.float32))
+    assert_attn_close(f32(got), want, "clipped")
+    assert torch.all(out[total:] == 3.0)
+
+
+def test_any_layout_more_than_4096_requests(gpu):
+    """The planner's per-request arrays move to the workspace past 4096 requests; on this
+    route single-token requests are tiles too. Sampled rows against the oracle."""
+    say("any-layout prefill with 5000 requests (24-token blocks)")
+    rng = np.random.default_rng(13)
+    n = 5000
+    qlen = np.where(rng.random(n) < 0.4, 1, rng.integers(2, 6, n)).astype(np.int32)
+    prefix = rng.integers(0, 60, n).astype(np.int32)
+    q, k, v, bt, qsl, ctx = _case(gpu, 13, 24, 8, 4, 64, qlen, prefix)
+    got = f32(prefill_attention(q, k, v, torch.from_numpy(bt).to(gpu),
+                                torch.from_numpy(qsl).to(gpu), torch.from_numpy(ctx).to(gpu),
+                                output=torch.full_like(q, 3.0), cache_block_size=24))
+    torch.cuda.synchronize()
+    rows = np.concatenate([qsl[:-1][::97], qsl[1:][::89] - 1])
+    pairs = np.stack([rows, rows % 8], 1).astype(np.int32)
+    want = oracle.prefill(u16(q), u16(k), u16(v), bt, qsl, ctx, block_size=24, pairs=pairs,
+                          out=np.full(q.shape, 3.0, np.float32))
+    r, h = pairs[:, 0], pairs[:, 1]
+    assert_attn_close(got[r, h], want[r, h], "5000 requests")
