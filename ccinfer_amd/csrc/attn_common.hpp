@@ -13,10 +13,12 @@
 namespace ccinfer::hipk {
 
 using bf16x8 = __bf16 __attribute__((ext_vector_type(8)));
+using f32x2 = float __attribute__((ext_vector_type(2)));
 using f32x4 = float __attribute__((ext_vector_type(4)));
 using f32x16 = float __attribute__((ext_vector_type(16)));
 using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
 using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
+using u32x3 = uint32_t __attribute__((ext_vector_type(3)));
 
 constexpr int kWave = 64;
 constexpr float kLog2e = 1.4426950408889634f;

@@ -258,7 +258,7 @@ size_t decode_bytes_for(int batch_size, int max_blocks_per_req, int num_q_heads,
     size_t bytes = 0;
     for (const bool fp8 : {false, true}) {
         const DecodePlan plan =
-            plan_decode(batch_size, num_q_heads, num_kv_heads,
+            plan_decode(batch_size, num_q_heads, num_kv_heads, head_dim,
                         max_blocks_per_req * cache_block_size, true, fp8);
         bytes = std::max(bytes, decode_workspace_bytes(batch_size, num_q_heads, head_dim, plan));
     }
@@ -367,7 +367,7 @@ int decode_entry(const void* q, const void* k_cache, const void* v_cache,
     if (!decode_fast_supported(num_q_heads, num_kv_heads, head_dim, cache_block_size))
         return CCINFER_ERR_INTERNAL;
     const bool staged = !(aligned16(q) && aligned16(output));
-    const DecodePlan plan = plan_decode(batch_size, num_q_heads, num_kv_heads,
+    const DecodePlan plan = plan_decode(batch_size, num_q_heads, num_kv_heads, head_dim,
                                         max_blocks_per_req * cache_block_size, true);
     // the size the query returns without the row copies, which only a call with unaligned
     // q / output uses (it covers the fp8 entry's plan too)
@@ -519,7 +519,7 @@ int ccinfer_decode_attention_fp8(const void* q, const void* k_cache, const void*
     if (!fast_aligned(q, k_cache, v_cache, output) || !aligned16(k_scale) || !aligned16(v_scale))
         return CCINFER_ERR_INVALID_ARGUMENT;
     const DecodePlan plan =
-        plan_decode(batch_size, num_q_heads, num_kv_heads,
+        plan_decode(batch_size, num_q_heads, num_kv_heads, head_dim,
                     max_blocks_per_req * cache_block_size, true, true);
     const size_t need = ccinfer_decode_workspace_size(batch_size, max_blocks_per_req,
                                                       num_q_heads, num_kv_heads, head_dim,

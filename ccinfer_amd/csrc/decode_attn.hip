@@ -67,6 +67,14 @@ constexpr int64_t kEvenWaves = 1024;
 // conversion and MFMA work): configs[1]'s batch 61.2 -> 56.0 us against kEvenWaves, while
 // bf16 runs 96.3 us at kEvenWaves and 98.3 at twice that.
 constexpr int64_t kEvenWavesFp8 = 2048;
+// bf16 rows of up to 80 dims (160 bytes): the shorter chunks leave the one wavefront per SIMD
+// waiting on its chunk loop, and a second one helps. 64 x 4096 positions, 1024 -> 2048:
+// d=32 68.2 -> 58.0 us, d=80 137.3 -> 132.9 (16 x 4096: 37.1 -> 33.9), d=64 93.6 -> 92.4;
+// slower at d=96 (146.6 -> 147.5), 112, 120, 128 and 192.
+constexpr int kShortRowDims = 80;
+constexpr int64_t flat_waves(bool fp8, int head_dim) {
+    return fp8 || head_dim <= kShortRowDims ? kEvenWavesFp8 : kEvenWaves;
+}
 constexpr int kFlatMinItems = 4;
 // Flat launches of at least this many wavefronts (two rounds at the split kernel's two waves
 // per SIMD) snap their ranges to request boundaries (decode_flat_index_kernel).
@@ -553,7 +561,7 @@ __device__ __forceinline__ T kv_load(const T* p) {
 // registers per piece in flight: 48-1198 spilled VGPRs here, 7.6x instead of 1.7x.)
 template <bool kTL, int kU, typename T>
 __device__ __forceinline__ T kv_piece(const __bf16* p) {
-    constexpr int kWords = sizeof(T) / 4;
+    constexpr int kWords = std::is_same_v<T, u32x3> ? 3 : sizeof(T) / 4;
     if constexpr (kU == 0) {
         return kv_load<kTL>(reinterpret_cast<const T*>(p));
     } else if constexpr (kU == 4) {
@@ -629,6 +637,10 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<D, KS>& c,
             if (!kMasked || vok) w = kv_piece<kTL, kU, u32x4>(row);
 #pragma unroll
             for (int x = 0; x < 4; ++x) c.v[e][x] = vok ? w[x] : 0u;
+        } else if constexpr (NV == 6) {  // D = 96: a 12-byte piece per lane
+            const u32x3 w = kv_piece<kTL, kU, u32x3>(row);
+#pragma unroll
+            for (int x = 0; x < 3; ++x) c.v[e][x] = w[x];
         } else if constexpr (NV == 4) {
             u32x2 w = u32x2{0, 0};
             if (!kMasked || vok) w = kv_piece<kTL, kU, u32x2>(row);
@@ -829,22 +841,35 @@ __device__ __forceinline__ void consume_chunk(SoftmaxState<D>& st, ChunkRegsF8<D
 // Split weights are computed one split per lane and broadcast with readlane; every lane then
 // accumulates its D/64 dims over the splits, 8 splits' partial rows loaded before any is
 // used so a row costs a couple of memory latencies, not one per split.
+// The columns of a row the merges give lane `lane`: kPer consecutive ones, lanes past the
+// row (D = 96: lanes 48-63) re-reading its last column and storing nothing.
+template <int D>
+struct MergeCols {
+    static constexpr int kPer = (D + 63) / 64;
+    static __device__ __forceinline__ int col(int lane, int x) {
+        if constexpr (D % 64 == 0)
+            return lane * kPer + x;
+        else
+            return min(lane * kPer + x, D - 1);
+    }
+};
+
 template <int D>
 __device__ void merge_row(const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
                           int64_t base, int ns, float eps, __bf16* __restrict__ o, int lane,
                           int dr = D) {
-    constexpr int kPer = D / 64;
+    constexpr int kPer = MergeCols<D>::kPer;
     constexpr int kBatch = 8;
     // The first batch of partial rows is loaded together with the (m, l) pairs, before the
     // row max is known (two memory round trips per row instead of three).
     float v_first[kBatch][kPer];
     {
-        const float* po = ws_o + base * D + lane * kPer;
+        const float* po = ws_o + base * D;
 #pragma unroll
         for (int u = 0; u < kBatch; ++u) {
             const int t = min(u, ns - 1);
 #pragma unroll
-            for (int x = 0; x < kPer; ++x) v_first[u][x] = po[t * D + x];
+            for (int x = 0; x < kPer; ++x) v_first[u][x] = po[t * D + MergeCols<D>::col(lane, x)];
         }
     }
     float mmax = kNegInf;
@@ -864,7 +889,7 @@ __device__ void merge_row(const float* __restrict__ ws_o, const float* __restric
                 lsum += ws_ml[(base + s) * 2 + 1] * w;
             }
             const int nt = min(64, ns - sb);
-            const float* po = ws_o + (base + sb) * D + lane * kPer;
+            const float* po = ws_o + (base + sb) * D;
             for (int t0 = 0; t0 < nt; t0 += kBatch) {
                 float v[kBatch][kPer];
                 if (sb == 0 && t0 == 0) {
@@ -877,7 +902,8 @@ __device__ void merge_row(const float* __restrict__ ws_o, const float* __restric
                     for (int u = 0; u < kBatch; ++u) {
                         const int t = min(t0 + u, nt - 1);  // clamped: a repeat's weight is 0
 #pragma unroll
-                        for (int x = 0; x < kPer; ++x) v[u][x] = po[t * D + x];
+                        for (int x = 0; x < kPer; ++x)
+                            v[u][x] = po[t * D + MergeCols<D>::col(lane, x)];
                     }
                 }
 #pragma unroll
@@ -908,7 +934,7 @@ __device__ void merge_row_two(const float* __restrict__ ws_o, const float* __res
                               int64_t base, int ns, const float* __restrict__ sh_o,
                               const float* __restrict__ sh_ml, int64_t sbase, int sn,
                               float eps, __bf16* __restrict__ o, int lane, int dr) {
-    constexpr int kPer = D / 64;
+    constexpr int kPer = MergeCols<D>::kPer;
     constexpr int kBatch = 8;
     const int n = ns + sn;
     auto row = [&](int t) {
@@ -939,9 +965,9 @@ __device__ void merge_row_two(const float* __restrict__ ws_o, const float* __res
                 float v[kBatch][kPer];
 #pragma unroll
                 for (int u = 0; u < kBatch; ++u) {  // clamped: a repeat's weight is 0
-                    const float* po = row(tb + min(t0 + u, nt - 1)) + lane * kPer;
+                    const float* po = row(tb + min(t0 + u, nt - 1));
 #pragma unroll
-                    for (int x = 0; x < kPer; ++x) v[u][x] = po[x];
+                    for (int x = 0; x < kPer; ++x) v[u][x] = po[MergeCols<D>::col(lane, x)];
                 }
 #pragma unroll
                 for (int u = 0; u < kBatch; ++u) {
@@ -1336,9 +1362,10 @@ __device__ __forceinline__ void shared_prefix_work(
 // kPad: head_dim dr < D (see load_chunk); q and output rows hold dr elements.
 // kTL: the K/V loads stay in L2 (see kv_load).
 // kShared: workgroups from split_wgs on run shared_prefix_work (decode_attention_shared).
+// Wavefronts per SIMD: one at D = 256, three at D = 96 (168 VGPRs, no spills), else two.
 template <int D, bool F8, bool kPad, bool kTL, bool kShared = false,
           int KS = DecodeShape<D>::kSteps, int NBUF = 2, int kU = 0>
-__global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
+__global__ __launch_bounds__(256, D == 256 ? 1 : D == 96 ? 3 : 2) void decode_split_kernel(
     const __bf16* __restrict__ q, void* k_cache_v, void* v_cache_v,
     const float* __restrict__ k_scale,
     const float* __restrict__ v_scale, const int32_t* __restrict__ block_table,
@@ -1378,10 +1405,12 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
     const int G = hq / hkv;
 
     // One split (the item's s-th of ns, over positions [begin, end)). The lane index comes
-    // in as an argument: at the padded head dims up to 128 the flat plan passes it through
-    // an empty asm on every segment, so the compiler recomputes the lane-derived addressing
-    // per segment instead of holding it across the segment loop (70 spilled VGPRs without,
-    // 17 with, outside the chunk loop); elsewhere that recomputation measured slower.
+    // in as an argument: at head dim 96 and the padded head dims up to 128 the flat plan
+    // passes it through an empty asm on every segment, so the compiler recomputes the
+    // lane-derived addressing per segment instead of holding it across the segment loop
+    // (padded: 70 spilled VGPRs without, 17 with, outside the chunk loop; head dim 96 at
+    // three wavefronts per SIMD: 27 without, none with); elsewhere that recomputation
+    // measured slower.
     auto process = [&](int lane, int item, int s, int ns, int first_slot, int ctx, int begin,
                        int end) __attribute__((always_inline)) {
     const int j = lane & 15;
@@ -1455,6 +1484,11 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
                 f32x4{st.acc[0][r], st.acc[1][r], st.acc[2][r], st.acc[3][r]};
             *reinterpret_cast<f32x4*>(po + NV * (4 * g + r) + 4) =
                 f32x4{st.acc[4][r], st.acc[5][r], st.acc[6][r], st.acc[7][r]};
+        } else if constexpr (NV == 6) {
+#pragma unroll
+            for (int x = 0; x < 3; ++x)
+                *reinterpret_cast<f32x2*>(po + NV * (4 * g + r) + 2 * x) =
+                    f32x2{st.acc[2 * x][r], st.acc[2 * x + 1][r]};
         } else {
 #pragma unroll
             for (int n = 0; n < NV; ++n) po[NV * (4 * g + r) + n] = st.acc[n][r];
@@ -1485,7 +1519,7 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : 2) void decode_split_kernel(
         if (invalid_w) process(lane, rest, 0, 0, 0, -1, 0, 0);
         for (int k = 1; ok; ++k) {
             int lane_k = lane;
-            if constexpr (kPad && D == 128) asm volatile("" : "+v"(lane_k));
+            if constexpr ((kPad && D == 128) || D == 96) asm volatile("" : "+v"(lane_k));
             process(lane_k, fs.req, fs.split, fs.nsplit, fs.first_slot, fs.ctx, fs.begin,
                     fs.end);
             if (!fs.more) break;
@@ -1591,7 +1625,7 @@ __global__ __launch_bounds__(64 * GroupShape<D>::kWaves) void decode_group_kerne
         }
     }
     __syncthreads();
-    constexpr int kPer = D / 64;
+    constexpr int kPer = MergeCols<D>::kPer;
     for (int jj = wave; jj < G; jj += W) {
         float mmax = kNegInf;
 #pragma unroll
@@ -1607,15 +1641,14 @@ __global__ __launch_bounds__(64 * GroupShape<D>::kWaves) void decode_group_kerne
                 lsum += lds_l[w * kMaxG + jj] * wt;
 #pragma unroll
                 for (int x = 0; x < kPer; ++x)
-                    acc[x] += lds_o[(w * kMaxG + jj) * D + lane * kPer + x] * wt;
+                    acc[x] += lds_o[(w * kMaxG + jj) * D + MergeCols<D>::col(lane, x)] * wt;
             }
         }
         const float inv = lsum > 0.f ? 1.f / (lsum + items.eps) : 0.f;
         __bf16* o = out + (static_cast<int64_t>(qrow) * hq + h * G + jj) * ds;
 #pragma unroll
         for (int x = 0; x < kPer; ++x)
-            if (!kPad || lane * kPer + x < dr)
-                o[lane * kPer + x] = static_cast<__bf16>(acc[x] * inv);
+            if (lane * kPer + x < dr) o[lane * kPer + x] = static_cast<__bf16>(acc[x] * inv);
     }
 }
 
@@ -1706,7 +1739,7 @@ int decode_head_rep(int G) {
 // SIMD its registers allow (about 156 / 217 / 430 VGPRs at head dims 64 / 128 / 256).
 template <int D>
 constexpr int resident_waves() {
-    return 1024 * (D <= 64 ? 3 : D <= 128 ? 2 : 1);
+    return 1024 * (D <= 64 || D == 96 ? 3 : D <= 128 ? 2 : 1);
 }
 
 // The shared-prefix partials the merge adds to the rows of decode_attention_shared.
@@ -1730,9 +1763,10 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
     // rep query heads each; virtual head v reads cache head v / rep.
     const int rep = decode_head_rep(hq / hkv);
     hkv *= rep;
-    // Padded rows, virtual heads and 2-byte pieces read lines more than once: those loads
-    // stay in L2.
-    const bool tl = kPad || rep > 1 || kU != 0;
+    // Padded rows, virtual heads, 2-byte pieces and rows that are not whole 128-byte lines
+    // (head dim 96: neighbouring kv heads' rows share lines) read lines more than once:
+    // those loads stay in L2.
+    const bool tl = kPad || rep > 1 || kU != 0 || D % 64 != 0;
     if (plan.group) {
         const int64_t groups = static_cast<int64_t>(it.num_items) * hkv;
         auto go = [&](auto tl_tag) {
@@ -1744,7 +1778,7 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
         };
         if (kPad || tl)
             go(std::true_type{});
-        else if constexpr (!kPad)
+        else if constexpr (!kPad && D % 64 == 0)
             go(std::false_type{});
         return hipGetLastError();
     }
@@ -1795,12 +1829,12 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
         if constexpr (!F8 && kU == 0) {
             if (tl)
                 go(std::true_type{}, std::true_type{});
-            else if constexpr (!kPad)
+            else if constexpr (!kPad && D % 64 == 0)
                 go(std::false_type{}, std::true_type{});
         }
     } else if (tl) {
         go(std::true_type{}, std::false_type{});
-    } else if constexpr (!kPad) {
+    } else if constexpr (!kPad && D % 64 == 0) {
         go(std::false_type{}, std::false_type{});
     }
     hipError_t err = hipGetLastError();
@@ -1817,8 +1851,8 @@ hipError_t launch_decode(const void* q, const void* k_cache, const void* v_cache
 
 }  // namespace
 
-DecodePlan plan_decode(int num_items, int num_q_heads, int num_kv_heads, int max_ctx,
-                       bool allow_flat, bool fp8, bool allow_group) {
+DecodePlan plan_decode(int num_items, int num_q_heads, int num_kv_heads, int head_dim,
+                       int max_ctx, bool allow_flat, bool fp8, bool allow_group) {
     // Query groups above one MFMA N-tile run as several virtual kv heads (launch_decode).
     num_kv_heads *= decode_head_rep(num_q_heads / num_kv_heads);
     DecodePlan p;
@@ -1838,7 +1872,7 @@ DecodePlan plan_decode(int num_items, int num_q_heads, int num_kv_heads, int max
         // One workgroup per CU, and at least one range per request and kv head (many short
         // rows would otherwise crowd several segments into each range).
         p.wave_target = static_cast<int>(std::max<int64_t>(
-            std::max<int64_t>(1, (fp8 ? kEvenWavesFp8 : kEvenWaves) / num_kv_heads),
+            std::max<int64_t>(1, flat_waves(fp8, head_dim) / num_kv_heads),
             num_items));
         p.flat_snap = static_cast<int64_t>(p.wave_target) * num_kv_heads >= kSnapWaves;
         p.flat_index = num_items > kFlatMaxItems || p.flat_snap;
@@ -1883,8 +1917,16 @@ int decode_mfma_dim(int head_dim) {
     return head_dim <= 256 && head_dim % 16 == 0 ? 256 : 0;
 }
 
-DecodePlan plan_decode_items(int num_items, int num_q_heads, int num_kv_heads, int max_ctx,
-                             bool fp8) {
+// The decode kernels' head dim: the MFMA size above, except head dim 96, which has a tile
+// of its own (3 K steps, 6 V dims per lane): in the 128 tile a quarter of every V load's
+// lanes sit idle and the same registers hold 12 KB of K/V per chunk instead of 16, and the
+// loads in flight are what bounds this kernel.
+int decode_tile_dim(int head_dim) {
+    return head_dim == 96 ? 96 : decode_mfma_dim(head_dim);
+}
+
+DecodePlan plan_decode_items(int num_items, int num_q_heads, int num_kv_heads, int head_dim,
+                             int max_ctx, bool fp8) {
     // The decode items of a prefill batch: their count is known on the device only, and is
     // often zero (a pure prompt batch). One launch of one workgroup per possible (item,
     // kv_head) costs far less than the split plan's two launches, each of which dispatches a
@@ -1897,15 +1939,15 @@ DecodePlan plan_decode_items(int num_items, int num_q_heads, int num_kv_heads, i
         p.group = true;
         return p;
     }
-    return plan_decode(num_items, num_q_heads, num_kv_heads, max_ctx, true, fp8);
+    return plan_decode(num_items, num_q_heads, num_kv_heads, head_dim, max_ctx, true, fp8);
 }
 
 size_t decode_workspace_bytes(int num_items, int num_q_heads, int head_dim,
                               const DecodePlan& plan) {
     if (plan.group || (!plan.flat && plan.splits <= 1)) return 0;
-    // partial O (rows of the MFMA head dim) + (m, l) per partial row, then the merge
+    // partial O (rows of the kernels' head dim) + (m, l) per partial row, then the merge
     // descriptors
-    const int d = decode_mfma_dim(head_dim);
+    const int d = decode_tile_dim(head_dim);
     const size_t rows = partial_rows(num_items, num_q_heads, plan);
     if (plan.flat_index)
         return index_offset(rows, d, num_items, num_q_heads) +
@@ -1936,7 +1978,7 @@ hipError_t decode_attention(const void* q, const void* k_cache, const void* v_ca
                 items.denom_eps, items.zero_invalid ? 1 : 0,
                 static_cast<const __bf16*>(items.new_k), static_cast<const __bf16*>(items.new_v),
                 items.max_slots};
-    const int D = decode_mfma_dim(head_dim);
+    const int D = decode_tile_dim(head_dim);
     const bool pad = D != head_dim;
     // Caches whose rows are not 16-byte aligned run the kernels with 4-byte or 2-byte piece
     // loads.
@@ -1955,6 +1997,8 @@ hipError_t decode_attention(const void* q, const void* k_cache, const void* v_ca
         case 64:
             if (pad) CCI_DECODE(64, true);
             CCI_DECODE(64, false);
+        case 96:
+            CCI_DECODE(96, false);
         case 128:
             if (pad) CCI_DECODE(128, true);
             CCI_DECODE(128, false);
@@ -2009,8 +2053,8 @@ SharedLayout shared_layout(int B, int mbpr, int hq, int hkv, int head_dim) {
     SharedLayout L{};
     // the suffixes: plain decode's split plan (never the group plan, whose rows do not go
     // through the merge), with the merge always on
-    L.plan = plan_decode(B, hq, hkv, mbpr * kBlock, true, false, false);
-    const int d = decode_mfma_dim(head_dim);
+    L.plan = plan_decode(B, hq, hkv, head_dim, mbpr * kBlock, true, false, false);
+    const int d = decode_tile_dim(head_dim);
     const size_t rows = partial_rows(B, hq, L.plan);
     L.regular = L.plan.flat_index ? index_offset(rows, d, B, hq) + index_bytes(B, L.plan.slots)
                                   : desc_offset(rows, d) +
@@ -2088,7 +2132,7 @@ hipError_t decode_attention_shared(const void* q, const void* k_cache, const voi
     const SharedLayout L = shared_layout(batch_size, max_blocks_per_req, num_q_heads,
                                          num_kv_heads, head_dim);
     char* ws = static_cast<char*>(workspace);
-    const int D = decode_mfma_dim(head_dim);
+    const int D = decode_tile_dim(head_dim);
     const bool pad = D != head_dim;
 #define CCI_SHARED(DD, PP)                                                                  \
     return launch_decode_shared<DD, PP>(q, k_cache, v_cache, block_table, context_lens,    \
@@ -2098,6 +2142,8 @@ hipError_t decode_attention_shared(const void* q, const void* k_cache, const voi
         case 64:
             if (pad) CCI_SHARED(64, true);
             CCI_SHARED(64, false);
+        case 96:
+            CCI_SHARED(96, false);
         case 128:
             if (pad) CCI_SHARED(128, true);
             CCI_SHARED(128, false);

@@ -39,12 +39,12 @@ constexpr int kFlatMaxItems = 256;
 
 // Returns the plan for a batch whose longest context is max_ctx tokens. allow_flat: the
 // flat mode may be used (it resolves items through DecodeItems like the kernel does).
-DecodePlan plan_decode(int num_items, int num_q_heads, int num_kv_heads, int max_ctx,
-                       bool allow_flat, bool fp8 = false, bool allow_group = true);
+DecodePlan plan_decode(int num_items, int num_q_heads, int num_kv_heads, int head_dim,
+                       int max_ctx, bool allow_flat, bool fp8 = false, bool allow_group = true);
 
 // The plan for the single-token items of a prefill batch (at most num_items of them).
-DecodePlan plan_decode_items(int num_items, int num_q_heads, int num_kv_heads, int max_ctx,
-                             bool fp8 = false);
+DecodePlan plan_decode_items(int num_items, int num_q_heads, int num_kv_heads, int head_dim,
+                             int max_ctx, bool fp8 = false);
 
 // Scratch bytes the split-KV decode needs for `num_items` query rows.
 size_t decode_workspace_bytes(int num_items, int num_q_heads, int head_dim,

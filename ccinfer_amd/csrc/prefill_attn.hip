@@ -1501,7 +1501,7 @@ PrefillLayout prefill_layout(int batch_size, int total_query_tokens, int max_blo
     const int D = decode_mfma_dim(head_dim);  // the kernels' (padded) head dim
     L.tile_tokens = tile_tokens_for(D, G);
     L.max_tiles = total_query_tokens / L.tile_tokens + batch_size;
-    L.plan = plan_decode_items(batch_size, num_q_heads, num_kv_heads,
+    L.plan = plan_decode_items(batch_size, num_q_heads, num_kv_heads, head_dim,
                                max_blocks_per_req * block_size, fp8);
     size_t off = 0;
     L.counts_off = off;

@@ -6,7 +6,8 @@ so the merge writes NaN); this replays its counting in numpy and checks that the
 always leaves room: the number of ranges and the number of partial slots (splits) stay within
 `slots`, for the even ranges, the snapped ranges and the whole-request layout.
 Constants restate decode_attn.hip: kChunk 32, kMaxSplitTokens 2048, kEvenWaves 1024 (2048
-for fp8), kFlatMinItems 4, kSnapWaves 4096."""
+for fp8 and for bf16 rows of up to 80 dims: the `fp8=True` cases), kFlatMinItems 4,
+kSnapWaves 4096."""
 import numpy as np
 import pytest
 

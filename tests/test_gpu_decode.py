@@ -122,7 +122,10 @@ def test_head_shapes(gpu, hq, hkv, d):
     (16, 8, 80, 2, 3000),     # fixed split plan + merge kernel
     (8, 2, 32, 3, 900),
     (8, 4, 192, 2, 2500),
-    (16, 8, 96, 40, 5000),    # balanced split plan + merge kernel
+    (16, 8, 96, 40, 5000),    # balanced split plan + merge kernel (head dim 96 tile)
+    (16, 8, 96, 1, 500),      # head dim 96 tile: group plan
+    (16, 8, 96, 2, 3000),     # head dim 96 tile: fixed split plan
+    (64, 4, 96, 3, 700),      # head dim 96 tile, G = 16
     (8, 8, 120, 12, 4000),
     (8, 4, 192, 24, 3000),
     (16, 4, 112, 64, 2000),
@@ -246,10 +249,11 @@ def test_two_byte_aligned_views(gpu, which):
     (64, 128, 4096, 16, 8, 128, 1),   # configs[1]: flat plan with merge
     (1, 512, 512, 16, 8, 128, 3),     # group plan
     (2, 100, 3000, 16, 8, 256, 1),    # fixed split plan, head dim 256
-    (300, 1, 400, 16, 8, 96, 5),      # indexed flat plan, padded head dim
+    (300, 1, 400, 16, 8, 96, 5),      # indexed flat plan, head dim 96 tile
+    (300, 1, 400, 16, 8, 80, 3),      # indexed flat plan, padded head dim
     (40, 50, 900, 64, 2, 64, 7),      # 32 query heads per kv head (virtual heads)
     (64, 128, 4096, 16, 8, 128, 2),   # 4-byte aligned: word loads
-    (1, 512, 512, 16, 8, 96, 6),      # 4-byte aligned, group plan, padded head dim
+    (1, 512, 512, 16, 8, 96, 6),      # 4-byte aligned, group plan, head dim 96 tile
 ])
 def test_two_byte_aligned_caches_on_mfma_path(gpu, batch, ctx_lo, ctx_hi, hq, hkv, d, offset):
     """K and V caches offset by an odd number of elements (only 2-byte aligned): the MFMA
@@ -282,7 +286,7 @@ def test_two_byte_aligned_caches_on_mfma_path(gpu, batch, ctx_lo, ctx_hi, hq, hk
 @pytest.mark.parametrize("batch,ctx_lo,ctx_hi,hq,hkv,d,offset", [
     (64, 128, 4096, 16, 8, 128, 1),   # configs[1]: split plan with merge
     (1, 512, 512, 16, 8, 128, 3),     # group plan (one launch)
-    (300, 1, 400, 16, 8, 96, 5),      # flat plan with index kernel, padded head dim
+    (300, 1, 400, 16, 8, 96, 5),      # flat plan with index kernel, head dim 96 tile
 ])
 def test_two_byte_aligned_q_and_output_on_mfma_path(gpu, batch, ctx_lo, ctx_hi, hq, hkv, d,
                                                     offset):

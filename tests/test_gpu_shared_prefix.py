@@ -38,7 +38,8 @@ def run(fn, w, dev):
     (37, 512, 1, 300, 5, 32, 8, 128),        # G = 4 (4 members per tile), 1-token suffixes
     (20, 1024, 40, 700, 2, 8, 8, 64),        # G = 1 (16 members per tile)
     (24, 768, 10, 200, 4, 64, 8, 128),       # G = 8 (2 members per tile)
-    (30, 256, 5, 90, 3, 16, 8, 96),          # padded head dim
+    (30, 256, 5, 90, 3, 16, 8, 96),          # head dim 96 tile
+    (30, 256, 5, 90, 3, 16, 8, 80),          # padded head dim
     (300, 512, 1, 400, 7, 16, 8, 128),       # past 256 requests: the indexed flat plan
     (3, 1024, 100, 300, 1, 16, 8, 128),      # 3 requests: the fixed split plan
 ])
