@@ -19,6 +19,9 @@ using f32x16 = float __attribute__((ext_vector_type(16)));
 using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
 using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
 using u32x3 = uint32_t __attribute__((ext_vector_type(3)));
+// A 12-byte piece at 4-byte alignment: loads through this type claim only that alignment,
+// so the compiler may not widen them to 16 bytes past the piece.
+typedef u32x3 u32x3_a4 __attribute__((aligned(4)));
 
 constexpr int kWave = 64;
 constexpr float kLog2e = 1.4426950408889634f;

@@ -562,7 +562,9 @@ __device__ __forceinline__ T kv_load(const T* p) {
 template <bool kTL, int kU, typename T>
 __device__ __forceinline__ T kv_piece(const __bf16* p) {
     constexpr int kWords = std::is_same_v<T, u32x3> ? 3 : sizeof(T) / 4;
-    if constexpr (kU == 0) {
+    if constexpr (kU == 0 && std::is_same_v<T, u32x3>) {
+        return kv_load<kTL>(reinterpret_cast<const u32x3_a4*>(p));
+    } else if constexpr (kU == 0) {
         return kv_load<kTL>(reinterpret_cast<const T*>(p));
     } else if constexpr (kU == 4) {
         const uint32_t* e = reinterpret_cast<const uint32_t*>(p);
