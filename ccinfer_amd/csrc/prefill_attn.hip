@@ -22,14 +22,18 @@
 //      and every O accumulator of a lane belongs to one query row (lane-local rescale).
 //      Tiles entirely above the causal diagonal are skipped; masking only runs on the
 //      diagonal / ragged tiles.
-//   3. single-token requests go through the split-KV decode kernel (decode_attn.hip) with
-//      prefill semantics (no 1e-6 in the denominator, bad rows left untouched); for batches
-//      of 32+ requests on the caller's side stream (when given) forked after the planner and
+//   3. single-token requests run with prefill semantics (no 1e-6 in the denominator, bad
+//      rows left untouched). Batches of at most 512 (request, virtual kv head) groups with
+//      table rows of at most 2048 positions run them in extra workgroups at the front of the
+//      tile launch (the decode kernels' group body, decode_core.hpp): no further launch.
+//      Others go through the split-KV decode kernels (decode_attn.hip): for batches of 32+
+//      requests on the caller's side stream (when given) forked after the planner and
 //      joined back at the end, so the memory-bound decode items run beside the MFMA-bound
 //      tiles.
 #include <type_traits>
 
 #include "attn_common.hpp"
+#include "decode_core.hpp"
 #include "kernels.hpp"
 
 namespace ccinfer::hipk {
@@ -775,7 +779,8 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
                          const int32_t* __restrict__ context_lens, __bf16* __restrict__ out,
                          const int32_t* __restrict__ counts, const TileEntry* __restrict__ tiles,
                          int total_tokens, int mbpr, int hq, int hkv, float scale_log2,
-                         int dr) {
+                         int dr, dcore::ItemArgs dec_items, int dec_wgs, int dec_hkv,
+                         int dec_rep) {
     static_assert(!(F8 && kPad), "fp8 runs the native head dims only");
     const int ds = kPad ? dr : D;  // row stride of q / cache / output (elements)
     using Sh = PipeShape<D>;
@@ -812,13 +817,35 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
     __shared__ int32_t lds_bt[F8 ? kMaxTableLds : 1];
     __shared__ int s_holes[kPipeWaves];
 
+    // The first dec_wgs workgroups run the batch's single-token requests instead: one per
+    // (request, virtual kv head), the decode kernels' group body with prefill semantics,
+    // its partial rows in the K/V buffers (two wavefronts' 16 x D floats per buffer).
+    if constexpr (!F8) {
+        if (static_cast<int>(blockIdx.x) < dec_wgs) {
+            static_assert(dcore::GroupShape<D>::kWaves == kPipeWaves &&
+                              kTileElems * 2 >= 2 * dcore::GroupShape<D>::kMaxG * D * 4,
+                          "the group body's partial rows fit two per K/V buffer");
+            auto part = [&](int w) {
+                __bf16* b = w < 2 ? lds_k0 : w < 4 ? lds_k1 : w < 6 ? lds_k2 : lds_v0;
+                return reinterpret_cast<float*>(b) + (w & 1) * dcore::GroupShape<D>::kMaxG * D;
+            };
+            float* lm = reinterpret_cast<float*>(lds_v1);
+            dcore::decode_group_body<D, false, kPad, true, 0>(
+                q, const_cast<void*>(k_cache_v), const_cast<void*>(v_cache_v), nullptr, nullptr,
+                block_table, context_lens, out, dec_items, mbpr, hq, dec_hkv, scale_log2, dr,
+                dec_rep, static_cast<int>(blockIdx.x), part, lm,
+                lm + kPipeWaves * dcore::GroupShape<D>::kMaxG);
+            return;
+        }
+    }
+    const int bid = static_cast<int>(blockIdx.x) - dec_wgs;
     const int G = hq / hkv;
     const int HPW = heads_per_wg(G);
     const int WPH = kPipeWaves / HPW;
     const int U = hkv * (G / HPW);
-    const int tile_idx = blockIdx.x / U;
+    const int tile_idx = bid / U;
     if (tile_idx >= counts[0]) return;
-    const int u = blockIdx.x % U;
+    const int u = bid % U;
     const int kvh = u / (G / HPW);
     const int hg = u % (G / HPW);
     const TileEntry te = tiles[tile_idx];
@@ -1529,22 +1556,35 @@ hipError_t launch_tiles(const void* q, const void* k_cache, const void* v_cache,
                         const int32_t* context_lens, void* output, int total_query_tokens,
                         int mbpr, int hq, int hkv, int block_size, const int32_t* counts,
                         const TileEntry* tiles, const void* zero_row, int max_tiles,
-                        hipStream_t stream, int dr) {
+                        hipStream_t stream, int dr, int batch_size, bool fused_dec) {
     const int G = hq / hkv;
     const int U = hkv * (G / heads_per_wg(G));
-    const int64_t grid = static_cast<int64_t>(max_tiles) * U;
     const float scale_log2 = kLog2e / sqrtf(static_cast<float>(dr));
     if constexpr (pipe_head_dim(D)) {
+        // fused_dec: the single-token requests run in the first workgroups of this launch,
+        // one per (request, virtual kv head), with prefill semantics (no 1e-6 in the
+        // denominator, malformed rows untouched).
+        const int rep = dcore::decode_head_rep(G);
+        dcore::ItemArgs it{};
+        int dec_wgs = 0;
+        if (fused_dec) {
+            it.num_items = batch_size;
+            it.qsl = qsl;
+            it.singles_total = total_query_tokens;
+            dec_wgs = batch_size * hkv * rep;
+        }
+        const int64_t grid = static_cast<int64_t>(max_tiles) * U + dec_wgs;
         prefill_pipe_kernel<D, F8, kPad>
             <<<static_cast<unsigned>(grid), PipeShape<D>::kThreads, 0, stream>>>(
             static_cast<const __bf16*>(q), k_cache, v_cache, k_scale, v_scale, block_table, qsl,
             context_lens,
             static_cast<__bf16*>(output), counts, tiles, total_query_tokens, mbpr, hq, hkv,
-            scale_log2, dr);
+            scale_log2, dr, it, dec_wgs, hkv * rep, rep);
         return hipGetLastError();
     } else if constexpr (F8) {
         return hipErrorInvalidValue;  // fp8 has the pipelined path only
     } else {
+        const int64_t grid = static_cast<int64_t>(max_tiles) * U;
         prefill_tile_kernel<D, kPad><<<static_cast<unsigned>(grid), kThreads, 0, stream>>>(
             static_cast<const __bf16*>(q), static_cast<const __bf16*>(k_cache),
             static_cast<const __bf16*>(v_cache), block_table, qsl, context_lens,
@@ -1591,6 +1631,17 @@ namespace {
 // where their near-empty launches take no CUs from the tiles (and, ahead of the tile
 // kernel rather than behind it, cost ~0.7 us less per step).
 constexpr int kOverlapMinRequests = 32;
+// The fused route's limits: at most this many (request, virtual kv head) workgroups ahead of
+// the tiles (each of a pure prompt batch's requests costs one that only reads its query
+// length), and table rows of at most this many positions (one workgroup streams a whole
+// row through one CU: ~34 us at 2048 positions, ~65 us at 4096). Measured on one box
+// against the decode launches (serial, split plan): configs[2] 149.1 -> 143.7 us, 16 x 512
+// prompts 45.5 -> 43.1, 64 x 128 prompts 61.4 -> 42.3; mixed batches of 128-1024 prompt
+// tokens with 4-60 single-token requests of 200-2000 positions 31.5 / 57.7 / 91.5 -> 27.5 /
+// 34.2 / 62.0 us. With rows of up to 4000 positions a batch of one 16-token prompt and 4
+// long single-token requests ran 35.6 -> 46.5 us, hence the 2048 bound.
+constexpr int64_t kFusedDecodeGroups = 512;
+constexpr int64_t kFusedDecodeMaxCtx = 2048;
 
 }  // namespace
 
@@ -1648,7 +1699,16 @@ hipError_t prefill_impl(const void* q, const void* k_cache, const void* v_cache,
                                     items, max_blocks_per_req, num_q_heads, num_kv_heads,
                                     head_dim, block_size, L.plan, ws + L.decode_ws_off, s);
     };
-    const bool fork = overlap != nullptr && overlap->side != nullptr &&
+    // Small batches whose table rows are short enough run their single-token requests
+    // inside the tile launch (fused_dec): no decode launches at all, which a pure prompt
+    // batch -- most prefill steps -- would otherwise pay for work known on the device only.
+    const int Dk = decode_mfma_dim(head_dim);
+    const int64_t dec_groups = static_cast<int64_t>(batch_size) * num_kv_heads *
+                               dcore::decode_head_rep(num_q_heads / num_kv_heads);
+    const bool fused_dec = !F8 && pipe_head_dim(Dk) && dec_groups <= kFusedDecodeGroups &&
+                           static_cast<int64_t>(max_blocks_per_req) * block_size <=
+                               kFusedDecodeMaxCtx;
+    const bool fork = !fused_dec && overlap != nullptr && overlap->side != nullptr &&
                       batch_size >= kOverlapMinRequests;
     // Once the side stream has waited on the fork event it is joined back on every path,
     // errors included (an unjoined fork would invalidate a capture of the caller's stream).
@@ -1664,7 +1724,7 @@ hipError_t prefill_impl(const void* q, const void* k_cache, const void* v_cache,
         if (err != hipSuccess) return err;
         err = launch_decode_items(overlap->side);
         if (err != hipSuccess) return join(err);
-    } else {
+    } else if (!fused_dec) {
         err = launch_decode_items(stream);
         if (err != hipSuccess) return err;
     }
@@ -1674,7 +1734,8 @@ hipError_t prefill_impl(const void* q, const void* k_cache, const void* v_cache,
     launch_tiles<DD, F8, PP>(q, k_cache, v_cache, k_scale, v_scale, block_table,             \
                              query_start_loc, context_lens, output, total_query_tokens,      \
                              max_blocks_per_req, num_q_heads, num_kv_heads, block_size,      \
-                             counts, tiles, zero_row, L.max_tiles, stream, head_dim)
+                             counts, tiles, zero_row, L.max_tiles, stream, head_dim,         \
+                             batch_size, fused_dec)
     if (F8 && pad) {
         err = hipErrorInvalidValue;  // fp8 runs the native head dims only
     } else {

@@ -435,17 +435,20 @@ def test_mixed_batch_with_600_decode_items(gpu):
     assert_attn_close(got[rows], ref, "600 decode items")
 
 
-@pytest.mark.parametrize("n_req", [40, 257])
-def test_mixed_batch_same_bits_serial_and_forked(gpu, n_req):
+@pytest.mark.parametrize("n_req,mbpr", [(40, 24), (40, 136), (257, 24)])
+def test_mixed_batch_same_bits_serial_and_forked(gpu, n_req, mbpr):
     """A mixed batch gives the same bits whether its decode items run after the tiles or,
     with a side stream (32+ requests), beside them: the planner lists the decode items in
     request order, so their split plan does not depend on timing. Every row must also
     match the oracle: ragged prompts, single-token items, empty and malformed (prefix < 0)
-    requests, a table hole. 257 requests take the decode plan's index kernel."""
+    requests, a table hole. 40 requests with 24-block rows run the decode items inside the
+    tile launch (with or without the side stream); with 136-block rows (past 2048
+    positions) they take the decode kernels; 257 requests take the decode plan's index
+    kernel."""
     from ccinfer_amd import SideStream
-    say(f"prefill mixed batch serial vs forked, {n_req} requests")
+    say(f"prefill mixed batch serial vs forked, {n_req} requests, {mbpr} blocks per row")
     rng = np.random.default_rng(900 + n_req)
-    hq, hkv, d, mbpr = 16, 8, 128, 24
+    hq, hkv, d = 16, 8, 128
     qlen = rng.choice([0, 1, 1, 2, 7, 33, 129], size=n_req).astype(np.int32)
     prefix = rng.integers(0, 200, n_req).astype(np.int32)
     ctx = np.minimum(qlen + prefix, mbpr * 16).astype(np.int32)
@@ -482,4 +485,48 @@ def test_mixed_batch_same_bits_serial_and_forked(gpu, n_req):
         print("bad rows", len(bad), "requests", np.unique(req))
     assert_attn_close(f32(outs[1]), want, f"forked {n_req}")
     assert_attn_close(f32(outs[0]), want, f"serial {n_req}")
+    assert torch.equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (32, 1, 80), (8, 8, 64), (64, 2, 128)])
+def test_single_token_requests_inside_the_tile_launch(gpu, hq, hkv, d):
+    """Batches of up to 256 (request, kv head) groups with table rows of up to 2048 positions
+    run their single-token requests as extra workgroups of the tile launch (no decode
+    launches). Every row against the oracle: single-token requests with 1..2048 positions,
+    prompts, empty and malformed (prefix < 0) requests, a table hole, rows past
+    total_query_tokens, virtual kv heads (G = 32) and padded head dims; the side stream
+    changes nothing."""
+    from ccinfer_amd import SideStream
+    say(f"prefill single-token requests in the tile launch hq={hq} hkv={hkv} d={d}")
+    rng = np.random.default_rng(hq * 100 + d)
+    n_req, mbpr = 24, 128
+    qlen = rng.choice([0, 1, 1, 1, 2, 33, 129], size=n_req).astype(np.int32)
+    prefix = rng.integers(0, 2048, n_req).astype(np.int32)
+    ctx = np.minimum(qlen + prefix, mbpr * 16).astype(np.int32)
+    ctx[1], qlen[1] = 2048, 1                      # a full-length single-token row
+    ctx[7] = np.maximum(qlen[7] - 1, 0)            # prefix < 0: rows left untouched
+    pool = n_req * mbpr
+    bt = rng.permutation(pool).astype(np.int32).reshape(n_req, mbpr)
+    bt[3, 5] = -1                                  # a hole
+    qsl = np.concatenate([[0], np.cumsum(qlen)]).astype(np.int32)
+    total = int(qsl[-1])
+    clip = total - 1 if qlen[-1] == 1 else total   # the last request's row past the end
+    g = torch.Generator(device=gpu)
+    g.manual_seed(hq + d)
+    q = W.randn_bf16((total, hq, d), g, gpu)
+    kc = W.randn_bf16((pool * 16, hkv, d), g, gpu)
+    vc = W.randn_bf16((pool * 16, hkv, d), g, gpu)
+    w = W.PagedWorkload("fused_dec", hq, hkv, d, ctx, bt, pool, q, kc, vc, query_start_loc=qsl)
+    m = w.device_meta(gpu)
+    outs = []
+    for side in (None, SideStream(gpu)):
+        o = torch.full_like(q, 7.0)
+        prefill_attention(q[:clip], kc, vc, m["block_table"], m["query_start_loc"],
+                          m["context_lens"], output=o[:clip], overlap=side)
+        torch.cuda.synchronize()
+        outs.append(o)
+    want = oracle_prefill(w, total=clip, out=np.full((clip, hq, d), 7.0, np.float32))
+    got = f32(outs[0])
+    assert_attn_close(got[:clip], want, f"fused decode items hq{hq}/hkv{hkv}/d{d}")
+    assert np.all(got[clip:] == 7.0)
     assert torch.equal(outs[0], outs[1])
