@@ -23,7 +23,7 @@
 //      Tiles entirely above the causal diagonal are skipped; masking only runs on the
 //      diagonal / ragged tiles.
 //   3. single-token requests run with prefill semantics (no 1e-6 in the denominator, bad
-//      rows left untouched). Batches of at most 512 (request, virtual kv head) groups with
+//      rows left untouched). Batches (bf16 or fp8) of at most 512 (request, virtual kv head) groups with
 //      table rows of at most 2048 positions run them in extra workgroups at the front of the
 //      tile launch (the decode kernels' group body, decode_core.hpp): no further launch.
 //      Others go through the split-KV decode kernels (decode_attn.hip): for batches of 32+
@@ -819,24 +819,28 @@ void prefill_pipe_kernel(const __bf16* __restrict__ q, const void* __restrict__ 
 
     // The first dec_wgs workgroups run the batch's single-token requests instead: one per
     // (request, virtual kv head), the decode kernels' group body with prefill semantics,
-    // its partial rows in the K/V buffers (two wavefronts' 16 x D floats per buffer).
-    if constexpr (!F8) {
-        if (static_cast<int>(blockIdx.x) < dec_wgs) {
-            static_assert(dcore::GroupShape<D>::kWaves == kPipeWaves &&
-                              kTileElems * 2 >= 2 * dcore::GroupShape<D>::kMaxG * D * 4,
-                          "the group body's partial rows fit two per K/V buffer");
-            auto part = [&](int w) {
-                __bf16* b = w < 2 ? lds_k0 : w < 4 ? lds_k1 : w < 6 ? lds_k2 : lds_v0;
-                return reinterpret_cast<float*>(b) + (w & 1) * dcore::GroupShape<D>::kMaxG * D;
-            };
-            float* lm = reinterpret_cast<float*>(lds_v1);
-            dcore::decode_group_body<D, false, kPad, true, 0>(
-                q, const_cast<void*>(k_cache_v), const_cast<void*>(v_cache_v), nullptr, nullptr,
-                block_table, context_lens, out, dec_items, mbpr, hq, dec_hkv, scale_log2, dr,
-                dec_rep, static_cast<int>(blockIdx.x), part, lm,
-                lm + kPipeWaves * dcore::GroupShape<D>::kMaxG);
-            return;
-        }
+    // its partial rows in four of the bf16 K/V buffers (two wavefronts' 16 x D floats per
+    // buffer) and its (m, l) pairs in a fifth buffer.
+    if (static_cast<int>(blockIdx.x) < dec_wgs) {
+        static_assert(dcore::GroupShape<D>::kWaves == kPipeWaves &&
+                          kTileElems * 2 >= 2 * dcore::GroupShape<D>::kMaxG * D * 4 &&
+                          (F8 ? kF8Bytes : kTileElems * 2) >= 2 * kPipeWaves * 16 * 4,
+                      "the group body's partial rows fit two per K/V buffer");
+        auto part = [&](int w) {
+            __bf16* b;
+            if constexpr (F8)
+                b = w < 2 ? lds_k0 : w < 4 ? lds_k1 : w < 6 ? lds_v0 : lds_v1;
+            else
+                b = w < 2 ? lds_k0 : w < 4 ? lds_k1 : w < 6 ? lds_k2 : lds_v0;
+            return reinterpret_cast<float*>(b) + (w & 1) * dcore::GroupShape<D>::kMaxG * D;
+        };
+        float* lm = F8 ? reinterpret_cast<float*>(lds_k8_0) : reinterpret_cast<float*>(lds_v1);
+        dcore::decode_group_body<D, F8, kPad, true, 0>(
+            q, const_cast<void*>(k_cache_v), const_cast<void*>(v_cache_v), k_scale, v_scale,
+            block_table, context_lens, out, dec_items, mbpr, hq, dec_hkv, scale_log2, dr,
+            dec_rep, static_cast<int>(blockIdx.x), part, lm,
+            lm + kPipeWaves * dcore::GroupShape<D>::kMaxG);
+        return;
     }
     const int bid = static_cast<int>(blockIdx.x) - dec_wgs;
     const int G = hq / hkv;
@@ -1705,7 +1709,7 @@ hipError_t prefill_impl(const void* q, const void* k_cache, const void* v_cache,
     const int Dk = decode_mfma_dim(head_dim);
     const int64_t dec_groups = static_cast<int64_t>(batch_size) * num_kv_heads *
                                dcore::decode_head_rep(num_q_heads / num_kv_heads);
-    const bool fused_dec = !F8 && pipe_head_dim(Dk) && dec_groups <= kFusedDecodeGroups &&
+    const bool fused_dec = pipe_head_dim(Dk) && dec_groups <= kFusedDecodeGroups &&
                            static_cast<int64_t>(max_blocks_per_req) * block_size <=
                                kFusedDecodeMaxCtx;
     const bool fork = !fused_dec && overlap != nullptr && overlap->side != nullptr &&

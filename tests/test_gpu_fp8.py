@@ -153,10 +153,16 @@ def test_prefill_fp8_equals_bf16_prefill_of_its_dequantised_cache(gpu, hq, hkv, 
     assert_attn_close(f32(out8), want, "fp8 prefill vs oracle")
 
 
-def test_prefill_fp8_mixed_batch_with_side_stream_decode_items(gpu):
+@pytest.mark.parametrize("dec_hi,prefix_hi", [(4096, 2048), (2000, 1024)])
+def test_prefill_fp8_mixed_batch_with_side_stream_decode_items(gpu, dec_hi, prefix_hi):
+    """Rows past 2048 positions: the decode items take the fp8 decode kernels on the side
+    stream; rows within 2048: they run inside the tile launch. Either way the oracle's
+    bar, the same bits with and without the side stream, and the fp8 decode operator's
+    result on the decode rows."""
     from ccinfer_amd import prefill_attention_fp8
-    say("fp8 prefill mixed batch")
-    w = W.mixed_step(device=gpu, n_chunks=2, chunk=128, n_decode=40, dec_hi=4096)
+    say(f"fp8 prefill mixed batch, decode rows up to {dec_hi}")
+    w = W.mixed_step(device=gpu, n_chunks=2, chunk=128, n_decode=40, dec_hi=dec_hi,
+                     dec_lo=min(1024, dec_hi), prefix_hi=prefix_hi)
     meta = w.device_meta(gpu)
     kc, vc, ks, vs = quantised_cache(gpu, w, w.hkv, w.d)
     from ccinfer_amd import SideStream
