@@ -1,4 +1,6 @@
-// Paged decode attention for gfx950: split-KV (flash-decoding) on bf16 MFMA tiles.
+// Paged decode attention for gfx950: split-KV (flash-decoding) on bf16 MFMA tiles. The
+// device building blocks (chunk loads, online softmax, the split loop, the group body) live
+// in decode_core.hpp, which the prefill launch includes too.
 //
 // Semantics follow the reference decode (src/kernel/attention/decode_attn.cu:364-473):
 //   out[b, hq, :] = softmax(q . K_ctx^T / sqrt(D)) . V_ctx  with kv_head = hq / (Hq/Hkv),
