@@ -152,7 +152,10 @@ __device__ __forceinline__ T kv_load(const T* p) {
 // still touches whole lines -- and the rest of the kernel is unchanged. (The choice is per
 // kernel: a branch per piece keeps both paths' registers live.) (Two
 // aligned 16-byte loads shifted into place, as the prefill staging does, hold twice the
-// registers per piece in flight: 48-1198 spilled VGPRs here, 7.6x instead of 1.7x.)
+// registers per piece in flight: 48-1198 spilled VGPRs here, 7.6x instead of 1.7x. The
+// whole dwords around a 2-byte-aligned piece, one more than the piece, shifted with
+// v_alignbyte: 8 spilled VGPRs at head dim 128 and 37 at 96 / 192, where the 2-byte loads,
+// which fill both halves of one register each, spill none.)
 template <bool kTL, int kU, typename T>
 __device__ __forceinline__ T kv_piece(const __bf16* p) {
     constexpr int kWords = std::is_same_v<T, u32x3> ? 3 : sizeof(T) / 4;
