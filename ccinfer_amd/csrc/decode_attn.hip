@@ -831,10 +831,11 @@ __device__ __forceinline__ void shared_prefix_work(
 // kPad: head_dim dr < D (see load_chunk); q and output rows hold dr elements.
 // kTL: the K/V loads stay in L2 (see kv_load).
 // kShared: workgroups from split_wgs on run shared_prefix_work (decode_attention_shared).
-// Wavefronts per SIMD: one at D = 256, three at D = 96 (168 VGPRs, no spills), else two.
+// Wavefronts per SIMD: one at D = 192 / 256, three at D = 96 (168 VGPRs, no spills), else
+// two.
 template <int D, bool F8, bool kPad, bool kTL, bool kShared = false,
           int KS = DecodeShape<D>::kSteps, int NBUF = 2, int kU = 0>
-__global__ __launch_bounds__(256, D == 256 ? 1 : D == 96 ? 3 : 2) void decode_split_kernel(
+__global__ __launch_bounds__(256, D >= 192 ? 1 : D == 96 ? 3 : 2) void decode_split_kernel(
     const __bf16* __restrict__ q, void* k_cache_v, void* v_cache_v,
     const float* __restrict__ k_scale,
     const float* __restrict__ v_scale, const int32_t* __restrict__ block_table,
@@ -958,6 +959,12 @@ __global__ __launch_bounds__(256, D == 256 ? 1 : D == 96 ? 3 : 2) void decode_sp
             for (int x = 0; x < 3; ++x)
                 *reinterpret_cast<f32x2*>(po + NV * (4 * g + r) + 2 * x) =
                     f32x2{st.acc[2 * x][r], st.acc[2 * x + 1][r]};
+        } else if constexpr (NV == 12) {
+#pragma unroll
+            for (int x = 0; x < 3; ++x)
+                *reinterpret_cast<f32x4*>(po + NV * (4 * g + r) + 4 * x) =
+                    f32x4{st.acc[4 * x][r], st.acc[4 * x + 1][r], st.acc[4 * x + 2][r],
+                          st.acc[4 * x + 3][r]};
         } else {
 #pragma unroll
             for (int n = 0; n < NV; ++n) po[NV * (4 * g + r) + n] = st.acc[n][r];
@@ -1284,12 +1291,12 @@ int decode_mfma_dim(int head_dim) {
     return head_dim <= 256 && head_dim % 16 == 0 ? 256 : 0;
 }
 
-// The decode kernels' head dim: the MFMA size above, except head dim 96, which has a tile
-// of its own (3 K steps, 6 V dims per lane): in the 128 tile a quarter of every V load's
-// lanes sit idle and the same registers hold 12 KB of K/V per chunk instead of 16, and the
-// loads in flight are what bounds this kernel.
+// The decode kernels' head dim: the MFMA size above, except head dims 96 and 192, which
+// have tiles of their own (3 / 6 K steps, 6 / 12 V dims per lane): in the padded tile a
+// quarter of every V load's lanes would sit idle. 64 x 4096 positions: d=96 152 -> 146 us,
+// d=192 175.5 -> 150.6 us.
 int decode_tile_dim(int head_dim) {
-    return head_dim == 96 ? 96 : decode_mfma_dim(head_dim);
+    return head_dim == 96 || head_dim == 192 ? head_dim : decode_mfma_dim(head_dim);
 }
 
 DecodePlan plan_decode_items(int num_items, int num_q_heads, int num_kv_heads, int head_dim,
@@ -1366,6 +1373,8 @@ hipError_t decode_attention(const void* q, const void* k_cache, const void* v_ca
             CCI_DECODE(64, false);
         case 96:
             CCI_DECODE(96, false);
+        case 192:
+            CCI_DECODE(192, false);
         case 128:
             if (pad) CCI_DECODE(128, true);
             CCI_DECODE(128, false);
@@ -1511,6 +1520,8 @@ hipError_t decode_attention_shared(const void* q, const void* k_cache, const voi
             CCI_SHARED(64, false);
         case 96:
             CCI_SHARED(96, false);
+        case 192:
+            CCI_SHARED(192, false);
         case 128:
             if (pad) CCI_SHARED(128, true);
             CCI_SHARED(128, false);

@@ -240,6 +240,13 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<D, KS>& c,
             const u32x3 w = kv_piece<kTL, kU, u32x3>(row);
 #pragma unroll
             for (int x = 0; x < 3; ++x) c.v[e][x] = w[x];
+        } else if constexpr (NV == 12) {  // D = 192: a 24-byte piece per lane
+            const u32x4 w0 = kv_piece<kTL, kU, u32x4>(row);
+            const u32x2 w1 = kv_piece<kTL, kU, u32x2>(row + 8);
+#pragma unroll
+            for (int x = 0; x < 4; ++x) c.v[e][x] = w0[x];
+            c.v[e][4] = w1[0];
+            c.v[e][5] = w1[1];
         } else if constexpr (NV == 4) {
             u32x2 w = u32x2{0, 0};
             if (!kMasked || vok) w = kv_piece<kTL, kU, u32x2>(row);

@@ -118,7 +118,7 @@ def test_head_shapes(gpu, hq, hkv, d):
 @pytest.mark.parametrize("hq,hkv,d,batch,ctx_hi", [
     (16, 8, 80, 1, 500),      # one workgroup per (request, kv_head), parts merged in LDS
     (8, 2, 32, 1, 400),
-    (8, 4, 192, 1, 300),
+    (8, 4, 192, 1, 300),      # head dim 192 tile
     (16, 8, 80, 2, 3000),     # fixed split plan + merge kernel
     (8, 2, 32, 3, 900),
     (8, 4, 192, 2, 2500),
@@ -131,8 +131,9 @@ def test_head_shapes(gpu, hq, hkv, d):
     (16, 4, 112, 64, 2000),
     (8, 8, 32, 48, 6000)])
 def test_padded_head_dims_every_plan(gpu, hq, hkv, d, batch, ctx_hi):
-    """Head dims below 64 / 128 / 256 run the MFMA kernels padded with zeros; every decode
-    plan (LDS-merged groups, balanced splits with the merge kernel) against the oracle."""
+    """Head dims below 64 / 128 / 256 run the MFMA kernels padded with zeros (96 and 192 in
+    tiles of their own); every decode plan (LDS-merged groups, balanced splits with the
+    merge kernel) against the oracle."""
     say(f"decode padded d={d} hq={hq} hkv={hkv} batch={batch} ctx<={ctx_hi}")
     w = W.decode_batched(device=gpu, seed=d * 7 + batch, batch=batch, ctx_lo=1, ctx_hi=ctx_hi,
                          hq=hq, hkv=hkv, d=d, with_write=False)
@@ -251,6 +252,7 @@ def test_two_byte_aligned_views(gpu, which):
     (2, 100, 3000, 16, 8, 256, 1),    # fixed split plan, head dim 256
     (300, 1, 400, 16, 8, 96, 5),      # indexed flat plan, head dim 96 tile
     (300, 1, 400, 16, 8, 80, 3),      # indexed flat plan, padded head dim
+    (40, 50, 900, 8, 4, 192, 5),      # head dim 192 tile
     (40, 50, 900, 64, 2, 64, 7),      # 32 query heads per kv head (virtual heads)
     (64, 128, 4096, 16, 8, 128, 2),   # 4-byte aligned: word loads
     (1, 512, 512, 16, 8, 96, 6),      # 4-byte aligned, group plan, head dim 96 tile

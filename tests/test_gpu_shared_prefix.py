@@ -40,6 +40,7 @@ def run(fn, w, dev):
     (24, 768, 10, 200, 4, 64, 8, 128),       # G = 8 (2 members per tile)
     (30, 256, 5, 90, 3, 16, 8, 96),          # head dim 96 tile
     (30, 256, 5, 90, 3, 16, 8, 80),          # padded head dim
+    (30, 256, 5, 90, 3, 8, 4, 192),          # head dim 192 tile
     (300, 512, 1, 400, 7, 16, 8, 128),       # past 256 requests: the indexed flat plan
     (3, 1024, 100, 300, 1, 16, 8, 128),      # 3 requests: the fixed split plan
 ])
