@@ -17,6 +17,7 @@ using f32x2 = float __attribute__((ext_vector_type(2)));
 using f32x4 = float __attribute__((ext_vector_type(4)));
 using f32x16 = float __attribute__((ext_vector_type(16)));
 using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
+using u32x1 = uint32_t __attribute__((ext_vector_type(1)));
 using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
 using u32x3 = uint32_t __attribute__((ext_vector_type(3)));
 // A 12-byte piece at 4-byte alignment: loads through this type claim only that alignment,

@@ -959,6 +959,8 @@ __global__ __launch_bounds__(256, D >= 192 ? 1 : D == 96 ? 3 : 2) void decode_sp
             for (int x = 0; x < 3; ++x)
                 *reinterpret_cast<f32x2*>(po + NV * (4 * g + r) + 2 * x) =
                     f32x2{st.acc[2 * x][r], st.acc[2 * x + 1][r]};
+        } else if constexpr (NV == 2) {
+            *reinterpret_cast<f32x2*>(po + NV * (4 * g + r)) = f32x2{st.acc[0][r], st.acc[1][r]};
         } else if constexpr (NV == 12) {
 #pragma unroll
             for (int x = 0; x < 3; ++x)
@@ -1291,12 +1293,13 @@ int decode_mfma_dim(int head_dim) {
     return head_dim <= 256 && head_dim % 16 == 0 ? 256 : 0;
 }
 
-// The decode kernels' head dim: the MFMA size above, except head dims 96 and 192, which
-// have tiles of their own (3 / 6 K steps, 6 / 12 V dims per lane): in the padded tile a
-// quarter of every V load's lanes would sit idle. 64 x 4096 positions: d=96 152 -> 146 us,
-// d=192 175.5 -> 150.6 us.
+// The decode kernels' head dim: the MFMA size above, except head dims 32, 96 and 192,
+// which have tiles of their own (1 / 3 / 6 K steps, 2 / 6 / 12 V dims per lane): in the
+// padded tile a quarter or half of every V load's lanes would sit idle. 64 x 4096
+// positions: d=32 58.1 -> 47.9 us, d=96 152 -> 146 us, d=192 175.5 -> 150.6 us.
 int decode_tile_dim(int head_dim) {
-    return head_dim == 96 || head_dim == 192 ? head_dim : decode_mfma_dim(head_dim);
+    return head_dim == 32 || head_dim == 96 || head_dim == 192 ? head_dim
+                                                               : decode_mfma_dim(head_dim);
 }
 
 DecodePlan plan_decode_items(int num_items, int num_q_heads, int num_kv_heads, int head_dim,
@@ -1371,6 +1374,8 @@ hipError_t decode_attention(const void* q, const void* k_cache, const void* v_ca
         case 64:
             if (pad) CCI_DECODE(64, true);
             CCI_DECODE(64, false);
+        case 32:
+            CCI_DECODE(32, false);
         case 96:
             CCI_DECODE(96, false);
         case 192:
@@ -1518,6 +1523,8 @@ hipError_t decode_attention_shared(const void* q, const void* k_cache, const voi
         case 64:
             if (pad) CCI_SHARED(64, true);
             CCI_SHARED(64, false);
+        case 32:
+            CCI_SHARED(32, false);
         case 96:
             CCI_SHARED(96, false);
         case 192:

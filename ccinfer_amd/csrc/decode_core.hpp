@@ -240,6 +240,8 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<D, KS>& c,
             const u32x3 w = kv_piece<kTL, kU, u32x3>(row);
 #pragma unroll
             for (int x = 0; x < 3; ++x) c.v[e][x] = w[x];
+        } else if constexpr (NV == 2) {  // D = 32: a 4-byte piece per lane
+            c.v[e][0] = kv_piece<kTL, kU, u32x1>(row)[0];
         } else if constexpr (NV == 12) {  // D = 192: a 24-byte piece per lane
             const u32x4 w0 = kv_piece<kTL, kU, u32x4>(row);
             const u32x2 w1 = kv_piece<kTL, kU, u32x2>(row + 8);

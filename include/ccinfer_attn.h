@@ -127,8 +127,8 @@ size_t ccinfer_decode_workspace_size(int batch_size, int max_blocks_per_req, int
  * [max_blocks_per_req] int32; context_lens: [batch_size] int32, including the current
  * token (whose K/V must already be written). cache_block_size must be 16 and head_dim one
  * of {32,64,80,96,112,120,128,192,256} (as in the reference); all of them run the MFMA
- * kernels (96 and 192 in tiles of their own; 32 padded to 64, 80 and 112-120 to 128,
- * with zeros), for any query group
+ * kernels (32, 96 and 192 in tiles of their own; 80 and 112-120 padded to 128 with
+ * zeros), for any query group
  * size (groups above 16 heads run as several groups of at most 16 over the same KV head).
  * Unlike the reference, there is no
  * context-length ceiling (split-KV). Batches of at most 16 (request, q-head) rows with

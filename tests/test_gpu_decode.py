@@ -131,8 +131,8 @@ def test_head_shapes(gpu, hq, hkv, d):
     (16, 4, 112, 64, 2000),
     (8, 8, 32, 48, 6000)])
 def test_padded_head_dims_every_plan(gpu, hq, hkv, d, batch, ctx_hi):
-    """Head dims below 64 / 128 / 256 run the MFMA kernels padded with zeros (96 and 192 in
-    tiles of their own); every decode plan (LDS-merged groups, balanced splits with the
+    """Head dims below 64 / 128 / 256 run the MFMA kernels padded with zeros (32, 96 and 192
+    in tiles of their own); every decode plan (LDS-merged groups, balanced splits with the
     merge kernel) against the oracle."""
     say(f"decode padded d={d} hq={hq} hkv={hkv} batch={batch} ctx<={ctx_hi}")
     w = W.decode_batched(device=gpu, seed=d * 7 + batch, batch=batch, ctx_lo=1, ctx_hi=ctx_hi,

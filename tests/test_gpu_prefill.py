@@ -532,11 +532,12 @@ def test_single_token_requests_inside_the_tile_launch(gpu, hq, hkv, d):
     assert torch.equal(outs[0], outs[1])
 
 
-@pytest.mark.parametrize("d", [160, 192, 224])
+@pytest.mark.parametrize("d", [48, 160, 192, 224])
 def test_single_token_requests_at_wide_head_dims(gpu, d):
-    """Head dims above 128 with single-token requests of up to 3000 positions: those run
-    the decode kernels (192 in its own tile, 160 / 224 padded to 256) beside the head-dim-256
-    tile kernel; every row against the oracle."""
+    """Head dims off the decode entry's list with single-token requests of up to 3000
+    positions (past the fused route's 2048): those run the decode kernels (192 in its own
+    tile, 160 / 224 padded to 256, 48 padded to 64) beside the tile kernel; every row
+    against the oracle."""
     say(f"prefill mixed batch d={d}")
     w = W.mixed_step(device=gpu, seed=d, n_chunks=2, chunk=64, prefix_hi=512, n_decode=12,
                      dec_lo=100, dec_hi=3000, hq=8, hkv=4, d=d)
