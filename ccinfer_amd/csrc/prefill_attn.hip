@@ -23,7 +23,7 @@
 //      Tiles entirely above the causal diagonal are skipped; masking only runs on the
 //      diagonal / ragged tiles.
 //   3. single-token requests run with prefill semantics (no 1e-6 in the denominator, bad
-//      rows left untouched). Batches (bf16 or fp8) of at most 512 (request, virtual kv head) groups with
+//      rows left untouched). Batches (bf16 or fp8) of at most 1024 (request, virtual kv head) groups with
 //      table rows of at most 2048 positions run them in extra workgroups at the front of the
 //      tile launch (the decode kernels' group body, decode_core.hpp): no further launch.
 //      Others go through the split-KV decode kernels (decode_attn.hip): for batches of 32+
@@ -1643,8 +1643,12 @@ constexpr int kOverlapMinRequests = 32;
 // prompts 45.5 -> 43.1, 64 x 128 prompts 61.4 -> 42.3; mixed batches of 128-1024 prompt
 // tokens with 4-60 single-token requests of 200-2000 positions 31.5 / 57.7 / 91.5 -> 27.5 /
 // 34.2 / 62.0 us. With rows of up to 4000 positions a batch of one 16-token prompt and 4
-// long single-token requests ran 35.6 -> 46.5 us, hence the 2048 bound.
-constexpr int64_t kFusedDecodeGroups = 512;
+// long single-token requests ran 35.6 -> 46.5 us, hence the 2048 bound. Group counts (same
+// box, bound 512 -> 1024 / 2048): 128 x 128 prompts 79.5 -> 74.4 us, 2 prompts + 126
+// single-token requests of 1500-2000 positions 253.5 -> 192.3 us; at ~2000 groups 4 prompts
+// + 250 requests of 200-2000 positions ran 181.3 -> 194.8 us (beyond ~1000 single-token
+// requests per launch the split plan streams them faster), hence 1024.
+constexpr int64_t kFusedDecodeGroups = 1024;
 constexpr int64_t kFusedDecodeMaxCtx = 2048;
 
 }  // namespace
